@@ -1,0 +1,305 @@
+"""Benchmark: FP8 input quantization + FP8 linear (exact bias) at 9216 x 4096 -> 16384.
+
+One step = fused_fp8_quantize_e4m3 on x (9216, 4096) bf16 followed by the FP8
+GEMM with the bias epilogue against W (16384, 4096) e4m3 — the patched
+FP8Linear.forward of the reference's FFN up-projection at the 576p shape.
+`value` is that step's throughput in TFLOP/s (2*M*N*K per step) with inputs
+resident in HBM. The JSON line also carries:
+  roofline      the FP8 GEMM kernel alone, timed with HIP events on its stream
+  fused_ops     every fused elementwise/norm op at its own shape: achieved
+                HBM GB/s (algorithmic bytes / kernel time) and fraction of peak
+  cpu_baseline  the numpy oracle of the same step on a bounded row sample,
+                on this host's cores
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-fused]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0
+
+M, K, N = 9216, 4096, 16384
+
+
+def _parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-fused", action="store_true")
+    ap.add_argument("--seed", type=int, default=20260100)
+    return ap.parse_args()
+
+
+def _gen(seed, device):
+    import torch
+
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    return g
+
+
+def make_fp8_linear_inputs(seed: int, device: str, m: int = M, k: int = K, n: int = N):
+    """x ~ N(0,1) bf16 with 0.1% of entries x50; W from N(0,0.02) quantized
+    per tensor to e4m3; bias ~ N(0,0.01) bf16; input scale amax(x)/448 (0-dim)."""
+    import torch
+
+    g = _gen(seed, device)
+    x = torch.randn((m, k), generator=g, device=device, dtype=torch.float32)
+    idx = torch.randperm(m * k, generator=g, device=device)[: (m * k) // 1000]
+    x.view(-1)[idx] *= 50.0
+    x = x.to(torch.bfloat16)
+    s_in = (x.float().abs().amax() / 448.0).reshape(())
+    wf = torch.randn((n, k), generator=g, device=device, dtype=torch.float32) * 0.02
+    s_w = (wf.abs().amax() / 448.0).reshape(())
+    w = torch.clamp(wf / s_w, -448, 448).to(torch.float8_e4m3fn)
+    del wf
+    bias = (torch.randn((n,), generator=g, device=device, dtype=torch.float32) * 0.01).to(torch.bfloat16)
+    return x, s_in, w, s_w, bias
+
+
+def _graph_time_us(fn, reps: int = 20, inner: int = 25) -> float:
+    """Mean per-call GPU time of fn: `inner` calls captured in one HIP graph,
+    the graph replayed `reps` times between two events on the capture stream."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(inner):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(reps):
+        graph.replay()
+    e1.record(st)
+    e1.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / (reps * inner)
+    del graph
+    return us
+
+
+def fused_op_rows(seed: int) -> dict:
+    """Each fused op at its configured shape: achieved GB/s from algorithmic
+    bytes per call over the mean kernel time (HIP graph of back-to-back calls)."""
+    import torch
+
+    from opengenie_amd import ltx_ops as L
+
+    dev = "cuda"
+    rows = {}
+
+    def rec(name, nbytes, us, shape):
+        gbs = nbytes / (us * 1e-6) / 1e9
+        rows[name] = {"shape": shape, "bytes": int(nbytes), "us": round(us, 3), "GB/s": round(gbs, 1),
+                      "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+    g = _gen(seed + 1, dev)
+    # AdaZero from the table, (1, 2304, 4096), one timestep row for all tokens.
+    C = 4096
+    x = torch.randn((1, 2304, C), generator=g, device=dev).to(torch.bfloat16)
+    table = (torch.randn((6, C), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    ts = (torch.randn((1, 1, 6 * C), generator=g, device=dev) * 0.5).to(torch.bfloat16).expand(1, 2304, 6 * C)
+    us = _graph_time_us(lambda: L.fused_adazero_from_ada(x, 1e-6, table, ts, shift_index=0, scale_index=1))
+    rec("adazero_from_ada", 2 * 2304 * C * 2 + 2 * C * 2 * 2, us, "x(1,2304,4096) ts broadcast")
+    del x, table, ts
+
+    # FP8 input quantizer at 9216 x 4096.
+    xq = torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
+    sq = torch.tensor(0.05, device=dev)
+    us = _graph_time_us(lambda: L.fused_fp8_quantize_e4m3(xq, sq))
+    rec("fp8_quantize_e4m3", M * K * 3, us, "x(9216,4096)")
+
+    # Q/K RMSNorm + split RoPE at N = 9216.
+    q = torch.randn((1, M, 4096), generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn((1, M, 4096), generator=g, device=dev).to(torch.bfloat16)
+    qw = (1 + 0.05 * torch.randn((4096,), generator=g, device=dev)).to(torch.bfloat16)
+    kw = (1 + 0.05 * torch.randn((4096,), generator=g, device=dev)).to(torch.bfloat16)
+    from opengenie_amd.rope import video_rope_cos_sin
+
+    cos, sin = video_rope_cos_sin((16, 18, 32), heads=32, head_dim=128, device=dev)
+    us = _graph_time_us(lambda: L.fused_video_qk_rmsnorm_rope(q, k, qw, kw, 1e-6, cos, sin))
+    rec("video_qk_rmsnorm_rope", M * 4096 * 2 * 4 + 2 * 32 * M * 64 * 2 + 2 * 4096 * 2, us, "q,k(1,9216,4096)")
+
+    # Per-head FP8 quantizer on one (1, 9216, 32, 128) tensor.
+    us = _graph_time_us(lambda: L.fused_fp8_quantize_e4m3_per_head_4d(q.view(1, M, 32, 128)), inner=10)
+    rec("fp8_quantize_per_head", M * 4096 * (2 + 2 + 1), us, "x(1,9216,32,128)")
+    del q, k, xq, cos, sin
+
+    # Continuation block ops at N = 14080 with per-token timesteps (9 rows).
+    Nc = 14080
+    xc = torch.randn((1, Nc, C), generator=g, device=dev).to(torch.bfloat16)
+    yc = torch.randn((1, Nc, C), generator=g, device=dev).to(torch.bfloat16)
+    tab9 = (torch.randn((9, C), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    tsc = synthetic_timestep_embeddings(Nc, 9 * C, prefix_tokens=2640, seed=seed + 2, device=dev)
+    bias = (torch.randn((C,), generator=g, device=dev) * 0.01).to(torch.bfloat16)
+    per_tok = Nc * C * 2
+    us = _graph_time_us(lambda: L.fused_adaln_affine_from_ada(xc, tab9, tsc, shift_index=6, scale_index=7), inner=10)
+    rec("adaln_affine_from_ada", 4 * per_tok + 2 * C * 2, us, "x(1,14080,4096) per-token ts")
+    us = _graph_time_us(lambda: L.fused_residual_gate_bias_from_ada(xc, yc, bias, tab9, tsc, gate_index=2), inner=10)
+    rec("residual_gate_bias_from_ada", 4 * per_tok + 2 * C * 2, us, "x,y(1,14080,4096) per-token ts")
+    us = _graph_time_us(lambda: L.fused_residual_gate_from_ada(xc, yc, tab9, tsc, gate_index=8), inner=10)
+    rec("residual_gate_from_ada", 4 * per_tok + C * 2, us, "x,y(1,14080,4096) per-token ts")
+    del xc, yc, tsc
+    torch.cuda.empty_cache()
+    return rows
+
+
+def synthetic_timestep_embeddings(tokens: int, width: int, prefix_tokens: int, seed: int, device: str):
+    """Per-token Ada timestep embeddings for a continuation window: the first
+    `prefix_tokens` tokens (the clean conditioning frames) share the t = 0
+    embedding; every other token gets e(t) = a + t*b with its own t ~ U(0,1)
+    and fixed a, b ~ N(0, 0.5). Shape (1, tokens, width) bf16."""
+    import torch
+
+    g = _gen(seed, device)
+    a = torch.randn((width,), generator=g, device=device) * 0.5
+    b = torch.randn((width,), generator=g, device=device) * 0.5
+    t = torch.rand((tokens, 1), generator=g, device=device)
+    t[:prefix_tokens] = 0.0
+    return (a + t * b).to(torch.bfloat16).unsqueeze(0)
+
+
+def cpu_baseline(x, s_in, w, s_w, bias, target_s: float = 12.0) -> dict:
+    """The numpy oracle of one step (quantize + FP8 GEMM + bias) on a row
+    sample of x, on this host's cores; scaled to TFLOP/s of the sample."""
+    import numpy as np
+    import torch
+
+    from oracle import ltx_ops as O
+    from oracle.numerics import T
+
+    cores = len(os.sched_getaffinity(0))
+    try:
+        from threadpoolctl import threadpool_limits
+
+        threadpool_limits(cores)
+    except Exception:
+        pass
+    wc = w.view(torch.uint8).cpu().numpy()
+    bias_t = T(bias.float().cpu().numpy(), "bf16")
+    sa, sb = float(s_in), float(s_w)
+
+    def run(rows: int) -> float:
+        xs = T(x[:rows].float().cpu().numpy(), "bf16")
+        t0 = time.perf_counter()
+        q = O.fp8_quantize_e4m3(xs, sa, True, device="cuda")
+        O.fp8_linear(q, wc, sa, sb, bias_t)
+        return time.perf_counter() - t0
+
+    rows = 32
+    t = run(rows)
+    rows = int(max(32, min(M, rows * max(1.0, (target_s / 2) / max(t, 1e-3)))))
+    rows -= rows % 32
+    times = [run(rows) for _ in range(2)]
+    best = min(times)
+    flops = 2.0 * rows * N * K
+    return {"value": round(flops / best / 1e12, 5), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"numpy oracle (float64 GEMM of decoded e4m3, exact bf16/e4m3 rounding) of quantize + "
+                      f"FP8 linear + bias on {rows} of the {M} rows x {K} -> {N}; best of 2; {best:.2f} s"}
+
+
+def main() -> None:
+    args = _parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the fused ops and the FP8 linear shard by token rows with no "
+              f"exchange, so a {args.gpus}-GPU figure adds nothing one GPU cannot show; run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from opengenie_amd import ltx_ops as L
+    from opengenie_amd import _lib
+
+    _lib.load()
+    dev = "cuda"
+    x, s_in, w, s_w, bias = make_fp8_linear_inputs(args.seed, dev)
+
+    def step():
+        q = L.fused_fp8_quantize_e4m3(x, s_in)
+        return L.fp8_scaled_mm(q, w, s_in, s_w, bias)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    flops = 2.0 * M * N * K
+    value = flops / dt / 1e12
+
+    # Dominant kernel alone: the FP8 GEMM, HIP events on its own stream.
+    q = L.fused_fp8_quantize_e4m3(x, s_in)
+    out = torch.empty((M, N), device=dev, dtype=torch.bfloat16)
+    st = torch.cuda.current_stream()
+    lib = _lib.load()
+    args_c = (q.data_ptr(), K, w.data_ptr(), K, s_in.data_ptr(), s_w.data_ptr(), bias.data_ptr(), _lib.DT_BF16,
+              out.data_ptr(), N, M, N, K, st.cuda_stream)
+    reps = max(10, args.steps)
+    for _ in range(3):
+        lib.oga_fp8_linear(*args_c)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(reps):
+        rc = lib.oga_fp8_linear(*args_c)
+    e1.record(st)
+    e1.synchronize()
+    assert rc == 0
+    gemm_us = e0.elapsed_time(e1) * 1000.0 / reps
+    achieved = flops / (gemm_us * 1e-6) / 1e12
+
+    fused = {} if args.no_fused else fused_op_rows(args.seed)
+    cpu = None if args.no_cpu else cpu_baseline(x, s_in, w, s_w, bias)
+
+    line = {
+        "metric": "fused-op HBM GB/s (% of peak) + FP8 linear TFLOPS at 9216 tok x 4096 bf16",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3 (fp32 accumulate, bf16 out)",
+        "data": "synthetic",
+        "config": {"workload": "FP8 input quant + FP8Linear (exact bf16 bias) 576p FFN up-proj",
+                   "m_tokens": M, "k_in": K, "n_out": N, "input_scale": "amax/448 0-dim",
+                   "outliers": "0.1% x50"},
+        "roofline": {"bound": "mfma", "kernel": "k_fp8_gemm", "achieved": round(achieved, 1),
+                     "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
+                     "traffic": None, "us_per_launch": round(gemm_us, 2)},
+        "fused_ops": fused,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,195 @@
+/*
+ * opengenie_amd — C ABI of the MI355X (gfx950) fused LTX-2.3 DiT block ops.
+ *
+ * One stateless entry point per fused op of plugyawn/opengenie
+ * `ltx_serve/triton_ltx_ops.py` (cited per function as file:line of that
+ * reference file). Conventions:
+ *   - all pointers are device pointers the caller allocated; nothing here
+ *     allocates, frees or synchronises;
+ *   - strides are in elements; dtype arguments take the OGA_DT_* codes;
+ *   - `stream` is a hipStream_t (NULL = the default stream); kernels are
+ *     enqueued on it and the call returns without waiting;
+ *   - the return value is 0 on success, a negative OGA_E* code for a bad
+ *     argument (oga_last_error() then describes it), or a positive
+ *     hipError_t from the launch.
+ * Rounding: every op computes in float32 and rounds to bf16 (nearest even)
+ * exactly where torch evaluating the reference's torch expression would hold
+ * a bf16 result; an intermediate whose torch dtype is float32 is not rounded.
+ */
+#ifndef OPENGENIE_AMD_H
+#define OPENGENIE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { OGA_DT_BF16 = 0, OGA_DT_F32 = 1 };
+enum { OGA_OK = 0, OGA_EINVAL = -1, OGA_EUNSUPPORTED = -2 };
+
+/* Library identification and the last argument-error message (per thread). */
+int oga_abi_version(void);
+const char* oga_last_error(void);
+
+/*
+ * AdaZero from the Ada table: `fused_adazero_from_ada`
+ * (triton_ltx_ops.py:40-91; Ada values :983-998; guard :1001-1018).
+ * x, y: (batch*tokens, cols) bf16 contiguous, cols in {2048, 4096}.
+ * table (P, cols): element (i, c) at table[i*tab_s0 + c*tab_s1].
+ * timestep viewed (batch, tokens, P, cols) with strides ts_strides[4]
+ * (a zero token stride is allowed: one timestep row shared by all tokens).
+ * y = R(R?(R(rms_norm(x)) * R?(1 + scale)) + shift), with
+ * shift/scale = R?(R?(table[i]) + ts[b, t, i]) as in the torch path.
+ */
+int oga_adazero_from_ada(const void* x, void* y, int64_t batch, int64_t tokens, int64_t cols,
+                         const void* table, int table_dtype, int64_t tab_s0, int64_t tab_s1,
+                         const void* timestep, int ts_dtype, const int64_t ts_strides[4],
+                         int shift_index, int scale_index, float eps, void* stream);
+
+/*
+ * AdaZero with materialised scale/shift: `fused_adazero`
+ * (triton_ltx_ops.py:8-37; guard :1626-1637).
+ * x, y viewed (batch, tokens, cols); scale/shift are that shape after torch
+ * broadcasting, given by strides (b, t, c) (zero for a broadcast axis).
+ */
+int oga_adazero(const void* x, void* y, int64_t batch, int64_t tokens, int64_t cols,
+                const void* scale, int scale_dtype, const int64_t scale_strides[3],
+                const void* shift, int shift_dtype, const int64_t shift_strides[3],
+                float eps, void* stream);
+
+/* `fused_adaln_affine_from_ada` (triton_ltx_ops.py:94-141):
+ * y = R(R?(x * R?(1 + scale)) + shift). Same table/timestep convention. */
+int oga_adaln_affine_from_ada(const void* x, void* y, int64_t batch, int64_t tokens, int64_t cols,
+                              const void* table, int table_dtype, int64_t tab_s0, int64_t tab_s1,
+                              const void* timestep, int ts_dtype, const int64_t ts_strides[4],
+                              int shift_index, int scale_index, void* stream);
+
+/* `fused_mul_from_ada` (triton_ltx_ops.py:695-739): y = R(x * gate). */
+int oga_mul_from_ada(const void* x, void* y, int64_t batch, int64_t tokens, int64_t cols,
+                     const void* table, int table_dtype, int64_t tab_s0, int64_t tab_s1,
+                     const void* timestep, int ts_dtype, const int64_t ts_strides[4],
+                     int gate_index, void* stream);
+
+/* `fused_residual_gate_from_ada` (triton_ltx_ops.py:640-692) in the
+ * production residual mode: out = R(x + R?(y * gate)). */
+int oga_residual_gate_from_ada(const void* x, const void* y, void* out, int64_t batch, int64_t tokens,
+                               int64_t cols, const void* table, int table_dtype, int64_t tab_s0,
+                               int64_t tab_s1, const void* timestep, int ts_dtype,
+                               const int64_t ts_strides[4], int gate_index, void* stream);
+
+/* `fused_residual_gate_bias_from_ada` (triton_ltx_ops.py:204-262):
+ * out = R(x + R?(R(y + R(bias)) * gate)). bias is (cols,) bf16 or f32. */
+int oga_residual_gate_bias_from_ada(const void* x, const void* y, const void* bias, int bias_dtype,
+                                    void* out, int64_t batch, int64_t tokens, int64_t cols,
+                                    const void* table, int table_dtype, int64_t tab_s0, int64_t tab_s1,
+                                    const void* timestep, int ts_dtype, const int64_t ts_strides[4],
+                                    int gate_index, void* stream);
+
+/* `fused_residual_gate_bf16` (triton_ltx_ops.py:590-611):
+ * out = R(x + R(y * gate)), gate bf16 broadcast to (batch, tokens, cols)
+ * through strides (b, t, c). */
+int oga_residual_gate_bf16(const void* x, const void* y, const void* gate, const int64_t gate_strides[3],
+                           void* out, int64_t batch, int64_t tokens, int64_t cols, void* stream);
+
+/* `fused_bias_add_bf16` (triton_ltx_ops.py:185-201): out = R(x + R(bias)),
+ * x (rows, cols) bf16 contiguous, bias (cols,) bf16 or f32. */
+int oga_bias_add_bf16(const void* x, const void* bias, int bias_dtype, void* out, int64_t rows,
+                      int64_t cols, void* stream);
+
+/* `fused_head_gate_mul_bf16` (triton_ltx_ops.py:614-637):
+ * out[r, h*dim_head + d] = R(x[r, ...] * gates[r*g_s0 + h*g_s1]), bf16. */
+int oga_head_gate_mul_bf16(const void* x, const void* gates, int64_t g_s0, int64_t g_s1, void* out,
+                           int64_t rows, int64_t heads, int64_t dim_head, void* stream);
+
+/*
+ * `fused_fp8_quantize_e4m3` (triton_ltx_ops.py:144-161; torch path :146-148):
+ * q = e4m3fn(clamp(x * (1/scale), -448, 448)) for n contiguous bf16 inputs.
+ * scale is a device float32 with one element. scale_is_0dim selects torch's
+ * dtype rule for a 0-dim scale tensor (both operands taken to bf16 before the
+ * multiply, the product rounded to bf16) versus a (1,)-shaped one (float32
+ * product). q holds n e4m3fn codes.
+ */
+int oga_fp8_quantize_e4m3(const void* x, const float* scale, int scale_is_0dim, void* q, int64_t n,
+                          void* stream);
+
+/* `fused_gelu_tanh_fp8_quantize_e4m3` (triton_ltx_ops.py:164-182): the
+ * quantizer above applied to R(gelu_tanh(x)). */
+int oga_gelu_tanh_fp8_quantize_e4m3(const void* x, const float* scale, int scale_is_0dim, void* q,
+                                    int64_t n, void* stream);
+
+/*
+ * `fused_fp8_quantize_e4m3_per_head_4d` (triton_ltx_ops.py:265-317; torch
+ * path :976-980). x [B, N, H, D] bf16 contiguous, D in {64, 128}, H*D a
+ * multiple of 512. scale_out [B, H] float32 = max(amax|x|, 1e-12) / 448;
+ * q [B, N, H, D] e4m3fn = e4m3(clamp(x / scale, +-448)). `workspace` holds
+ * oga_fp8_per_head_workspace_bytes(...) bytes of caller-owned device memory.
+ */
+int64_t oga_fp8_per_head_workspace_bytes(int64_t batch, int64_t tokens, int64_t heads, int64_t head_dim);
+int oga_fp8_quantize_per_head(const void* x, void* q, float* scale_out, void* workspace, int64_t batch,
+                              int64_t tokens, int64_t heads, int64_t head_dim, void* stream);
+
+/*
+ * `fused_video_qk_rmsnorm_rope` (triton_ltx_ops.py:320-378; torch path
+ * :958-973; guard :1502-1537). q, k, q_out, k_out: (batch*tokens, heads*128)
+ * bf16 contiguous with heads*128 == cols in {2048, 4096}; weights (cols,)
+ * bf16 or f32; cos/sin [batch or 1, heads, tokens, 64] with strides
+ * cos_strides/sin_strides (last stride 1), bf16 or f32 (same dtype).
+ * o = split-RoPE(R(x * inv * w)) with each torch op rounded per dtype.
+ */
+int oga_video_qk_rmsnorm_rope(const void* q, const void* k, const void* q_weight, const void* k_weight,
+                              int weight_dtype, const void* cos, const void* sin, int cs_dtype,
+                              const int64_t cos_strides[4], const int64_t sin_strides[4], void* q_out,
+                              void* k_out, int64_t batch, int64_t tokens, int64_t cols, int64_t heads,
+                              float eps, void* stream);
+
+/* One-tensor form used by `fused_video_qk_rmsnorm_rope_separate`
+ * (triton_ltx_ops.py:432-505), which launches it once for q and once for k. */
+int oga_video_rmsnorm_rope(const void* x, const void* weight, int weight_dtype, const void* cos,
+                           const void* sin, int cs_dtype, const int64_t cos_strides[4],
+                           const int64_t sin_strides[4], void* out, int64_t batch, int64_t tokens,
+                           int64_t cols, int64_t heads, float eps, void* stream);
+
+/* `fused_video_qk_bias_rmsnorm_rope` (triton_ltx_ops.py:508-587): q and k
+ * first become R(q + R(q_bias)), R(k + R(k_bias)). */
+int oga_video_qk_bias_rmsnorm_rope(const void* q, const void* k, const void* q_bias, const void* k_bias,
+                                   int bias_dtype, const void* q_weight, const void* k_weight,
+                                   int weight_dtype, const void* cos, const void* sin, int cs_dtype,
+                                   const int64_t cos_strides[4], const int64_t sin_strides[4],
+                                   void* q_out, void* k_out, int64_t batch, int64_t tokens, int64_t cols,
+                                   int64_t heads, float eps, void* stream);
+
+/* `fused_video_qkv_rmsnorm_rope_pack` (triton_ltx_ops.py:381-429): writes
+ * qkv [batch, tokens, 3, heads, 128] = (rope(q), rope(k), v). */
+int oga_video_qkv_rmsnorm_rope_pack(const void* q, const void* k, const void* v, const void* q_weight,
+                                    const void* k_weight, int weight_dtype, const void* cos,
+                                    const void* sin, int cs_dtype, const int64_t cos_strides[4],
+                                    const int64_t sin_strides[4], void* qkv_out, int64_t batch,
+                                    int64_t tokens, int64_t cols, int64_t heads, float eps, void* stream);
+
+/*
+ * FP8 linear: the patched `FP8Linear.forward` (triton_ltx_ops.py:1671-1718),
+ * `fp8_linear_from_quantized_e4m3` (:742-759) and `fp8_linear_without_bias`
+ * (:762-781). a [M, K] and w [N, K] are e4m3fn codes with row strides lda,
+ * ldw (K-contiguous); scale_a, scale_b device float32 scalars.
+ * out [M, N] bf16 (row stride ldo) = R(acc * (scale_a*scale_b)), then, if
+ * bias (N,) is given, R(out + R(bias)) — the two roundings of `_scaled_mm`
+ * followed by the separate bias add. K must be a multiple of 128.
+ */
+int oga_fp8_linear(const void* a, int64_t lda, const void* w, int64_t ldw, const float* scale_a,
+                   const float* scale_b, const void* bias, int bias_dtype, void* out, int64_t ldo,
+                   int64_t m, int64_t n, int64_t k, void* stream);
+
+/*
+ * Conversion self-test: runs the device rounding primitives every kernel
+ * uses on n float32 inputs: bf16_out[i] = bf16 bits of R(in[i]) and
+ * e4m3_out[i] = e4m3fn(clamp(in[i], +-448)). No reference counterpart; it
+ * lets a test pin the hardware conversions against the oracle bit by bit.
+ */
+int oga_selftest_convert(const float* in, uint16_t* bf16_out, uint8_t* e4m3_out, int64_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OPENGENIE_AMD_H */

@@ -1,0 +1,279 @@
+"""numpy restatement of the reference's torch path for each fused op.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py). Each function restates
+the torch expression that plugyawn/opengenie evaluates for the op, at the
+precision torch uses: every elementwise op is computed in float32 and rounded
+to bfloat16 wherever torch's result dtype is bfloat16 (`numerics.T` tracks
+that dtype). Citations are to `ltx_serve/triton_ltx_ops.py` unless stated.
+
+Arrays: bf16 tensors are float32 arrays holding bf16 values. Functions take
+`numerics.T` values (value + dtype tag) where the reference accepts more than
+one dtype, and plain arrays where it accepts only bf16.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from .numerics import (
+    E4M3_MAX,
+    T,
+    add,
+    add_scalar,
+    bf16_round,
+    clamp,
+    e4m3_decode,
+    e4m3_encode,
+    f32,
+    mul,
+    sub,
+)
+
+
+def bf(v) -> T:
+    return T(v, "bf16")
+
+
+# --------------------------------------------------------------------------
+# Ada values from the scale/shift table
+# --------------------------------------------------------------------------
+def ada_values_from_table(table: T, timestep: T, batch: int, tokens: int, cols: int, *indices: int):
+    """`_torch_ada_values_from_table` (:983-998).
+
+    timestep is (B, Nt, P*C) with Nt == tokens or Nt == 1 (a broadcast view in
+    torch; the values are identical). Returns one T of shape (B, tokens, C) per
+    index: `table.to(ts.dtype)[i] + ts_view[:, :, i, :]` (:997-998).
+    """
+    params = table.v.shape[0]
+    ts = timestep.v.reshape(batch, timestep.v.shape[1], params, cols)
+    ts = np.broadcast_to(ts, (batch, tokens, params, cols))
+    tab = table.to(timestep.dt)
+    out = []
+    for i in indices:
+        out.append(add(T(tab.v[i].reshape(1, 1, cols), tab.dt), T(ts[:, :, i, :], timestep.dt)))
+    return tuple(out)
+
+
+# --------------------------------------------------------------------------
+# RMSNorm
+# --------------------------------------------------------------------------
+def rms_norm(x: T, eps: float, weight: T | None = None) -> T:
+    """torch.nn.functional.rms_norm(x, (C,), weight, eps) for bf16 x.
+
+    inv = 1 / sqrt(mean(x^2) + eps) in float32 with the mean taken from the
+    exact sum of squares (squares of bf16 values are exact in float32; the sum
+    is accumulated in float64, whose rounding error is far below float32's);
+    y = x * inv [* w] in float32, rounded once to x's dtype. The single
+    rounding with a weight was probed on torch 2.10 CPU.
+    """
+    xv = x.v.astype(np.float64)
+    ss = np.sum(xv * xv, axis=-1, keepdims=True)
+    cols = x.v.shape[-1]
+    mean = (ss / cols).astype(np.float32)
+    inv = np.float32(1.0) / np.sqrt(mean + np.float32(eps))
+    y = x.v * inv
+    if weight is not None:
+        y = y * weight.v
+    return T(bf16_round(y) if x.dt == "bf16" else f32(y), x.dt)
+
+
+# --------------------------------------------------------------------------
+# AdaZero family
+# --------------------------------------------------------------------------
+def adazero(x: T, eps: float, scale: T, shift: T) -> T:
+    """`fused_adazero` torch path (:9-10): rms_norm(x) * (1 + scale) + shift."""
+    n = rms_norm(x, eps)
+    return add(mul(n, add_scalar(scale, 1.0)), shift)
+
+
+def adazero_from_ada(x: T, eps: float, table: T, timestep: T, shift_index: int, scale_index: int) -> T:
+    """`fused_adazero_from_ada` torch path (:50-60)."""
+    b, n, c = x.v.shape
+    shift, scale = ada_values_from_table(table, timestep, b, n, c, shift_index, scale_index)
+    return adazero(x, eps, scale, shift)
+
+
+def adaln_affine_from_ada(x: T, table: T, timestep: T, shift_index: int, scale_index: int) -> T:
+    """`fused_adaln_affine_from_ada` torch path (:102-112): x * (1 + scale) + shift."""
+    b, n, c = x.v.shape
+    shift, scale = ada_values_from_table(table, timestep, b, n, c, shift_index, scale_index)
+    return add(mul(x, add_scalar(scale, 1.0)), shift)
+
+
+def mul_from_ada(x: T, table: T, timestep: T, gate_index: int) -> T:
+    """`fused_mul_from_ada` torch path (:702-711): x * gate."""
+    b, n, c = x.v.shape
+    (gate,) = ada_values_from_table(table, timestep, b, n, c, gate_index)
+    return mul(x, gate)
+
+
+# --------------------------------------------------------------------------
+# Residual gates
+# --------------------------------------------------------------------------
+def residual_gate(x: T, y: T, gate: T) -> T:
+    """`x + y * gate` (:591-592); also `_simple_residual_gate` in the production
+    residual mode "triton_simple_bf16_round" (:1955-1960, :1977-1981)."""
+    return add(x, mul(y, gate))
+
+
+def residual_gate_from_ada(x: T, y: T, table: T, timestep: T, gate_index: int) -> T:
+    """`fused_residual_gate_from_ada` torch path (:650-659)."""
+    b, n, c = x.v.shape
+    (gate,) = ada_values_from_table(table, timestep, b, n, c, gate_index)
+    return residual_gate(x, y, gate)
+
+
+def bias_add(x: T, bias: T) -> T:
+    """`fused_bias_add_bf16` torch path (:186-187): x + bias.to(x.dtype)."""
+    return add(x, bias.to(x.dt))
+
+
+def residual_gate_bias_from_ada(x: T, y_no_bias: T, bias: T, table: T, timestep: T, gate_index: int) -> T:
+    """`fused_residual_gate_bias_from_ada` torch path (:214-228)."""
+    y = bias_add(y_no_bias, bias)
+    return residual_gate_from_ada(x, y, table, timestep, gate_index)
+
+
+def head_gate_mul(out: T, gates: T, heads: int, dim_head: int) -> T:
+    """`fused_head_gate_mul_bf16` torch path (:615-619)."""
+    b, n, _ = out.v.shape
+    o = T(out.v.reshape(b, n, heads, dim_head), out.dt)
+    g = T(gates.v.reshape(b, n, heads, 1), gates.dt)
+    r = mul(o, g)
+    return T(r.v.reshape(b, n, heads * dim_head), r.dt)
+
+
+# --------------------------------------------------------------------------
+# FP8 quantizers
+# --------------------------------------------------------------------------
+def fp8_quantize_e4m3(x: T, input_scale: float, scale_is_0dim: bool, device: str = "cuda") -> np.ndarray:
+    """`fused_fp8_quantize_e4m3` torch path (:146-148) -> uint8 e4m3fn codes.
+
+    clamp(x * input_scale.reciprocal(), -448, 448).to(float8_e4m3fn), with
+    r = float32(1 / s). Dtype of `x * r`: a 0-dim scale does not promote, so
+    the product is bf16 (rounded); a (1,)-shaped scale makes it float32.
+    On a GPU the 0-dim float32 operand is itself converted to the common
+    dtype (bf16) before the multiply (TensorIterator casts non-CPU-scalar
+    inputs to the common dtype); a 0-dim CPU tensor is read at full float32
+    precision. `device` selects which of the two the restatement follows.
+    """
+    r = np.float32(1.0) / np.float32(input_scale)
+    if scale_is_0dim:
+        rv = bf16_round(r) if device == "cuda" else f32(r)
+        y = T(bf16_round(x.v * rv), x.dt) if x.dt == "bf16" else T(x.v * rv, x.dt)
+    else:
+        y = T(x.v * r, "f32")
+    y = clamp(y, -E4M3_MAX, E4M3_MAX)
+    return e4m3_encode(y.v)
+
+
+def gelu_tanh(x: T) -> T:
+    """torch.nn.functional.gelu(x, approximate='tanh') for bf16 x: computed in
+    float32 as 0.5*x*(1+tanh(sqrt(2/pi)*(x+0.044715*x^3))), rounded once.
+    (float64 tanh here; parity unpinned at the last float32 bit.)"""
+    v = x.v.astype(np.float64)
+    g = 0.5 * v * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (v + 0.044715 * v * v * v)))
+    g = g.astype(np.float32)
+    return T(bf16_round(g) if x.dt == "bf16" else g, x.dt)
+
+
+def fp8_per_head_quantize(x: np.ndarray):
+    """`_torch_fp8_quantize_e4m3_per_head_4d` (:976-980) for x [B, N, H, D].
+
+    scale[b, h] = max(amax_{N,D} |x|, 1e-12) / 448 (float32 division);
+    q = e4m3(clamp(x / scale, -448, 448)) with a float32 division.
+    Returns (codes uint8 [B,N,H,D], scale float32 [B,H]).
+    """
+    xv = f32(x)
+    amax = np.abs(xv).max(axis=(1, 3)).astype(np.float32)
+    scale = np.maximum(amax, np.float32(1e-12)) / np.float32(E4M3_MAX)
+    q = xv / scale[:, None, :, None]
+    q = np.minimum(np.maximum(q, np.float32(-E4M3_MAX)), np.float32(E4M3_MAX))
+    return e4m3_encode(q), scale.astype(np.float32)
+
+
+# --------------------------------------------------------------------------
+# FP8 linear
+# --------------------------------------------------------------------------
+def fp8_scaled_mm(a_codes: np.ndarray, w_codes: np.ndarray, scale_a: float, scale_b: float) -> np.ndarray:
+    """torch._scaled_mm(a, w.t(), scale_a, scale_b, out_dtype=bf16).
+
+    a [M, K] and w [N, K] are e4m3fn codes. The products of two e4m3 values
+    are exact; the sum is taken in float64, scaled by scale_a*scale_b, rounded
+    to float32 and then to bf16. Matches a float32-accumulating GEMM up to its
+    accumulation rounding (the parity bar is rtol 1e-2).
+    """
+    a = e4m3_decode(a_codes).astype(np.float64)
+    w = e4m3_decode(w_codes).astype(np.float64)
+    acc = a @ w.T
+    out = (acc * (float(np.float32(scale_a)) * float(np.float32(scale_b)))).astype(np.float32)
+    return bf16_round(out)
+
+
+def fp8_linear(a_codes, w_codes, scale_a, scale_b, bias: T | None) -> np.ndarray:
+    """Patched `FP8Linear.forward` (:1691-1709): _scaled_mm, then `+ bias` in
+    bf16 (R(out + R(bias)), `fused_bias_add_bf16` / `output + bias.to(bf16)`)."""
+    out = fp8_scaled_mm(a_codes, w_codes, scale_a, scale_b)
+    if bias is None:
+        return out
+    return bias_add(bf(out), bias).v
+
+
+# --------------------------------------------------------------------------
+# Video Q/K preattention
+# --------------------------------------------------------------------------
+def split_rope(x: T, cos: T, sin: T) -> T:
+    """Split RoPE as restated by the reference's test
+    (tests/test_triton_ltx_ops.py:232-249): per head, first half f and second
+    half s: [f*cos - s*sin, s*cos + f*sin], each torch op rounded per dtype.
+    x is (B, N, H*D); cos/sin are (B or 1, H, N, D/2)."""
+    b, n, dim = x.v.shape
+    heads = cos.v.shape[1]
+    hd = dim // heads
+    half = hd // 2
+    xh = x.v.reshape(b, n, heads, hd).transpose(0, 2, 1, 3)
+    first = T(xh[..., :half], x.dt)
+    second = T(xh[..., half:], x.dt)
+    out_first = sub(mul(first, cos), mul(second, sin))
+    out_second = add(mul(second, cos), mul(first, sin))
+    dt = out_first.dt
+    o = np.concatenate([out_first.v, out_second.v], axis=-1).transpose(0, 2, 1, 3).reshape(b, n, dim)
+    return T(o, dt)
+
+
+def video_qk_rmsnorm_rope(q: T, k: T, q_weight: T, k_weight: T, eps: float, cos: T, sin: T):
+    """`_torch_video_qk_rmsnorm_rope` (:958-973) with the split RoPE of the
+    reference test restatement (ltx_core's apply_rotary_emb is not vendored)."""
+    qn = rms_norm(q, eps, q_weight)
+    kn = rms_norm(k, eps, k_weight)
+    return split_rope(qn, cos, sin), split_rope(kn, cos, sin)
+
+
+def video_qk_bias_rmsnorm_rope(q: T, k: T, q_bias: T, k_bias: T, q_weight: T, k_weight: T, eps, cos, sin):
+    """`fused_video_qk_bias_rmsnorm_rope` torch path (:519-522)."""
+    return video_qk_rmsnorm_rope(bias_add(q, q_bias), bias_add(k, k_bias), q_weight, k_weight, eps, cos, sin)
+
+
+def video_qkv_rmsnorm_rope_pack(q: T, k: T, v: T, q_weight: T, k_weight: T, eps, cos, sin) -> np.ndarray:
+    """`fused_video_qkv_rmsnorm_rope_pack` (:381-429): [B, N, 3, H, D] of
+    (rope(q), rope(k), v)."""
+    qo, ko = video_qk_rmsnorm_rope(q, k, q_weight, k_weight, eps, cos, sin)
+    b, n, dim = q.v.shape
+    heads = cos.v.shape[1]
+    return np.stack([qo.v, ko.v, v.v], axis=2).reshape(b, n, 3, heads, dim // heads)
+
+
+# --------------------------------------------------------------------------
+# Dense attention
+# --------------------------------------------------------------------------
+def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float | None = None) -> np.ndarray:
+    """softmax(q k^T * scale) v in float64 for [B, H, N, D] arrays (non-causal)."""
+    q = q.astype(np.float64)
+    k = k.astype(np.float64)
+    v = v.astype(np.float64)
+    d = q.shape[-1]
+    s = (q @ np.swapaxes(k, -1, -2)) * (scale if scale is not None else d ** -0.5)
+    s = s - s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    p = p / p.sum(axis=-1, keepdims=True)
+    return p @ v

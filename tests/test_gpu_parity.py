@@ -1,0 +1,422 @@
+"""GPU parity: each HIP op against the numpy oracle on identical seeded inputs.
+
+Inputs are drawn on the CPU with a seeded torch.Generator and copied to the
+GPU, so the oracle and the kernel see the same bits. Bar: bit-exact for every
+elementwise op and the FP8 codes; bf16 outputs of the RMS ops bit-exact
+(the kernel and the oracle both take the mean from the exact sum of squares);
+the FP8 GEMM within rtol 1e-2 (float32 accumulation order differs).
+Every test runs with OPENGENIE_AMD_STRICT=1 and checks the HIP path ran.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import tests.torch_reference as tr
+from oracle import ltx_ops as O
+from oracle.numerics import T, bf16_from_bits, bf16_round, e4m3_decode, e4m3_encode
+from tests.helpers import assert_same_bits, bf16_ulp_distance, nan_canon, np32, randn, to_T
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(autouse=True)
+def _strict(monkeypatch):
+    monkeypatch.setenv("OPENGENIE_AMD_STRICT", "1")
+    from opengenie_amd import ltx_ops
+
+    ltx_ops.reset_hip_calls()
+    yield
+
+
+def _ran(name: str) -> None:
+    from opengenie_amd import ltx_ops
+
+    assert ltx_ops.collect_hip_calls().get(name, 0) > 0, f"{name} did not take the HIP path"
+
+
+def g(t: torch.Tensor) -> torch.Tensor:
+    return t.to(DEV)
+
+
+def out_np(t: torch.Tensor) -> np.ndarray:
+    torch.cuda.synchronize()
+    return t.float().cpu().numpy()
+
+
+# ------------------------------------------------------------ conversions
+def test_selftest_conversions_match_oracle():
+    """The device rounding primitives every kernel uses, bit by bit."""
+    from opengenie_amd import _lib
+
+    rng = np.random.default_rng(100)
+    a = np.concatenate([
+        rng.integers(0, 2 ** 32, size=1 << 22, dtype=np.uint64).astype(np.uint32).view(np.float32),
+        bf16_from_bits(np.arange(1 << 16, dtype=np.uint16)),
+        e4m3_decode(np.arange(256, dtype=np.uint8)),
+    ]).astype(np.float32)
+    # e4m3 midpoints and their float32 neighbours
+    fin = np.unique(e4m3_decode(np.arange(256, dtype=np.uint8)))
+    fin = fin[np.isfinite(fin)]
+    mids = ((fin[1:].astype(np.float64) + fin[:-1]) / 2).astype(np.float32)
+    a = np.concatenate([a, mids, np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, np.float32(-np.inf))])
+    x = torch.from_numpy(a).to(DEV)
+    bo = torch.empty(a.size, dtype=torch.int16, device=DEV)
+    eo = torch.empty(a.size, dtype=torch.uint8, device=DEV)
+    _lib.call("oga_selftest_convert", x.data_ptr(), bo.data_ptr(), eo.data_ptr(), a.size,
+              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got_b = bo.cpu().numpy().view(np.uint16)
+    want_b = (bf16_round(a).view(np.uint32) >> 16).astype(np.uint16)
+    nan = np.isnan(a)
+    assert np.array_equal(got_b[~nan], want_b[~nan])
+    assert np.all((got_b[nan] & 0x7F80) == 0x7F80) and np.all(got_b[nan] & 0x7F)
+    with np.errstate(invalid="ignore"):
+        clamped = np.where(nan, a, np.clip(a, -448, 448)).astype(np.float32)
+    assert np.array_equal(nan_canon(eo.cpu().numpy()), nan_canon(e4m3_encode(clamped)))
+
+
+# ------------------------------------------------------------ Ada family
+def _ada(seed, rows, cols, params, table_dtype, ts_dtype, broadcast=False, batch=1):
+    x = randn((batch, rows, cols), seed)
+    table = randn((params, cols), seed + 1, dtype=table_dtype, std=0.02 if table_dtype == torch.bfloat16 else 1.0)
+    ts_rows = 1 if broadcast else rows
+    ts = randn((batch, ts_rows, params * cols), seed + 2, dtype=ts_dtype, std=0.5)
+    tsg = g(ts)
+    if broadcast:
+        tsg = tsg.expand(batch, rows, params * cols)
+        ts = ts.expand(batch, rows, params * cols)
+    return x, table, ts, g(x), g(table), tsg
+
+
+ADA_CASES = [
+    # rows, cols, params, table dtype, ts dtype, broadcast, batch
+    (9, 2048, 6, torch.float32, torch.bfloat16, False, 1),   # reference test shape
+    (9, 2048, 9, torch.float32, torch.bfloat16, False, 1),
+    (33, 4096, 6, torch.bfloat16, torch.bfloat16, True, 1),  # uniform timestep row
+    (17, 4096, 9, torch.bfloat16, torch.bfloat16, False, 2),
+    (5, 4096, 6, torch.bfloat16, torch.float32, False, 1),   # float32 Ada values
+    (7, 2048, 6, torch.float32, torch.float32, True, 3),
+    (1, 4096, 6, torch.bfloat16, torch.bfloat16, False, 1),
+]
+
+
+@pytest.mark.parametrize("rows,cols,params,tdt,sdt,bc,batch", ADA_CASES)
+def test_adazero_from_ada(rows, cols, params, tdt, sdt, bc, batch):
+    from opengenie_amd.ltx_ops import fused_adazero_from_ada
+
+    x, table, ts, xg, tg, sg = _ada(200 + rows, rows, cols, params, tdt, sdt, bc, batch)
+    out = fused_adazero_from_ada(xg, 1e-6, tg, sg, shift_index=3, scale_index=4)
+    _ran("fused_adazero_from_ada")
+    ref = O.adazero_from_ada(to_T(x), 1e-6, to_T(table), to_T(ts), 3, 4)
+    assert_same_bits(out_np(out), bf16_round(ref.v), "adazero_from_ada")
+
+
+@pytest.mark.parametrize("rows,cols,params,tdt,sdt,bc,batch", ADA_CASES)
+def test_adaln_affine_from_ada(rows, cols, params, tdt, sdt, bc, batch):
+    from opengenie_amd.ltx_ops import fused_adaln_affine_from_ada
+
+    x, table, ts, xg, tg, sg = _ada(300 + rows, rows, cols, params, tdt, sdt, bc, batch)
+    out = fused_adaln_affine_from_ada(xg, tg, sg, shift_index=params - 3, scale_index=params - 2)
+    _ran("fused_adaln_affine_from_ada")
+    ref = O.adaln_affine_from_ada(to_T(x), to_T(table), to_T(ts), params - 3, params - 2)
+    assert_same_bits(out_np(out), bf16_round(ref.v), "adaln_affine_from_ada")
+
+
+@pytest.mark.parametrize("rows,cols,params,tdt,sdt,bc,batch", ADA_CASES)
+def test_mul_from_ada(rows, cols, params, tdt, sdt, bc, batch):
+    from opengenie_amd.ltx_ops import fused_mul_from_ada
+
+    x, table, ts, xg, tg, sg = _ada(400 + rows, rows, cols, params, tdt, sdt, bc, batch)
+    out = fused_mul_from_ada(xg, tg, sg, gate_index=params - 1)
+    _ran("fused_mul_from_ada")
+    ref = O.mul_from_ada(to_T(x), to_T(table), to_T(ts), params - 1)
+    assert_same_bits(out_np(out), bf16_round(ref.v), "mul_from_ada")
+
+
+@pytest.mark.parametrize("rows,cols,params,tdt,sdt,bc,batch", ADA_CASES)
+def test_residual_gate_from_ada(rows, cols, params, tdt, sdt, bc, batch):
+    from opengenie_amd.ltx_ops import fused_residual_gate_from_ada
+
+    x, table, ts, xg, tg, sg = _ada(500 + rows, rows, cols, params, tdt, sdt, bc, batch)
+    y = randn((batch, rows, cols), 550 + rows)
+    out = fused_residual_gate_from_ada(xg, g(y), tg, sg, gate_index=params - 1)
+    _ran("fused_residual_gate_from_ada")
+    ref = O.residual_gate_from_ada(to_T(x), to_T(y), to_T(table), to_T(ts), params - 1)
+    assert_same_bits(out_np(out), bf16_round(ref.v), "residual_gate_from_ada")
+
+
+@pytest.mark.parametrize("bias_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,cols,params,tdt,sdt,bc,batch", ADA_CASES)
+def test_residual_gate_bias_from_ada(rows, cols, params, tdt, sdt, bc, batch, bias_dtype):
+    from opengenie_amd.ltx_ops import fused_residual_gate_bias_from_ada
+
+    x, table, ts, xg, tg, sg = _ada(600 + rows, rows, cols, params, tdt, sdt, bc, batch)
+    y = randn((batch, rows, cols), 650 + rows)
+    bias = randn((cols,), 660 + rows, dtype=bias_dtype, std=0.01)
+    out = fused_residual_gate_bias_from_ada(xg, g(y), g(bias), tg, sg, gate_index=2)
+    _ran("fused_residual_gate_bias_from_ada")
+    ref = O.residual_gate_bias_from_ada(to_T(x), to_T(y), to_T(bias), to_T(table), to_T(ts), 2)
+    assert_same_bits(out_np(out), bf16_round(ref.v), "residual_gate_bias_from_ada")
+
+
+def test_adazero_strided_scale_shift():
+    """Reference test :8-26 shape: stride-3 views for scale and shift."""
+    from opengenie_amd.ltx_ops import fused_adazero
+
+    x = randn((1, 7, 2048), 0)
+    ss = randn((1, 7, 3, 2048), 1)
+    out = fused_adazero(g(x), 1e-6, g(ss)[:, :, 1, :], g(ss)[:, :, 2, :])
+    _ran("fused_adazero")
+    ref = O.adazero(to_T(x), 1e-6, to_T(ss[:, :, 1, :]), to_T(ss[:, :, 2, :]))
+    assert_same_bits(out_np(out), ref.v, "adazero strided")
+
+
+@pytest.mark.parametrize("shape_s", [(1, 1, 4096), (2, 1, 4096), (4096,), (2, 5, 4096)])
+def test_adazero_broadcast_scale_shift(shape_s):
+    from opengenie_amd.ltx_ops import fused_adazero
+
+    x = randn((2, 5, 4096), 10)
+    sc = randn(shape_s, 11, dtype=torch.float32, std=0.1)
+    sh = randn(shape_s, 12, std=0.1)
+    out = fused_adazero(g(x), 1e-6, g(sc), g(sh))
+    _ran("fused_adazero")
+    ref = O.adazero(to_T(x), 1e-6, to_T(sc), to_T(sh))
+    assert_same_bits(out_np(out), bf16_round(ref.v), "adazero broadcast")
+
+
+def test_residual_gate_bf16_strided_gate():
+    """Reference test :29-47: gate is a stride-3 view."""
+    from opengenie_amd.ltx_ops import fused_residual_gate_bf16
+
+    x, y = randn((1, 7, 2048), 1), randn((1, 7, 2048), 2)
+    gates = randn((1, 7, 3, 2048), 3)
+    out = fused_residual_gate_bf16(g(x), g(y), g(gates)[:, :, 1, :])
+    _ran("fused_residual_gate_bf16")
+    assert_same_bits(out_np(out), O.residual_gate(to_T(x), to_T(y), to_T(gates[:, :, 1, :])).v, "residual gate")
+
+
+@pytest.mark.parametrize("gate_shape", [(1, 1, 4096), (4096,), (3, 1, 4096)])
+def test_residual_gate_bf16_broadcast(gate_shape):
+    from opengenie_amd.ltx_ops import fused_residual_gate_bf16
+
+    x, y = randn((3, 11, 4096), 4), randn((3, 11, 4096), 5)
+    gate = randn(gate_shape, 6)
+    out = fused_residual_gate_bf16(g(x), g(y), g(gate))
+    assert_same_bits(out_np(out), O.residual_gate(to_T(x), to_T(y), to_T(gate)).v, "residual gate bc")
+
+
+@pytest.mark.parametrize("rows,cols", [(11, 2048), (64, 16384), (3, 4100), (5, 13)])
+@pytest.mark.parametrize("bias_dtype", [torch.float32, torch.bfloat16])
+def test_bias_add(rows, cols, bias_dtype):
+    from opengenie_amd.ltx_ops import fused_bias_add_bf16
+
+    x = randn((rows, cols), 20)
+    bias = randn((cols,), 21, dtype=bias_dtype)
+    out = fused_bias_add_bf16(g(x), g(bias))
+    _ran("fused_bias_add_bf16")
+    assert_same_bits(out_np(out), O.bias_add(to_T(x), to_T(bias)).v, "bias_add")
+
+
+def test_head_gate_mul():
+    from opengenie_amd.ltx_ops import fused_head_gate_mul_bf16
+
+    out = randn((1, 13, 4096), 11)
+    gates = (2.0 * torch.sigmoid(randn((1, 13, 32), 12))).to(torch.bfloat16)
+    y = fused_head_gate_mul_bf16(g(out), g(gates), 32, 128)
+    _ran("fused_head_gate_mul_bf16")
+    assert_same_bits(out_np(y), O.head_gate_mul(to_T(out), to_T(gates), 32, 128).v, "head_gate_mul")
+
+
+# ------------------------------------------------------------ FP8 quantizers
+@pytest.mark.parametrize("zero_dim", [True, False])
+@pytest.mark.parametrize("scale", [0.05, 0.37, 1.0, 3.3e-3, 0.11160714])
+def test_fp8_quantize_exhaustive_bf16(scale, zero_dim):
+    """All 65536 bf16 patterns; codes equal the oracle's GPU-torch semantics."""
+    from opengenie_amd.ltx_ops import fused_fp8_quantize_e4m3
+
+    x = bf16_from_bits(np.arange(1 << 16, dtype=np.uint16))
+    xt = torch.from_numpy(x.copy()).to(torch.bfloat16)
+    s = torch.tensor(scale, dtype=torch.float32)
+    if not zero_dim:
+        s = s.reshape(1)
+    q = fused_fp8_quantize_e4m3(g(xt), g(s))
+    _ran("fused_fp8_quantize_e4m3")
+    torch.cuda.synchronize()
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = O.fp8_quantize_e4m3(T(x, "bf16"), scale, zero_dim, device="cuda")
+    assert np.array_equal(nan_canon(q.view(torch.uint8).cpu().numpy()), nan_canon(ref))
+
+
+@pytest.mark.parametrize("zero_dim", [True, False])
+def test_fp8_quantize_oracle_matches_torch_on_gpu(zero_dim):
+    """Pins the oracle's device semantics: torch evaluating the reference's
+    expression on the GPU gives the same codes as the oracle (device='cuda')."""
+    x = bf16_from_bits(np.arange(1 << 16, dtype=np.uint16))
+    xt = torch.from_numpy(x.copy()).to(torch.bfloat16)
+    for scale in (0.05, 0.37, 3.3e-3, 0.11160714, 0.0123):
+        s = torch.tensor(scale, dtype=torch.float32)
+        if not zero_dim:
+            s = s.reshape(1)
+        ref = tr.fp8_quantize_e4m3(g(xt), g(s)).view(torch.uint8).cpu().numpy()
+        with np.errstate(over="ignore", invalid="ignore"):
+            ours = O.fp8_quantize_e4m3(T(x, "bf16"), scale, zero_dim, device="cuda")
+        assert np.array_equal(nan_canon(ours), nan_canon(ref)), scale
+
+
+@pytest.mark.parametrize("n", [1, 15, 16, 17, 1000, 4096 * 3 + 5])
+def test_fp8_quantize_ragged_sizes(n):
+    from opengenie_amd.ltx_ops import fused_fp8_quantize_e4m3
+
+    x = randn((n,), 30 + n, std=40.0)
+    s = torch.tensor(0.07)
+    q = fused_fp8_quantize_e4m3(g(x), g(s))
+    torch.cuda.synchronize()
+    ref = O.fp8_quantize_e4m3(to_T(x), 0.07, True, device="cuda")
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), ref)
+
+
+def test_gelu_tanh_fp8_quantize():
+    from opengenie_amd.ltx_ops import fused_gelu_tanh_fp8_quantize_e4m3
+
+    x = randn((64, 4096), 31, std=2.0)
+    s = torch.tensor(0.02)
+    q = fused_gelu_tanh_fp8_quantize_e4m3(g(x), g(s))
+    _ran("fused_gelu_tanh_fp8_quantize_e4m3")
+    torch.cuda.synchronize()
+    ref = O.fp8_quantize_e4m3(O.gelu_tanh(to_T(x)), 0.02, True, device="cuda")
+    got = q.view(torch.uint8).cpu().numpy()
+    # tanh's last float32 bit is library-specific: rare one-step bf16 GELU
+    # differences may move a code by one step.
+    assert (got != ref).mean() < 1e-3
+    d = np.abs(e4m3_decode(got).astype(np.float64) - e4m3_decode(ref))
+    assert np.nanmax(d / np.maximum(np.abs(e4m3_decode(ref)), 2 ** -9)) <= 0.126
+
+
+@pytest.mark.parametrize("shape", [(1, 33, 32, 128), (2, 17, 16, 128), (1, 40, 32, 64), (1, 9216 // 16, 32, 128)])
+def test_fp8_per_head(shape):
+    from opengenie_amd.ltx_ops import fused_fp8_quantize_e4m3_per_head_4d
+
+    x = randn(shape, 40)
+    if shape[0] > 1:
+        x[1, :, 3, :] = 0  # an all-zero head takes the 1e-12 clamp
+    q, s = fused_fp8_quantize_e4m3_per_head_4d(g(x))
+    _ran("fused_fp8_quantize_e4m3_per_head_4d")
+    torch.cuda.synchronize()
+    qr, sr = O.fp8_per_head_quantize(np32(x))
+    assert_same_bits(s.cpu().numpy(), sr, "per-head scale")
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), qr)
+
+
+# ------------------------------------------------------------ Q/K preattention
+def _rope(seed, tokens, cos_dtype=torch.bfloat16, w_dtype=torch.bfloat16, cos_batch=1):
+    q = randn((1, tokens, 4096), seed)
+    k = randn((1, tokens, 4096), seed + 1)
+    qw = randn((4096,), seed + 2, dtype=w_dtype, std=0.05, mean=1.0)
+    kw = randn((4096,), seed + 3, dtype=w_dtype, std=0.05, mean=1.0)
+    freqs = randn((cos_batch, 32, tokens, 64), seed + 4, dtype=torch.float32, std=3.0)
+    return q, k, qw, kw, freqs.cos().to(cos_dtype), freqs.sin().to(cos_dtype)
+
+
+@pytest.mark.parametrize("tokens,cos_dtype,w_dtype", [
+    (17, torch.bfloat16, torch.bfloat16), (1, torch.bfloat16, torch.bfloat16), (130, torch.float32, torch.bfloat16),
+    (64, torch.bfloat16, torch.float32)])
+def test_video_qk_rmsnorm_rope(tokens, cos_dtype, w_dtype):
+    from opengenie_amd.ltx_ops import fused_video_qk_rmsnorm_rope
+
+    q, k, qw, kw, cos, sin = _rope(800 + tokens, tokens, cos_dtype, w_dtype)
+    oq, ok = fused_video_qk_rmsnorm_rope(g(q), g(k), g(qw), g(kw), 1e-6, g(cos), g(sin))
+    _ran("fused_video_qk_rmsnorm_rope")
+    rq, rk = O.video_qk_rmsnorm_rope(to_T(q), to_T(k), to_T(qw), to_T(kw), 1e-6, to_T(cos), to_T(sin))
+    assert_same_bits(out_np(oq), bf16_round(rq.v), "q")
+    assert_same_bits(out_np(ok), bf16_round(rk.v), "k")
+
+
+def test_video_qk_rmsnorm_rope_strided_cos():
+    """cos/sin as non-contiguous views (head and token strides permuted)."""
+    from opengenie_amd.ltx_ops import fused_video_qk_rmsnorm_rope
+
+    q, k, qw, kw, cos, sin = _rope(900, 24)
+    cos_v = g(cos.permute(0, 2, 1, 3).contiguous()).permute(0, 2, 1, 3)
+    sin_v = g(sin.permute(0, 2, 1, 3).contiguous()).permute(0, 2, 1, 3)
+    assert not cos_v.is_contiguous()
+    oq, ok = fused_video_qk_rmsnorm_rope(g(q), g(k), g(qw), g(kw), 1e-6, cos_v, sin_v)
+    rq, rk = O.video_qk_rmsnorm_rope(to_T(q), to_T(k), to_T(qw), to_T(kw), 1e-6, to_T(cos), to_T(sin))
+    assert_same_bits(out_np(oq), rq.v, "q")
+    assert_same_bits(out_np(ok), rk.v, "k")
+
+
+def test_video_qk_rmsnorm_rope_separate_and_pack_and_bias():
+    from opengenie_amd import ltx_ops as L
+
+    q, k, qw, kw, cos, sin = _rope(950, 33)
+    v = randn((1, 33, 4096), 960)
+    rq, rk = O.video_qk_rmsnorm_rope(to_T(q), to_T(k), to_T(qw), to_T(kw), 1e-6, to_T(cos), to_T(sin))
+    sq, sk = L.fused_video_qk_rmsnorm_rope_separate(g(q), g(k), g(qw), g(kw), 1e-6, g(cos), g(sin))
+    assert_same_bits(out_np(sq), rq.v, "separate q")
+    assert_same_bits(out_np(sk), rk.v, "separate k")
+    qkv = L.fused_video_qkv_rmsnorm_rope_pack(g(q), g(k), g(v), g(qw), g(kw), 1e-6, g(cos), g(sin))
+    ref = O.video_qkv_rmsnorm_rope_pack(to_T(q), to_T(k), to_T(v), to_T(qw), to_T(kw), 1e-6, to_T(cos), to_T(sin))
+    assert_same_bits(out_np(qkv), ref, "pack")
+    qb = randn((4096,), 970, dtype=torch.float32, std=0.1)
+    kb = randn((4096,), 971, dtype=torch.float32, std=0.1)
+    bq, bk = L.fused_video_qk_bias_rmsnorm_rope(g(q), g(k), g(qb), g(kb), g(qw), g(kw), 1e-6, g(cos), g(sin))
+    rbq, rbk = O.video_qk_bias_rmsnorm_rope(to_T(q), to_T(k), to_T(qb), to_T(kb), to_T(qw), to_T(kw), 1e-6,
+                                            to_T(cos), to_T(sin))
+    assert_same_bits(out_np(bq), rbq.v, "bias q")
+    assert_same_bits(out_np(bk), rbk.v, "bias k")
+
+
+# ------------------------------------------------------------ FP8 linear
+def _fp8_weights(n, k, seed):
+    wf = randn((n, k), seed, dtype=torch.float32, std=0.02)
+    ws = wf.abs().amax() / 448.0
+    w = torch.clamp(wf / ws, -448, 448).to(torch.float8_e4m3fn)
+    return w, ws.reshape(())
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 256, 128), (512, 768, 1024), (300, 520, 384), (1, 16, 128),
+                                   (1024, 4096, 4096)])
+@pytest.mark.parametrize("bias_dtype", [None, torch.bfloat16, torch.float32])
+def test_fp8_linear(m, n, k, bias_dtype):
+    from opengenie_amd.ltx_ops import fp8_scaled_mm
+
+    x = randn((m, k), 70 + m, std=1.0)
+    sa = (x.float().abs().amax() / 448.0).reshape(())
+    a = torch.clamp(x.float() / sa, -448, 448).to(torch.float8_e4m3fn)
+    w, sb = _fp8_weights(n, k, 71 + n)
+    bias = randn((n,), 72, dtype=bias_dtype, std=0.01) if bias_dtype is not None else None
+    out = fp8_scaled_mm(g(a), g(w), g(sa), g(sb), g(bias) if bias is not None else None)
+    _ran("fp8_scaled_mm")
+    ref = O.fp8_linear(a.view(torch.uint8).numpy(), w.view(torch.uint8).numpy(), float(sa), float(sb),
+                       to_T(bias) if bias is not None else None)
+    got = out_np(out)
+    np.testing.assert_allclose(got, ref, rtol=1e-2, atol=1e-3 * float(np.abs(ref).max()))
+    # The float32 accumulation order only moves results across a bf16
+    # rounding boundary rarely.
+    assert (bf16_ulp_distance(got, ref) > 1).mean() < 1e-3
+
+
+def test_fp8_linear_forward_module():
+    """The patched FP8Linear.forward on a duck-typed module, 3-D input."""
+    from opengenie_amd.ltx_ops import fp8_linear_forward
+
+    class Lin(torch.nn.Module):
+        pass
+
+    lin = Lin()
+    w, sb = _fp8_weights(512, 256, 90)
+    lin.weight = g(w)
+    lin.weight_scale = g(sb)
+    lin.input_scale = g(torch.tensor(0.0123))
+    lin.bias = g(randn((512,), 91, std=0.01))
+    x = randn((1, 77, 256), 92)
+    out = fp8_linear_forward(lin, g(x))
+    assert out.shape == (1, 77, 512)
+    q = O.fp8_quantize_e4m3(to_T(x), 0.0123, True, device="cuda").reshape(77, 256)
+    ref = O.fp8_linear(q, w.view(torch.uint8).numpy(), 0.0123, float(sb), to_T(lin.bias.cpu()))
+    np.testing.assert_allclose(out_np(out).reshape(77, 512), ref, rtol=1e-2, atol=1e-4)

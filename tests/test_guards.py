@@ -1,0 +1,97 @@
+"""Guard behaviour of the drop-in host module on the CPU.
+
+As in the reference, an input the fused kernel does not take falls back to
+the reference's torch expression; on CPU tensors every op takes that path,
+which is checked here against torch evaluating the same expression. Guard
+reason strings follow triton_ltx_ops.py:1513-1537."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import tests.torch_reference as tr
+from opengenie_amd import ltx_ops as L
+from tests.helpers import randn
+
+
+def test_cpu_inputs_take_the_torch_path():
+    x = randn((1, 9, 2048), 1)
+    table = randn((6, 2048), 2, dtype=torch.float32)
+    ts = randn((1, 9, 6 * 2048), 3)
+    L.reset_hip_calls()
+    out = L.fused_adazero_from_ada(x, 1e-6, table, ts, shift_index=3, scale_index=4)
+    assert torch.equal(out, tr.adazero_from_ada(x, 1e-6, table, ts, 3, 4))
+    assert L.collect_hip_calls() == {}
+
+
+def test_cpu_fallbacks_equal_reference_expressions():
+    x = randn((1, 9, 2048), 4)
+    y = randn((1, 9, 2048), 5)
+    table = randn((9, 2048), 6, dtype=torch.float32)
+    ts = randn((1, 9, 9 * 2048), 7)
+    bias = randn((2048,), 8, dtype=torch.float32)
+    assert torch.equal(L.fused_adaln_affine_from_ada(x, table, ts, shift_index=6, scale_index=7),
+                       tr.adaln_affine_from_ada(x, table, ts, 6, 7))
+    assert torch.equal(L.fused_residual_gate_from_ada(x, y, table, ts, gate_index=8),
+                       tr.residual_gate_from_ada(x, y, table, ts, 8))
+    assert torch.equal(L.fused_residual_gate_bias_from_ada(x, y, bias, table, ts, gate_index=8),
+                       tr.residual_gate_bias_from_ada(x, y, bias, table, ts, 8))
+    assert torch.equal(L.fused_mul_from_ada(x, table, ts, gate_index=8), tr.mul_from_ada(x, table, ts, 8))
+    assert torch.equal(L.fused_bias_add_bf16(x, bias), tr.bias_add(x, bias))
+    s = torch.tensor(0.05)
+    assert torch.equal(L.fused_fp8_quantize_e4m3(x, s).view(torch.uint8),
+                       tr.fp8_quantize_e4m3(x, s).view(torch.uint8))
+
+
+def test_residual_mode_selection():
+    x, y, gate = randn((1, 3, 2048), 1), randn((1, 3, 2048), 2), randn((1, 3, 2048), 3)
+    try:
+        L.set_block_residual_mode("addcmul")
+        assert torch.equal(L._simple_residual_gate(x, y, gate), torch.addcmul(x, y, gate))
+        L.set_block_residual_mode("triton_simple_bf16_round")
+        assert torch.equal(L._simple_residual_gate(x, y, gate), x + y * gate)
+        with pytest.raises(ValueError):
+            L.set_block_residual_mode("bogus")
+    finally:
+        L.set_block_residual_mode("triton_simple_bf16_round")
+
+
+def test_preattention_guard_reasons():
+    q = randn((1, 5, 4096), 1)
+    w = randn((4096,), 2)
+    cos = randn((1, 32, 5, 64), 3)
+    assert L._fused_video_qk_rmsnorm_rope_guard_reason(q, q, w, w, cos, cos) == "qk_device_or_dtype"
+    # The torch path is the reference's test restatement.
+    oq, ok = L.fused_video_qk_rmsnorm_rope(q, q, w, w, 1e-6, cos, cos)
+    rq, rk = tr.video_qk_rmsnorm_rope(q, q, w, w, 1e-6, cos, cos)
+    assert torch.equal(oq, rq) and torch.equal(ok, rk)
+
+
+def test_pack_returns_none_when_guard_fails():
+    q = randn((1, 5, 4096), 1)
+    w = randn((4096,), 2)
+    cos = randn((1, 32, 5, 64), 3)
+    assert L.fused_video_qkv_rmsnorm_rope_pack(q, q, q, w, w, 1e-6, cos, cos) is None
+
+
+def test_ada_index_and_shape_errors():
+    x = randn((1, 4, 2048), 1)
+    table = randn((6, 2048), 2)
+    ts = randn((1, 5, 6 * 2048), 3)  # token count mismatch
+    with pytest.raises(ValueError):
+        L.fused_adazero_from_ada(x, 1e-6, table, ts, shift_index=0, scale_index=1)
+
+
+def test_strict_mode_only_affects_gpu_tensors(monkeypatch):
+    monkeypatch.setenv("OPENGENIE_AMD_STRICT", "1")
+    x = randn((1, 3, 2048), 1)
+    bias = randn((2048,), 2)
+    assert torch.equal(L.fused_bias_add_bf16(x, bias), tr.bias_add(x, bias))
+
+
+def test_per_head_cpu_path():
+    x = randn((1, 8, 4, 64), 9)
+    q, s = L.fused_fp8_quantize_e4m3_per_head_4d(x)
+    qr, sr = tr.fp8_per_head(x)
+    assert torch.equal(q.view(torch.uint8), qr.view(torch.uint8)) and torch.equal(s, sr)
