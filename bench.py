@@ -40,6 +40,8 @@ def _parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fused", action="store_true")
     ap.add_argument("--seed", type=int, default=20260100)
+    ap.add_argument("--only", choices=["gemm", "quant", "fused", "copy"], default=None,
+                    help="run one workload --steps times and print its mean time (for profiler runs)")
     return ap.parse_args()
 
 
@@ -167,6 +169,22 @@ def fused_op_rows(seed: int) -> dict:
     return rows
 
 
+def copy_reference() -> dict:
+    """Achievable streaming bandwidth on this GPU: torch's device copy of a
+    bf16 tensor (read + write), for calibration next to the fused ops."""
+    import torch
+
+    out = {}
+    for n in (37_748_736 // 2, 461_373_440 // 4):
+        a = torch.empty(n, device="cuda", dtype=torch.bfloat16).normal_()
+        b = torch.empty_like(a)
+        us = _graph_time_us(lambda: b.copy_(a), reps=10, inner=10)
+        gbs = 2 * n * 2 / (us * 1e-6) / 1e9
+        out[f"copy_{2 * n * 2 // 1_000_000}MB"] = {"us": round(us, 3), "GB/s": round(gbs, 1),
+                                                    "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    return out
+
+
 def synthetic_timestep_embeddings(tokens: int, width: int, prefix_tokens: int, seed: int, device: str):
     """Per-token Ada timestep embeddings for a continuation window: the first
     `prefix_tokens` tokens (the clean conditioning frames) share the t = 0
@@ -236,7 +254,31 @@ def main() -> None:
 
     _lib.load()
     dev = "cuda"
+    if args.only == "fused":
+        print(json.dumps(fused_op_rows(args.seed)))
+        return
+    if args.only == "copy":
+        print(json.dumps(copy_reference()))
+        return
     x, s_in, w, s_w, bias = make_fp8_linear_inputs(args.seed, dev)
+    if args.only in ("gemm", "quant"):
+        q = L.fused_fp8_quantize_e4m3(x, s_in)
+        out = torch.empty((M, N), device=dev, dtype=torch.bfloat16)
+        lib = _lib.load()
+        st = torch.cuda.current_stream()
+        gargs = (q.data_ptr(), K, w.data_ptr(), K, s_in.data_ptr(), s_w.data_ptr(), bias.data_ptr(), _lib.DT_BF16,
+                 out.data_ptr(), N, M, N, K, st.cuda_stream)
+        fn = (lambda: lib.oga_fp8_linear(*gargs)) if args.only == "gemm" else (lambda: L.fused_fp8_quantize_e4m3(x, s_in))
+        for _ in range(args.warmup):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for _ in range(args.steps):
+            fn()
+        e1.record(st)
+        e1.synchronize()
+        print(json.dumps({"only": args.only, "us": e0.elapsed_time(e1) * 1000.0 / args.steps}))
+        return
 
     def step():
         q = L.fused_fp8_quantize_e4m3(x, s_in)
@@ -274,6 +316,8 @@ def main() -> None:
     achieved = flops / (gemm_us * 1e-6) / 1e12
 
     fused = {} if args.no_fused else fused_op_rows(args.seed)
+    if fused:
+        fused["copy_reference"] = copy_reference()
     cpu = None if args.no_cpu else cpu_baseline(x, s_in, w, s_w, bias)
 
     line = {

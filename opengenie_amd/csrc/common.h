@@ -89,6 +89,32 @@ OGA_DEVICE void load8(const void* base, int dt, int64_t off, int64_t sc, bool ve
   }
 }
 
+// Compile-time-typed 8-wide load (DT = OGA_DT_BF16 or OGA_DT_F32); VEC
+// selects 128-bit loads (contiguous, aligned) or an element gather.
+template <int DT, bool VEC>
+OGA_DEVICE void load8_t(const void* base, int64_t off, int64_t sc, float* f) {
+  if (DT == OGA_DT_BF16) {
+    const uint16_t* p = (const uint16_t*)base + off;
+    if (VEC) {
+      unpack8(*(const uint4*)p, f);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[i] = __uint_as_float(((uint32_t)p[i * sc]) << 16);
+    }
+  } else {
+    const float* p = (const float*)base + off;
+    if (VEC) {
+      const float4 a = *(const float4*)p;
+      const float4 b = *(const float4*)(p + 4);
+      f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+      f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[i] = p[i * sc];
+    }
+  }
+}
+
 // ------------------------------------------------------------- reductions
 // Wave-wide sum of a double with DPP butterflies inside each 16-lane row,
 // a ds_swizzle across the two rows of each half, and readlane across halves.

@@ -107,16 +107,20 @@ __global__ __launch_bounds__(256) void k_head_amax(const uint16_t* x, float* par
   }
 }
 
-// Pass 2: scale[b, h] = max(amax, 1e-12) / 448 (IEEE division).
-__global__ __launch_bounds__(256) void k_head_scale(const float* partial, float* scale, int64_t batch, int heads,
-                                                    int nchunk) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= batch * heads) return;
-  const int64_t b = i / heads;
-  const int h = (int)(i - b * heads);
+// Pass 2: scale[b, h] = max(amax, 1e-12) / 448 (IEEE division). One wave
+// per (b, h): lanes stride over the block partials, then a wave-wide max.
+__global__ __launch_bounds__(64) void k_head_scale(const float* partial, float* scale, int heads, int nchunk) {
+  const int64_t bh = blockIdx.x;
+  const int64_t b = bh / heads;
+  const int h = (int)(bh - b * heads);
+  const int lane = threadIdx.x;
   float m = 0.0f;
-  for (int c = 0; c < nchunk; ++c) m = fmaxf(m, partial[(b * nchunk + c) * heads + h]);
-  scale[i] = fmaxf(m, 1e-12f) / 448.0f;
+  for (int c = lane; c < nchunk; c += 64) m = fmaxf(m, partial[(b * nchunk + c) * heads + h]);
+  m = row16_max(m);
+  m = fmaxf(m, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(m), 0x401F)));
+  m = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0)),
+            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32)));
+  if (lane == 0) scale[bh] = fmaxf(m, 1e-12f) / 448.0f;
 }
 
 // Pass 3: q = e4m3(clamp(x / scale[b, h], +-448)), 16 elements per thread
@@ -224,8 +228,8 @@ extern "C" int oga_fp8_quantize_per_head(const void* x, void* q, float* scale_ou
   int rc = launch_status();
   if (rc) return rc;
   const int64_t bh = batch * heads;
-  hipLaunchKernelGGL(k_head_scale, dim3((unsigned)((bh + 255) / 256)), dim3(256), 0, st, partial, scale_out, batch,
-                     (int)heads, (int)head_chunks(tokens));
+  hipLaunchKernelGGL(k_head_scale, dim3((unsigned)bh), dim3(64), 0, st, partial, scale_out, (int)heads,
+                     (int)head_chunks(tokens));
   if ((rc = launch_status())) return rc;
   const int64_t n = batch * tokens * row;
   const int64_t threads = n / 16;

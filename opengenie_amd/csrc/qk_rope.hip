@@ -36,126 +36,197 @@ struct RopeArgs {
   int64_t c_sb, c_sh, c_st;
   int64_t s_sb, s_sh, s_st;
   int64_t out_stride;  // elements between consecutive output rows
-  int64_t rows, tokens;
+  int64_t tokens;
   int cols;
   int w_dt, b_dt, cs_dt;
   int cs_vec;
-  int rows_per_wave;
   float eps;
 };
 
-OGA_DEVICE int64_t rope_wave_id() { return (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); }
-
-// Normalised (and weight-scaled) row of one tensor as packed bf16 pairs.
-template <int CH, bool BIAS>
-OGA_DEVICE void norm_row(const uint16_t* x, const void* w, int w_dt, const void* bias, int b_dt, int64_t r,
-                         int cols, float eps, int lane, uint4* nv) {
-  float xf[CH][8];
-  double ss = 0.0;
-#pragma unroll
-  for (int j = 0; j < CH; ++j) {
-    const uint4 u = *(const uint4*)(x + r * cols + j * 512 + lane * 8);
-    unpack8(u, xf[j]);
-    if (BIAS) {
-      float bv[8];
-      load8(bias, b_dt, j * 512 + lane * 8, 1, true, bv);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) xf[j][i] = rbf(xf[j][i] + rbf(bv[i]));
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const double d = (double)xf[j][i];
-      ss = fma(d, d, ss);
-    }
-  }
-  const float inv = rms_inv(ss, cols, eps);
-#pragma unroll
-  for (int j = 0; j < CH; ++j) {
-    float wv[8], n[8];
-    load8(w, w_dt, j * 512 + lane * 8, 1, true, wv);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) n[i] = (xf[j][i] * inv) * wv[i];
-    nv[j] = pack8(n);
-  }
+OGA_DEVICE void lds_put8(float* s, int c0, const float* v) {
+  *(float4*)(s + c0) = make_float4(v[0], v[1], v[2], v[3]);
+  *(float4*)(s + c0 + 4) = make_float4(v[4], v[5], v[6], v[7]);
+}
+OGA_DEVICE void lds_get8(const float* s, int c0, float* v) {
+  const float4 a = *(const float4*)(s + c0);
+  const float4 b = *(const float4*)(s + c0 + 4);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
+// RMS normaliser of one packed row (after the optional bias, which the
+// row already carries): inv = 1/sqrt(mean(x^2) + eps), exact sum of squares.
 template <int CH>
-OGA_DEVICE void rope_row(const uint4* nv, const float (*cs)[8], const float (*sn)[8], bool second, bool cs_bf,
-                         uint16_t* out, int lane) {
+OGA_DEVICE float row_inv(const uint4* xv, float eps) {
+  double ss[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
   for (int j = 0; j < CH; ++j) {
-    uint4 pv;
-    pv.x = row_swap8(nv[j].x);
-    pv.y = row_swap8(nv[j].y);
-    pv.z = row_swap8(nv[j].z);
-    pv.w = row_swap8(nv[j].w);
-    float n[8], p[8], o[8];
-    unpack8(nv[j], n);
-    unpack8(pv, p);
+    float xf[8];
+    unpack8(xv[j], xf);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      float a = n[i] * cs[j][i];
-      float b = p[i] * sn[j][i];
-      if (cs_bf) {
-        a = rbf(a);
-        b = rbf(b);
-      }
-      o[i] = second ? a + b : a - b;
+      const double d = (double)xf[i];
+      ss[i & 3] = fma(d, d, ss[i & 3]);
     }
-    *(uint4*)(out + j * 512 + lane * 8) = pack8(o);
   }
+  return rms_inv((ss[0] + ss[1]) + (ss[2] + ss[3]), CH * 512, eps);
 }
 
-template <int CH, int NT, bool BIAS, bool PACK>
+// x <- R(x + R(bias)) for one vector step (bias already rounded in LDS).
+OGA_DEVICE uint4 add_bias8(const uint4& xv, const float* B, int c0) {
+  float xf[8], bv[8];
+  unpack8(xv, xf);
+  lds_get8(B, c0, bv);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) xf[i] = xf[i] + bv[i];
+  return pack8(xf);
+}
+
+// n = R(x * inv * w) for one vector step, packed.
+OGA_DEVICE uint4 norm8(const uint4& xv, const float* W, int c0, float inv) {
+  float xf[8], wv[8], n[8];
+  unpack8(xv, xf);
+  lds_get8(W, c0, wv);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) n[i] = (xf[i] * inv) * wv[i];
+  return pack8(n);
+}
+
+// Split RoPE of one vector step: partner values come from lane l^8.
+OGA_DEVICE uint4 rope8(const uint4& nv, const float* cs, const float* sn, bool second, bool cs_bf) {
+  uint4 pv;
+  pv.x = row_swap8(nv.x);
+  pv.y = row_swap8(nv.y);
+  pv.z = row_swap8(nv.z);
+  pv.w = row_swap8(nv.w);
+  float n[8], p[8], o[8];
+  unpack8(nv, n);
+  unpack8(pv, p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float a = n[i] * cs[i];
+    float b = p[i] * sn[i];
+    if (cs_bf) {
+      a = rbf(a);
+      b = rbf(b);
+    }
+    o[i] = second ? a + b : a - b;
+  }
+  return pack8(o);
+}
+
+// Grid (blocks_per_batch, batch); a 4-wave workgroup stages the norm weights
+// (and biases) in LDS as float, then each wave strides over token rows.
+template <int CH, int NT, bool BIAS, bool PACK, int CDT, bool VEC>
 __global__ __launch_bounds__(256) void k_rmsnorm_rope(RopeArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int64_t r0 = rope_wave_id() * a.rows_per_wave;
-  if (r0 >= a.rows) return;
-  const int64_t r1 = min(r0 + (int64_t)a.rows_per_wave, a.rows);
+  constexpr int C = CH * 512;
+  __shared__ float W0[C];
+  __shared__ float W1[NT == 2 ? C : 1];
+  __shared__ float B0[BIAS ? C : 1];
+  __shared__ float B1[BIAS && NT == 2 ? C : 1];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t b = blockIdx.y;
+#pragma unroll 1
+  for (int c0 = tid * 8; c0 < C; c0 += 256 * 8) {
+    float v[8];
+    load8(a.w0, a.w_dt, c0, 1, true, v);
+    lds_put8(W0, c0, v);
+    if (NT == 2) {
+      load8(a.w1, a.w_dt, c0, 1, true, v);
+      lds_put8(W1, c0, v);
+    }
+    if (BIAS) {
+      load8(a.b0, a.b_dt, c0, 1, true, v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = rbf(v[i]);
+      lds_put8(B0, c0, v);
+      if (NT == 2) {
+        load8(a.b1, a.b_dt, c0, 1, true, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = rbf(v[i]);
+        lds_put8(B1, c0, v);
+      }
+    }
+  }
+  __syncthreads();
+
   const bool second = (lane & 8) != 0;
   const int hd0 = (lane & 7) * 8;
-  const bool cs_bf = a.cs_dt == OGA_DT_BF16;
-
-  for (int64_t r = r0; r < r1; ++r) {
-    const int64_t b = r / a.tokens;
-    const int64_t t = r - b * a.tokens;
-
-    float cs[CH][8], sn[CH][8];
+  constexpr bool cs_bf = CDT == OGA_DT_BF16;
+  const int64_t step = (int64_t)gridDim.x * 4;
+  for (int64_t t = (int64_t)blockIdx.x * 4 + w; t < a.tokens; t += step) {
+    const int64_t r = b * a.tokens + t;
+    uint4 x0[CH], x1[CH];
+#pragma unroll
+    for (int j = 0; j < CH; ++j) x0[j] = *(const uint4*)(a.x0 + r * C + j * 512 + lane * 8);
+    if (NT == 2) {
+#pragma unroll
+      for (int j = 0; j < CH; ++j) x1[j] = *(const uint4*)(a.x1 + r * C + j * 512 + lane * 8);
+    }
+    if (BIAS) {
+#pragma unroll
+      for (int j = 0; j < CH; ++j) {
+        x0[j] = add_bias8(x0[j], B0, j * 512 + lane * 8);
+        if (NT == 2) x1[j] = add_bias8(x1[j], B1, j * 512 + lane * 8);
+      }
+    }
+    const float inv0 = row_inv<CH>(x0, a.eps);
+    const float inv1 = NT == 2 ? row_inv<CH>(x1, a.eps) : 0.0f;
+    const int64_t cbase = b * a.c_sb + t * a.c_st + hd0;
+    const int64_t sbase = b * a.s_sb + t * a.s_st + hd0;
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
+      const int c0 = j * 512 + lane * 8;
       const int64_t head = j * 4 + (lane >> 4);
-      load8(a.cos, a.cs_dt, b * a.c_sb + head * a.c_sh + t * a.c_st + hd0, 1, a.cs_vec, cs[j]);
-      load8(a.sin, a.cs_dt, b * a.s_sb + head * a.s_sh + t * a.s_st + hd0, 1, a.cs_vec, sn[j]);
-    }
-
-    uint4 nv[CH];
-    norm_row<CH, BIAS>(a.x0, a.w0, a.w_dt, a.b0, a.b_dt, r, a.cols, a.eps, lane, nv);
-    rope_row<CH>(nv, cs, sn, second, cs_bf, a.o0 + r * a.out_stride, lane);
-    if (NT == 2) {
-      norm_row<CH, BIAS>(a.x1, a.w1, a.w_dt, a.b1, a.b_dt, r, a.cols, a.eps, lane, nv);
-      rope_row<CH>(nv, cs, sn, second, cs_bf, a.o1 + r * a.out_stride, lane);
-    }
-    if (PACK) {
-#pragma unroll
-      for (int j = 0; j < CH; ++j)
-        *(uint4*)(a.ov + r * a.out_stride + j * 512 + lane * 8) =
-            *(const uint4*)(a.v + r * a.cols + j * 512 + lane * 8);
+      float cs[8], sn[8];
+      load8_t<CDT, VEC>(a.cos, cbase + head * a.c_sh, 1, cs);
+      load8_t<CDT, VEC>(a.sin, sbase + head * a.s_sh, 1, sn);
+      *(uint4*)(a.o0 + r * a.out_stride + c0) = rope8(norm8(x0[j], W0, c0, inv0), cs, sn, second, cs_bf);
+      if (NT == 2)
+        *(uint4*)(a.o1 + r * a.out_stride + c0) = rope8(norm8(x1[j], W1, c0, inv1), cs, sn, second, cs_bf);
+      if (PACK) *(uint4*)(a.ov + r * a.out_stride + c0) = *(const uint4*)(a.v + r * C + c0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 }
 
 template <int NT, bool BIAS, bool PACK>
-static int launch_rope(RopeArgs& a, hipStream_t st) {
-  if (a.rows == 0) return OGA_OK;
+static int launch_rope(RopeArgs& a, int64_t batch, hipStream_t st) {
+  if (batch == 0 || a.tokens == 0) return OGA_OK;
+  if (batch > 65535) return unsupported("batch > 65535");
   const int64_t target_waves = (int64_t)cu_count() * 16;
-  int64_t rpw = (a.rows + target_waves - 1) / target_waves;
-  a.rows_per_wave = (int)(rpw < 1 ? 1 : (rpw > 64 ? 64 : rpw));
-  const int64_t waves = (a.rows + a.rows_per_wave - 1) / a.rows_per_wave;
-  const dim3 grid((unsigned)((waves + 3) / 4));
-  if (a.cols == 4096)
-    hipLaunchKernelGGL((k_rmsnorm_rope<8, NT, BIAS, PACK>), grid, dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL((k_rmsnorm_rope<4, NT, BIAS, PACK>), grid, dim3(256), 0, st, a);
+  int64_t per_batch = ((target_waves + batch - 1) / batch + 3) / 4;
+  const int64_t need = (a.tokens + 3) / 4;
+  if (per_batch > need) per_batch = need;
+  if (per_batch < 1) per_batch = 1;
+  const dim3 grid((unsigned)per_batch, (unsigned)batch);
+  if (a.cols == 4096) {
+    if (a.cs_dt == OGA_DT_BF16) {
+      if (a.cs_vec)
+        hipLaunchKernelGGL((k_rmsnorm_rope<8, NT, BIAS, PACK, OGA_DT_BF16, true>), grid, dim3(256), 0, st, a);
+      else
+        hipLaunchKernelGGL((k_rmsnorm_rope<8, NT, BIAS, PACK, OGA_DT_BF16, false>), grid, dim3(256), 0, st, a);
+    } else {
+      if (a.cs_vec)
+        hipLaunchKernelGGL((k_rmsnorm_rope<8, NT, BIAS, PACK, OGA_DT_F32, true>), grid, dim3(256), 0, st, a);
+      else
+        hipLaunchKernelGGL((k_rmsnorm_rope<8, NT, BIAS, PACK, OGA_DT_F32, false>), grid, dim3(256), 0, st, a);
+    }
+  } else {
+    if (a.cs_dt == OGA_DT_BF16) {
+      if (a.cs_vec)
+        hipLaunchKernelGGL((k_rmsnorm_rope<4, NT, BIAS, PACK, OGA_DT_BF16, true>), grid, dim3(256), 0, st, a);
+      else
+        hipLaunchKernelGGL((k_rmsnorm_rope<4, NT, BIAS, PACK, OGA_DT_BF16, false>), grid, dim3(256), 0, st, a);
+    } else {
+      if (a.cs_vec)
+        hipLaunchKernelGGL((k_rmsnorm_rope<4, NT, BIAS, PACK, OGA_DT_F32, true>), grid, dim3(256), 0, st, a);
+      else
+        hipLaunchKernelGGL((k_rmsnorm_rope<4, NT, BIAS, PACK, OGA_DT_F32, false>), grid, dim3(256), 0, st, a);
+    }
+  }
   return launch_status();
 }
 
@@ -187,7 +258,6 @@ static int rope_common(RopeArgs& a, const void* x0, const void* x1, const void* 
   a.s_sh = sst[1];
   a.s_st = sst[2];
   a.cs_vec = vec8_ok(cos, cs_dt, a.c_sb, a.c_sh, a.c_st, 1) && vec8_ok(sin, cs_dt, a.s_sb, a.s_sh, a.s_st, 1);
-  a.rows = batch * tokens;
   a.tokens = tokens;
   a.cols = (int)cols;
   a.out_stride = cols;
@@ -212,7 +282,7 @@ extern "C" int oga_video_qk_rmsnorm_rope(const void* q, const void* k, const voi
   if (!aligned(q_out, 16) || !aligned(k_out, 16)) return fail("outputs must be 16-byte aligned");
   a.o0 = (uint16_t*)q_out;
   a.o1 = (uint16_t*)k_out;
-  return launch_rope<2, false, false>(a, (hipStream_t)stream);
+  return launch_rope<2, false, false>(a, batch, (hipStream_t)stream);
 }
 
 extern "C" int oga_video_rmsnorm_rope(const void* x, const void* weight, int weight_dtype, const void* cos,
@@ -226,7 +296,7 @@ extern "C" int oga_video_rmsnorm_rope(const void* x, const void* weight, int wei
   if (rc) return rc;
   if (!aligned(out, 16)) return fail("output must be 16-byte aligned");
   a.o0 = (uint16_t*)out;
-  return launch_rope<1, false, false>(a, (hipStream_t)stream);
+  return launch_rope<1, false, false>(a, batch, (hipStream_t)stream);
 }
 
 extern "C" int oga_video_qk_bias_rmsnorm_rope(const void* q, const void* k, const void* q_bias, const void* k_bias,
@@ -249,7 +319,7 @@ extern "C" int oga_video_qk_bias_rmsnorm_rope(const void* q, const void* k, cons
   a.b_dt = bias_dtype;
   a.o0 = (uint16_t*)q_out;
   a.o1 = (uint16_t*)k_out;
-  return launch_rope<2, true, false>(a, (hipStream_t)stream);
+  return launch_rope<2, true, false>(a, batch, (hipStream_t)stream);
 }
 
 extern "C" int oga_video_qkv_rmsnorm_rope_pack(const void* q, const void* k, const void* v, const void* q_weight,
@@ -269,5 +339,5 @@ extern "C" int oga_video_qkv_rmsnorm_rope_pack(const void* q, const void* k, con
   a.o1 = (uint16_t*)qkv_out + cols;
   a.ov = (uint16_t*)qkv_out + 2 * cols;
   a.out_stride = 3 * cols;
-  return launch_rope<2, false, true>(a, (hipStream_t)stream);
+  return launch_rope<2, false, true>(a, batch, (hipStream_t)stream);
 }

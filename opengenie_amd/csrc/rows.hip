@@ -62,220 +62,206 @@ OGA_DEVICE void ada_value8(const AdaSrc& s, const float* tabv, int64_t b, int64_
 
 OGA_DEVICE int64_t wave_id() { return (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); }
 
-// ------------------------------------------------------------------ AdaZero
-struct AdaZeroArgs {
-  const uint16_t* x;
-  uint16_t* y;
-  int64_t rows, tokens;
-  int cols;
-  float eps;
-  int rows_per_wave;
-  AdaSrc shift, scale;
-};
+// ------------------------------------------------------------- row kernel
+// One kernel family for AdaZero and the Ada-gated elementwise ops:
+//   ADAZERO:    y = R( R?(n * R?(1 + scale)) + shift ),  n = R(x * inv_rms)
+//   ADALN:      y = R( R?(x * R?(1 + scale)) + shift )
+//   MUL:        y = R( x * gate )
+//   RESID:      y = R( x + R?(y_in * gate) )
+//   RESID_BIAS: y = R( x + R?(R(y_in + R(bias)) * gate) )
+// R? rounds iff the Ada values are bf16 (torch: bf16 op bf16 -> bf16).
+// s0 is the shift (ADAZERO/ADALN) or the gate; s1 the scale.
+//
+// Grid (blocks_per_batch, batch): a workgroup of 4 waves owns tokens of one
+// batch. It first stages the per-column constants in LDS -- the finished Ada
+// values when the timestep row is shared by all tokens (UNIFORM), otherwise
+// the (rounded) table rows -- plus the rounded bias, then each wave streams
+// token rows: 8 (or 4) 128-bit loads per tensor row, constants read back
+// from LDS 8 columns at a time.
+enum RowOp { OP_ADAZERO = 0, OP_ADALN = 1, OP_MUL = 2, OP_RESID = 3, OP_RESID_BIAS = 4 };
 
-// y = R( R?( n * R?(1 + scale) ) + shift ),  n = R(x * inv_rms)
-// R? rounds iff the scale values are bf16 (torch: bf16 * bf16 -> bf16).
-template <int CH, bool UNIFORM>
-__global__ __launch_bounds__(256) void k_adazero(AdaZeroArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int64_t r0 = wave_id() * a.rows_per_wave;
-  if (r0 >= a.rows) return;
-  const int64_t r1 = min(r0 + (int64_t)a.rows_per_wave, a.rows);
-  const bool scale_bf = a.scale.ts_dt == OGA_DT_BF16;
-
-  // UNIFORM: c0 = shift, c1 = R?(1 + scale), finished per column for batch cb.
-  // Otherwise: c0/c1 hold the table parts of shift/scale.
-  float c0[CH][8], c1[CH][8];
-  int64_t cb = -1;
-  if (!UNIFORM) {
-#pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      ada_table8(a.shift, j * 512 + lane * 8, c0[j]);
-      ada_table8(a.scale, j * 512 + lane * 8, c1[j]);
-    }
-  }
-
-  for (int64_t r = r0; r < r1; ++r) {
-    const int64_t b = r / a.tokens;
-    const int64_t t = r - b * a.tokens;
-    uint4 xv[CH];
-#pragma unroll
-    for (int j = 0; j < CH; ++j) xv[j] = *(const uint4*)(a.x + r * a.cols + j * 512 + lane * 8);
-
-    if (UNIFORM && b != cb) {
-#pragma unroll
-      for (int j = 0; j < CH; ++j) {
-        float tab[8];
-        const int col0 = j * 512 + lane * 8;
-        ada_table8(a.shift, col0, tab);
-        ada_value8(a.shift, tab, b, 0, col0, c0[j]);
-        ada_table8(a.scale, col0, tab);
-        ada_value8(a.scale, tab, b, 0, col0, c1[j]);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          float f = 1.0f + c1[j][i];
-          c1[j][i] = scale_bf ? rbf(f) : f;
-        }
-      }
-      cb = b;
-    }
-
-    double ss = 0.0;
-    float xf[CH][8];
-#pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      unpack8(xv[j], xf[j]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const double d = (double)xf[j][i];
-        ss = fma(d, d, ss);
-      }
-    }
-    const float inv = rms_inv(ss, a.cols, a.eps);
-
-#pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      const int col0 = j * 512 + lane * 8;
-      float sh[8], f[8];
-      if (UNIFORM) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) { sh[i] = c0[j][i]; f[i] = c1[j][i]; }
-      } else {
-        ada_value8(a.shift, c0[j], b, t, col0, sh);
-        ada_value8(a.scale, c1[j], b, t, col0, f);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float v = 1.0f + f[i];
-          f[i] = scale_bf ? rbf(v) : v;
-        }
-      }
-      float o[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float n = rbf(xf[j][i] * inv);
-        float p = n * f[i];
-        if (scale_bf) p = rbf(p);
-        o[i] = p + sh[i];
-      }
-      *(uint4*)(a.y + r * a.cols + col0) = pack8(o);
-    }
-  }
-}
-
-// ---------------------------------------------------- Ada-gated elementwise
-enum EwOp { EW_ADALN = 0, EW_MUL = 1, EW_RESID = 2, EW_RESID_BIAS = 3 };
-
-struct EwArgs {
+struct RowArgs {
   const uint16_t* x;
   const uint16_t* y;
   uint16_t* out;
   const void* bias;
   int bias_dt;
-  int64_t rows, tokens;
+  int64_t tokens;
   int cols;
-  int rows_per_wave;
-  AdaSrc s0;  // shift (ADALN) or gate
-  AdaSrc s1;  // scale (ADALN only)
+  float eps;
+  AdaSrc s0, s1;
 };
 
-// ADALN:      out = R( R?(x * R?(1 + scale)) + shift )
-// MUL:        out = R( x * gate )
-// RESID:      out = R( x + R?(y * gate) )
-// RESID_BIAS: out = R( x + R?(R(y + R(bias)) * gate) )
-// R? rounds iff the Ada values are bf16.
-template <int CH, int OP, bool UNIFORM>
-__global__ __launch_bounds__(256) void k_ada_ew(EwArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int64_t r0 = wave_id() * a.rows_per_wave;
-  if (r0 >= a.rows) return;
-  const int64_t r1 = min(r0 + (int64_t)a.rows_per_wave, a.rows);
-  const bool v_bf = a.s0.ts_dt == OGA_DT_BF16;
-  const bool f_bf = a.s1.ts_dt == OGA_DT_BF16;
+template <int OP>
+struct RowTraits {
+  static constexpr bool kTwo = OP == OP_ADAZERO || OP == OP_ADALN;  // uses s1
+  static constexpr bool kY = OP == OP_RESID || OP == OP_RESID_BIAS;
+  static constexpr bool kBias = OP == OP_RESID_BIAS;
+};
 
-  // UNIFORM: c0/c1 are finished values (gate, or shift and R?(1+scale)).
-  // Otherwise: table parts.
-  float c0[CH][8], c1[CH][8], bi[CH][8];
-  int64_t cb = -1;
+OGA_DEVICE void lds_store8(float* s, int col0, const float* v) {
+  *(float4*)(s + col0) = make_float4(v[0], v[1], v[2], v[3]);
+  *(float4*)(s + col0 + 4) = make_float4(v[4], v[5], v[6], v[7]);
+}
+OGA_DEVICE void lds_load8(const float* s, int col0, float* v) {
+  const float4 a = *(const float4*)(s + col0);
+  const float4 b = *(const float4*)(s + col0 + 4);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+template <int CH, int OP, bool UNIFORM, int D0, int D1, bool VEC>
+__global__ __launch_bounds__(256) void k_row(RowArgs a) {
+  using Tr = RowTraits<OP>;
+  constexpr int C = CH * 512;
+  // torch dtypes of the two Ada values (s0: shift or gate, s1: scale); a
+  // product with a bf16 value is bf16, with a float32 value float32.
+  constexpr bool B0 = D0 == OGA_DT_BF16;
+  constexpr bool B1 = D1 == OGA_DT_BF16;
+  __shared__ float L0[C];
+  __shared__ float L1[Tr::kTwo ? C : 1];
+  __shared__ float LB[Tr::kBias ? C : 1];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t b = blockIdx.y;
+  const int64_t step = (int64_t)gridDim.x * 4;
+  int64_t t = (int64_t)blockIdx.x * 4 + w;
+
+  // The first row's loads go out before the staging so their latency
+  // overlaps it.
+  uint4 xv[CH], yv[CH];
+  if (t < a.tokens) {
+    const int64_t r = b * a.tokens + t;
 #pragma unroll
-  for (int j = 0; j < CH; ++j) {
-    const int col0 = j * 512 + lane * 8;
-    if (!UNIFORM) {
-      ada_table8(a.s0, col0, c0[j]);
-      if (OP == EW_ADALN) ada_table8(a.s1, col0, c1[j]);
-    }
-    if (OP == EW_RESID_BIAS) {
-      load8(a.bias, a.bias_dt, col0, 1, true, bi[j]);
+    for (int j = 0; j < CH; ++j) xv[j] = *(const uint4*)(a.x + r * C + j * 512 + lane * 8);
+    if (Tr::kY) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) bi[j][i] = rbf(bi[j][i]);
+      for (int j = 0; j < CH; ++j) yv[j] = *(const uint4*)(a.y + r * C + j * 512 + lane * 8);
     }
   }
 
-  for (int64_t r = r0; r < r1; ++r) {
-    const int64_t b = r / a.tokens;
-    const int64_t t = r - b * a.tokens;
-    uint4 xv[CH], yv[CH];
-#pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      xv[j] = *(const uint4*)(a.x + r * a.cols + j * 512 + lane * 8);
-      if (OP == EW_RESID || OP == EW_RESID_BIAS) yv[j] = *(const uint4*)(a.y + r * a.cols + j * 512 + lane * 8);
+  // Stage per-column constants.
+#pragma unroll 1
+  for (int c0 = tid * 8; c0 < C; c0 += 256 * 8) {
+    float t[8], v[8];
+    ada_table8(a.s0, c0, t);
+    if (UNIFORM) {
+      ada_value8(a.s0, t, b, 0, c0, v);
+      lds_store8(L0, c0, v);
+    } else {
+      lds_store8(L0, c0, t);
     }
-    if (UNIFORM && b != cb) {
+    if (Tr::kTwo) {
+      ada_table8(a.s1, c0, t);
+      if (UNIFORM) {
+        ada_value8(a.s1, t, b, 0, c0, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float f = 1.0f + v[i];
+          v[i] = B1 ? rbf(f) : f;
+        }
+        lds_store8(L1, c0, v);
+      } else {
+        lds_store8(L1, c0, t);
+      }
+    }
+    if (Tr::kBias) {
+      load8(a.bias, a.bias_dt, c0, 1, true, v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = rbf(v[i]);
+      lds_store8(LB, c0, v);
+    }
+  }
+  __syncthreads();
+
+  const bool tab0 = a.s0.tab != nullptr;
+  const bool tab1 = a.s1.tab != nullptr;
+  for (bool first = true; t < a.tokens; t += step, first = false) {
+    const int64_t r = b * a.tokens + t;
+    uint16_t* outr = a.out + r * C + lane * 8;
+    const int64_t ts0 = a.s0.ts_off + b * a.s0.ts_sb + t * a.s0.ts_st;
+    const int64_t ts1 = a.s1.ts_off + b * a.s1.ts_sb + t * a.s1.ts_st;
+    if (!first) {
+#pragma unroll
+      for (int j = 0; j < CH; ++j) xv[j] = *(const uint4*)(a.x + r * C + j * 512 + lane * 8);
+      if (Tr::kY) {
+#pragma unroll
+        for (int j = 0; j < CH; ++j) yv[j] = *(const uint4*)(a.y + r * C + j * 512 + lane * 8);
+      }
+    }
+
+    float inv = 1.0f;
+    if (OP == OP_ADAZERO) {
+      double ss[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
       for (int j = 0; j < CH; ++j) {
-        float tab[8];
-        const int col0 = j * 512 + lane * 8;
-        ada_table8(a.s0, col0, tab);
-        ada_value8(a.s0, tab, b, 0, col0, c0[j]);
-        if (OP == EW_ADALN) {
-          ada_table8(a.s1, col0, tab);
-          ada_value8(a.s1, tab, b, 0, col0, c1[j]);
+        float f[8];
+        unpack8(xv[j], f);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const float f = 1.0f + c1[j][i];
-            c1[j][i] = f_bf ? rbf(f) : f;
-          }
+        for (int i = 0; i < 8; ++i) {
+          const double d = (double)f[i];
+          ss[i & 3] = fma(d, d, ss[i & 3]);
         }
       }
-      cb = b;
+      inv = rms_inv((ss[0] + ss[1]) + (ss[2] + ss[3]), C, a.eps);
     }
+
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       const int col0 = j * 512 + lane * 8;
-      float g[8], f[8];
-      if (UNIFORM) {
+      float v0[8], v1[8], xf[8], o[8];
+      lds_load8(L0, col0, v0);
+      if (Tr::kTwo) lds_load8(L1, col0, v1);
+      if (!UNIFORM) {
+        float tsv[8];
+        load8_t<D0, VEC>(a.s0.ts, ts0 + (int64_t)col0 * a.s0.ts_sc, a.s0.ts_sc, tsv);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) { g[i] = c0[j][i]; f[i] = c1[j][i]; }
-      } else {
-        ada_value8(a.s0, c0[j], b, t, col0, g);
-        if (OP == EW_ADALN) {
-          ada_value8(a.s1, c1[j], b, t, col0, f);
+        for (int i = 0; i < 8; ++i) {
+          float s = tab0 ? v0[i] + tsv[i] : tsv[i];
+          v0[i] = (tab0 && B0) ? rbf(s) : s;
+        }
+        if (Tr::kTwo) {
+          load8_t<D1, VEC>(a.s1.ts, ts1 + (int64_t)col0 * a.s1.ts_sc, a.s1.ts_sc, tsv);
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            const float v = 1.0f + f[i];
-            f[i] = f_bf ? rbf(v) : v;
+            float s = tab1 ? v1[i] + tsv[i] : tsv[i];
+            if (tab1 && B1) s = rbf(s);
+            const float f = 1.0f + s;
+            v1[i] = B1 ? rbf(f) : f;
           }
         }
       }
-      float xf[8], yf[8], o[8];
       unpack8(xv[j], xf);
-      if (OP == EW_RESID || OP == EW_RESID_BIAS) unpack8(yv[j], yf);
+      if (OP == OP_ADAZERO || OP == OP_ADALN) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if (OP == EW_ADALN) {
-          float p = xf[i] * f[i];
-          if (f_bf) p = rbf(p);
-          o[i] = p + g[i];
-        } else if (OP == EW_MUL) {
-          o[i] = xf[i] * g[i];
-        } else {
+        for (int i = 0; i < 8; ++i) {
+          const float n = OP == OP_ADAZERO ? rbf(xf[i] * inv) : xf[i];
+          float p = n * v1[i];
+          if (B1) p = rbf(p);
+          o[i] = p + v0[i];
+        }
+      } else if (OP == OP_MUL) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = xf[i] * v0[i];
+      } else {
+        float yf[8], bb[8];
+        unpack8(yv[j], yf);
+        if (Tr::kBias) lds_load8(LB, col0, bb);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
           float yy = yf[i];
-          if (OP == EW_RESID_BIAS) yy = rbf(yy + bi[j][i]);
-          float p = yy * g[i];
-          if (v_bf) p = rbf(p);
+          if (Tr::kBias) yy = rbf(yy + bb[i]);
+          float p = yy * v0[i];
+          if (B0) p = rbf(p);
           o[i] = xf[i] + p;
         }
       }
-      *(uint4*)(a.out + r * a.cols + col0) = pack8(o);
+      *(uint4*)(outr + j * 512) = pack8(o);
+      // Keep each vector step's constants live only within the step: the
+      // occupancy this buys hides the LDS latency better than hoisting.
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 }
@@ -372,54 +358,58 @@ static void make_direct_src(AdaSrc& s, const void* p, int dt, const int64_t* st3
   s.ts_vec = vec8_ok(p, dt, 0, s.ts_sb, s.ts_st, s.ts_sc);
 }
 
-// Rows per wave: one row per wave until every SIMD holds four waves; beyond
-// that a wave takes several rows, which amortises the per-column constants.
-static int rows_per_wave_for(int64_t rows) {
-  const int64_t target_waves = (int64_t)cu_count() * 4 * 4;
-  int64_t rpw = (rows + target_waves - 1) / target_waves;
-  if (rpw < 1) rpw = 1;
-  if (rpw > 64) rpw = 64;
-  return (int)rpw;
+// Grid: enough 4-wave workgroups per batch that the whole launch holds about
+// four waves per SIMD (capped by the token count); each wave then strides
+// over its batch's tokens.
+static dim3 row_grid(int64_t batch, int64_t tokens) {
+  const int64_t target_waves = (int64_t)cu_count() * 16;
+  int64_t per_batch = (target_waves + batch - 1) / batch;
+  per_batch = (per_batch + 3) / 4;  // workgroups
+  const int64_t need = (tokens + 3) / 4;
+  if (per_batch > need) per_batch = need;
+  if (per_batch < 1) per_batch = 1;
+  return dim3((unsigned)per_batch, (unsigned)batch);
 }
 
-static dim3 row_grid(int64_t rows, int rpw) {
-  const int64_t waves = (rows + rpw - 1) / rpw;
-  return dim3((unsigned)((waves + 3) / 4));
-}
-
-template <int CH>
-static int launch_adazero(AdaZeroArgs& a, bool uniform, hipStream_t st) {
-  const dim3 grid = row_grid(a.rows, a.rows_per_wave);
-  if (uniform)
-    hipLaunchKernelGGL((k_adazero<CH, true>), grid, dim3(256), 0, st, a);
+template <int CH, int OP, bool UNIFORM, int D0, int D1>
+static void launch_row_v(RowArgs& a, int64_t batch, bool vec, hipStream_t st) {
+  const dim3 grid = row_grid(batch, a.tokens);
+  if (vec)
+    hipLaunchKernelGGL((k_row<CH, OP, UNIFORM, D0, D1, true>), grid, dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL((k_adazero<CH, false>), grid, dim3(256), 0, st, a);
-  return launch_status();
+    hipLaunchKernelGGL((k_row<CH, OP, UNIFORM, D0, D1, false>), grid, dim3(256), 0, st, a);
 }
 
-static int run_adazero(AdaZeroArgs& a, hipStream_t st) {
-  if (a.rows == 0) return OGA_OK;
-  a.rows_per_wave = rows_per_wave_for(a.rows);
-  const bool uniform = a.shift.ts_st == 0 && a.scale.ts_st == 0;
-  return a.cols == 4096 ? launch_adazero<8>(a, uniform, st) : launch_adazero<4>(a, uniform, st);
+template <int CH, int OP, bool UNIFORM>
+static int launch_row_u(RowArgs& a, int64_t batch, bool vec, hipStream_t st) {
+  const int d0 = a.s0.ts_dt, d1 = a.s1.ts_dt;
+  if (d0 == OGA_DT_BF16 && d1 == OGA_DT_BF16)
+    launch_row_v<CH, OP, UNIFORM, OGA_DT_BF16, OGA_DT_BF16>(a, batch, vec, st);
+  else if (d0 == OGA_DT_F32 && d1 == OGA_DT_F32)
+    launch_row_v<CH, OP, UNIFORM, OGA_DT_F32, OGA_DT_F32>(a, batch, vec, st);
+  else if (OP == OP_ADAZERO && d0 == OGA_DT_BF16)
+    launch_row_v<CH, OP_ADAZERO, UNIFORM, OGA_DT_BF16, OGA_DT_F32>(a, batch, vec, st);
+  else if (OP == OP_ADAZERO)
+    launch_row_v<CH, OP_ADAZERO, UNIFORM, OGA_DT_F32, OGA_DT_BF16>(a, batch, vec, st);
+  else
+    return unsupported("Ada values of different dtypes");
+  return launch_status();
 }
 
 template <int CH, int OP>
-static int launch_ew_ch(EwArgs& a, bool uniform, hipStream_t st) {
-  const dim3 grid = row_grid(a.rows, a.rows_per_wave);
-  if (uniform)
-    hipLaunchKernelGGL((k_ada_ew<CH, OP, true>), grid, dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL((k_ada_ew<CH, OP, false>), grid, dim3(256), 0, st, a);
-  return launch_status();
+static int launch_row_ch(RowArgs& a, int64_t batch, bool uniform, bool vec, hipStream_t st) {
+  return uniform ? launch_row_u<CH, OP, true>(a, batch, vec, st) : launch_row_u<CH, OP, false>(a, batch, vec, st);
 }
 
 template <int OP>
-static int run_ew(EwArgs& a, hipStream_t st) {
-  if (a.rows == 0) return OGA_OK;
-  a.rows_per_wave = rows_per_wave_for(a.rows);
-  const bool uniform = a.s0.ts_st == 0 && (OP != EW_ADALN || a.s1.ts_st == 0);
-  return a.cols == 4096 ? launch_ew_ch<8, OP>(a, uniform, st) : launch_ew_ch<4, OP>(a, uniform, st);
+static int run_row(RowArgs& a, int64_t batch, hipStream_t st) {
+  if (batch == 0 || a.tokens == 0) return OGA_OK;
+  if (batch > 65535) return unsupported("batch > 65535");
+  constexpr bool two = RowTraits<OP>::kTwo;
+  const bool uniform = a.s0.ts_st == 0 && (!two || a.s1.ts_st == 0);
+  const bool vec = a.s0.ts_vec && (!two || a.s1.ts_vec);
+  return a.cols == 4096 ? launch_row_ch<8, OP>(a, batch, uniform, vec, st)
+                        : launch_row_ch<4, OP>(a, batch, uniform, vec, st);
 }
 
 static int check_rows(const void* x, const void* y, int64_t batch, int64_t tokens, int64_t cols) {
@@ -433,92 +423,81 @@ static int check_rows(const void* x, const void* y, int64_t batch, int64_t token
 
 using namespace oga;
 
-extern "C" int oga_adazero_from_ada(const void* x, void* y, int64_t batch, int64_t tokens, int64_t cols,
-                                    const void* table, int table_dtype, int64_t tab_s0, int64_t tab_s1,
-                                    const void* timestep, int ts_dtype, const int64_t ts_strides[4],
-                                    int shift_index, int scale_index, float eps, void* stream) {
-  int rc = check_rows(x, y, batch, tokens, cols);
-  if (rc) return rc;
-  AdaZeroArgs a{};
-  a.x = (const uint16_t*)x;
-  a.y = (uint16_t*)y;
-  a.rows = batch * tokens;
-  a.tokens = tokens;
-  a.cols = (int)cols;
-  a.eps = eps;
-  const int64_t params = INT64_MAX;
-  if ((rc = make_ada_src(a.shift, table, table_dtype, tab_s0, tab_s1, timestep, ts_dtype, ts_strides, shift_index, params))) return rc;
-  if ((rc = make_ada_src(a.scale, table, table_dtype, tab_s0, tab_s1, timestep, ts_dtype, ts_strides, scale_index, params))) return rc;
-  return run_adazero(a, (hipStream_t)stream);
-}
-
-extern "C" int oga_adazero(const void* x, void* y, int64_t batch, int64_t tokens, int64_t cols, const void* scale,
-                           int scale_dtype, const int64_t scale_strides[3], const void* shift, int shift_dtype,
-                           const int64_t shift_strides[3], float eps, void* stream) {
-  int rc = check_rows(x, y, batch, tokens, cols);
-  if (rc) return rc;
-  if (!scale || !shift || !scale_strides || !shift_strides) return fail("null scale/shift");
-  if (!dt_ok(scale_dtype) || !dt_ok(shift_dtype)) return fail("scale/shift dtype must be bf16 or f32");
-  AdaZeroArgs a{};
-  a.x = (const uint16_t*)x;
-  a.y = (uint16_t*)y;
-  a.rows = batch * tokens;
-  a.tokens = tokens;
-  a.cols = (int)cols;
-  a.eps = eps;
-  make_direct_src(a.shift, shift, shift_dtype, shift_strides);
-  make_direct_src(a.scale, scale, scale_dtype, scale_strides);
-  return run_adazero(a, (hipStream_t)stream);
-}
-
-static int ew_common(EwArgs& a, const void* x, const void* y, void* out, int64_t batch, int64_t tokens, int64_t cols) {
+static int row_common(RowArgs& a, const void* x, const void* y, void* out, int64_t batch, int64_t tokens,
+                      int64_t cols) {
   int rc = check_rows(x, out, batch, tokens, cols);
   if (rc) return rc;
   if (y && !aligned(y, 16)) return fail("y must be 16-byte aligned");
   a.x = (const uint16_t*)x;
   a.y = (const uint16_t*)y;
   a.out = (uint16_t*)out;
-  a.rows = batch * tokens;
   a.tokens = tokens;
   a.cols = (int)cols;
   return OGA_OK;
+}
+
+extern "C" int oga_adazero_from_ada(const void* x, void* y, int64_t batch, int64_t tokens, int64_t cols,
+                                    const void* table, int table_dtype, int64_t tab_s0, int64_t tab_s1,
+                                    const void* timestep, int ts_dtype, const int64_t ts_strides[4],
+                                    int shift_index, int scale_index, float eps, void* stream) {
+  RowArgs a{};
+  int rc = row_common(a, x, nullptr, y, batch, tokens, cols);
+  if (rc) return rc;
+  a.eps = eps;
+  if ((rc = make_ada_src(a.s0, table, table_dtype, tab_s0, tab_s1, timestep, ts_dtype, ts_strides, shift_index, INT64_MAX))) return rc;
+  if ((rc = make_ada_src(a.s1, table, table_dtype, tab_s0, tab_s1, timestep, ts_dtype, ts_strides, scale_index, INT64_MAX))) return rc;
+  return run_row<OP_ADAZERO>(a, batch, (hipStream_t)stream);
+}
+
+extern "C" int oga_adazero(const void* x, void* y, int64_t batch, int64_t tokens, int64_t cols, const void* scale,
+                           int scale_dtype, const int64_t scale_strides[3], const void* shift, int shift_dtype,
+                           const int64_t shift_strides[3], float eps, void* stream) {
+  RowArgs a{};
+  int rc = row_common(a, x, nullptr, y, batch, tokens, cols);
+  if (rc) return rc;
+  if (!scale || !shift || !scale_strides || !shift_strides) return fail("null scale/shift");
+  if (!dt_ok(scale_dtype) || !dt_ok(shift_dtype)) return fail("scale/shift dtype must be bf16 or f32");
+  a.eps = eps;
+  make_direct_src(a.s0, shift, shift_dtype, shift_strides);
+  make_direct_src(a.s1, scale, scale_dtype, scale_strides);
+  return run_row<OP_ADAZERO>(a, batch, (hipStream_t)stream);
 }
 
 extern "C" int oga_adaln_affine_from_ada(const void* x, void* y, int64_t batch, int64_t tokens, int64_t cols,
                                          const void* table, int table_dtype, int64_t tab_s0, int64_t tab_s1,
                                          const void* timestep, int ts_dtype, const int64_t ts_strides[4],
                                          int shift_index, int scale_index, void* stream) {
-  EwArgs a{};
-  int rc = ew_common(a, x, nullptr, y, batch, tokens, cols);
+  RowArgs a{};
+  int rc = row_common(a, x, nullptr, y, batch, tokens, cols);
   if (rc) return rc;
   if ((rc = make_ada_src(a.s0, table, table_dtype, tab_s0, tab_s1, timestep, ts_dtype, ts_strides, shift_index, INT64_MAX))) return rc;
   if ((rc = make_ada_src(a.s1, table, table_dtype, tab_s0, tab_s1, timestep, ts_dtype, ts_strides, scale_index, INT64_MAX))) return rc;
-  return run_ew<EW_ADALN>(a, (hipStream_t)stream);
+  return run_row<OP_ADALN>(a, batch, (hipStream_t)stream);
 }
 
 extern "C" int oga_mul_from_ada(const void* x, void* y, int64_t batch, int64_t tokens, int64_t cols,
                                 const void* table, int table_dtype, int64_t tab_s0, int64_t tab_s1,
                                 const void* timestep, int ts_dtype, const int64_t ts_strides[4], int gate_index,
                                 void* stream) {
-  EwArgs a{};
-  int rc = ew_common(a, x, nullptr, y, batch, tokens, cols);
+  RowArgs a{};
+  int rc = row_common(a, x, nullptr, y, batch, tokens, cols);
   if (rc) return rc;
   if ((rc = make_ada_src(a.s0, table, table_dtype, tab_s0, tab_s1, timestep, ts_dtype, ts_strides, gate_index, INT64_MAX))) return rc;
   a.s1 = a.s0;
-  return run_ew<EW_MUL>(a, (hipStream_t)stream);
+  return run_row<OP_MUL>(a, batch, (hipStream_t)stream);
 }
 
 extern "C" int oga_residual_gate_from_ada(const void* x, const void* y, void* out, int64_t batch, int64_t tokens,
                                           int64_t cols, const void* table, int table_dtype, int64_t tab_s0,
                                           int64_t tab_s1, const void* timestep, int ts_dtype,
                                           const int64_t ts_strides[4], int gate_index, void* stream) {
-  EwArgs a{};
+  RowArgs a{};
   if (!y) return fail("null y");
-  int rc = ew_common(a, x, y, out, batch, tokens, cols);
+  int rc = row_common(a, x, y, out, batch, tokens, cols);
   if (rc) return rc;
   if ((rc = make_ada_src(a.s0, table, table_dtype, tab_s0, tab_s1, timestep, ts_dtype, ts_strides, gate_index, INT64_MAX))) return rc;
   a.s1 = a.s0;
-  return run_ew<EW_RESID>(a, (hipStream_t)stream);
+  return run_row<OP_RESID>(a, batch, (hipStream_t)stream);
 }
 
 extern "C" int oga_residual_gate_bias_from_ada(const void* x, const void* y, const void* bias, int bias_dtype,
@@ -526,28 +505,28 @@ extern "C" int oga_residual_gate_bias_from_ada(const void* x, const void* y, con
                                                const void* table, int table_dtype, int64_t tab_s0, int64_t tab_s1,
                                                const void* timestep, int ts_dtype, const int64_t ts_strides[4],
                                                int gate_index, void* stream) {
-  EwArgs a{};
+  RowArgs a{};
   if (!y || !bias) return fail("null y/bias");
   if (!dt_ok(bias_dtype)) return fail("bias dtype must be bf16 or f32");
   if (!aligned(bias, 32)) return fail("bias must be 32-byte aligned");
-  int rc = ew_common(a, x, y, out, batch, tokens, cols);
+  int rc = row_common(a, x, y, out, batch, tokens, cols);
   if (rc) return rc;
   a.bias = bias;
   a.bias_dt = bias_dtype;
   if ((rc = make_ada_src(a.s0, table, table_dtype, tab_s0, tab_s1, timestep, ts_dtype, ts_strides, gate_index, INT64_MAX))) return rc;
   a.s1 = a.s0;
-  return run_ew<EW_RESID_BIAS>(a, (hipStream_t)stream);
+  return run_row<OP_RESID_BIAS>(a, batch, (hipStream_t)stream);
 }
 
 extern "C" int oga_residual_gate_bf16(const void* x, const void* y, const void* gate, const int64_t gate_strides[3],
                                       void* out, int64_t batch, int64_t tokens, int64_t cols, void* stream) {
-  EwArgs a{};
+  RowArgs a{};
   if (!y || !gate || !gate_strides) return fail("null y/gate");
-  int rc = ew_common(a, x, y, out, batch, tokens, cols);
+  int rc = row_common(a, x, y, out, batch, tokens, cols);
   if (rc) return rc;
   make_direct_src(a.s0, gate, OGA_DT_BF16, gate_strides);
   a.s1 = a.s0;
-  return run_ew<EW_RESID>(a, (hipStream_t)stream);
+  return run_row<OP_RESID>(a, batch, (hipStream_t)stream);
 }
 
 extern "C" int oga_bias_add_bf16(const void* x, const void* bias, int bias_dtype, void* out, int64_t rows,
