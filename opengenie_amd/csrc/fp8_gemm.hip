@@ -7,19 +7,31 @@
 //   out = R(acc * (scale_a * scale_b));  out = R(out + R(bias))  (if bias)
 // acc is the float32 sum over k of a[m,k]*w[n,k] (each product exact).
 //
-// Tiling (gfx950): a 256x256 output tile per workgroup of 8 waves (two per
-// SIMD), each wave owning 128 (M) x 64 (N) as 8x4 blocks of
-// v_mfma_f32_16x16x128_f8f6f4 with its 128 accumulators in VGPRs.
-// K advances 128 bytes per step through a double-buffered LDS stage of
-// 2 x (256x128 A + 256x128 W) = 128 KiB, filled by LDS-DMA
-// (global_load_lds_dwordx4) so tiles never pass through VGPRs; the two
-// buffers are separate LDS objects so the DMA into one is known not to alias
-// the fragment reads of the other. Within a stage, row r's 16-byte
-// chunk c is stored at chunk position c ^ (r & 7), so the 128-bit fragment
-// reads of 8 consecutive rows hit 8 distinct bank groups.
+// Tiling (gfx950). A workgroup of 8 waves, two per SIMD, owns a 256 (M) x
+// 256 (N) output tile; wave (wm, wn) owns 128 (M) x 64 (N) of it as 2 x 4
+// blocks of v_mfma_f32_32x32x64_f8f6f4, whose 128 float32 accumulators per
+// lane live in the accumulation registers. K advances 64 bytes per step through a ring of
+// four LDS stages (4 x (256x64 A + 256x64 W) = 128 KiB) filled by LDS-DMA
+// (global_load_lds_dwordx4), so tiles never pass through VGPRs and three
+// steps of loads are in flight while one is consumed. Each stage is a
+// separate LDS object so the compiler can tell a DMA into one stage from the
+// fragment reads of another.
+//
+// Per step (software-pipelined): 4 MFMAs on fragments read during the
+// previous step, then one barrier that publishes the next stage and
+// releases the previous one, the DMA for three steps ahead into the released
+// stage, and 4 more MFMAs under which the next step's fragments are read.
+//
+// LDS layout of an operand stage (256 rows x 64 bytes): four rows share one
+// 256-byte line of the 64 LDS banks, row m's 16-byte chunk k0 sitting at
+//   (m / 4) * 256 + ((4 * (m % 4) + k0) ^ ((m / 4) % 16)) * 16,
+// which makes the 128-bit fragment reads (32 rows x 2 chunks per
+// instruction) and the 1 KiB DMA writes free of bank conflicts.
+//
 // The weight tile is the MFMA's A operand and the activation tile its B
-// operand, so each lane's 4 accumulator values are 4 consecutive output
-// columns of one row: the epilogue stores 8 bytes per lane.
+// operand, so each lane's accumulators hold 4 consecutive output columns of
+// one output row per group. The epilogue stages each wave's finished bf16
+// block in LDS and writes whole 128-byte rows, so HBM sees full lines.
 // Workgroups are numbered so that the eight XCDs (which receive workgroups
 // round-robin) each own a contiguous, M-grouped range of tiles.
 #include "common.h"
@@ -27,8 +39,17 @@
 
 namespace oga {
 
-constexpr int GM = 256, GN = 256, GK = 128;
+constexpr int GM = 256, GN = 256, GK = 64, NST = 4;
 constexpr int kGroupM = 8;
+constexpr int kStageU4 = GM * GK / 16;  // uint4 per operand stage (1024 = 16 KiB)
+constexpr int kWaves = 8;
+// Epilogue staging: each wave's 128 x 64 bf16 block in LDS with a padded row
+// pitch (128 + 16 bytes) so the 8-byte writes of 32 rows hit distinct banks.
+constexpr int kOutPitch = 144;
+constexpr int kOutWaveBytes = 128 * kOutPitch;
+constexpr int kLdsU4 = (NST * 2 * kStageU4 > kWaves * kOutWaveBytes / 16) ? NST * 2 * kStageU4
+                                                                          : kWaves * kOutWaveBytes / 16;
+constexpr int kDmaPerOp = GM / 16 / kWaves;  // 1 KiB DMA instructions per wave per operand per stage
 
 struct GemmArgs {
   const uint8_t* a;
@@ -46,68 +67,44 @@ struct GemmArgs {
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-OGA_DEVICE i32x8 lds_frag(const uint4* s, int row, int g) {
-  const int sw = row & 7;
-  const uint4 u0 = s[row * 8 + ((2 * g) ^ sw)];
-  const uint4 u1 = s[row * 8 + ((2 * g + 1) ^ sw)];
-  i32x8 r;
-  r[0] = (int)u0.x; r[1] = (int)u0.y; r[2] = (int)u0.z; r[3] = (int)u0.w;
-  r[4] = (int)u1.x; r[5] = (int)u1.y; r[6] = (int)u1.z; r[7] = (int)u1.w;
+// Byte offset in an operand stage of row m's 16-byte chunk k0.
+OGA_DEVICE int lds_pos(int m, int k0) { return (m >> 2) * 256 + (((m & 3) * 4 + k0) ^ ((m >> 2) & 15)) * 16; }
+
+// One 32-row MFMA operand fragment: lane l reads its row's logical chunks
+// 2h and 2h+1 (h = l / 32), at LDS byte addresses a0 + OFF and a1 + OFF.
+// The reads are issued as inline assembly so that the compiler, which does
+// not see them, adds no DMA-ordering waits of its own: the kernel orders LDS
+// explicitly (vmcnt before the barrier, lgkm_wait before the MFMAs).
+template <int OFF>
+OGA_DEVICE i32x8 frag(uint32_t a0, uint32_t a1) {
+  uint4 lo, hi;
+  asm volatile("ds_read_b128 %0, %2 offset:%4\n\tds_read_b128 %1, %3 offset:%4"
+               : "=v"(lo), "=v"(hi)
+               : "v"(a0), "v"(a1), "i"(OFF));
+  i32x8 r = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
   return r;
 }
 
-// Stage: 256 rows x 128 bytes of A and of W, written straight from global
-// memory into LDS (global_load_lds_dwordx4). One instruction fills 1 KiB of
-// LDS: lane p writes 16-byte slot base+p. Slot s holds row s/8, physical
-// chunk s%8 = logical chunk kc ^ (row & 7); so lane p of block b fetches row
-// 8b + p/8, logical chunk (p%8) ^ ((p/8)%8). Wave w fills blocks 4w..4w+3
-// of each operand.
-struct StagePtrs {
-  uint32_t a_off[4];
-  uint32_t w_off[4];
-};
+// s_waitcnt vmcnt(N) (expcnt/lgkmcnt left at their maxima); N < 64.
+#define OGA_WAIT_VM(N) __builtin_amdgcn_s_waitcnt(0x0F70 | ((N) & 15) | ((((N) >> 4) & 3) << 14))
+// s_waitcnt lgkmcnt(N) that also names the fragments it makes valid, so no
+// use of them can be scheduled before it; naming accumulators as well keeps
+// the MFMAs that update them from being scheduled after it.
+#define OGA_LGKM_WAIT(N, ...) asm volatile("s_waitcnt lgkmcnt(" #N ")" : __VA_ARGS__)
+// Workgroup barrier without the release fence of __syncthreads(), which
+// would drain every outstanding DMA (vmcnt(0)) and empty the prefetch ring.
+// Callers first wait for their own DMA group and LDS reads; the memory
+// clobber keeps the compiler from moving memory accesses across it.
+#define OGA_BARRIER() asm volatile("s_barrier" ::: "memory")
 
-OGA_DEVICE void stage_issue(const uint8_t* abase, const uint8_t* wbase, const StagePtrs& sp, uint32_t kofs,
-                            uint4* dA, uint4* dW, int wv) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int blk = wv * 4 + i;
-    __builtin_amdgcn_global_load_lds((const void*)(abase + (sp.a_off[i] + kofs)), (lds_void*)(dA + blk * 64), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((const void*)(wbase + (sp.w_off[i] + kofs)), (lds_void*)(dW + blk * 64), 16, 0, 0);
-  }
+OGA_DEVICE f32x16 mfma(const i32x8& w, const i32x8& a, const f32x16& c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w, a, c, 0, 0, 0, 0, 0, 0);
 }
 
-OGA_DEVICE void stage_compute(const uint4* sA, const uint4* sW, f32x4 (&acc)[8][4], int wm, int wn, int fr, int fg) {
-  i32x8 wf[4];
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb) wf[nb] = lds_frag(sW, wn * 64 + nb * 16 + fr, fg);
-#pragma unroll
-  for (int mb = 0; mb < 8; ++mb) {
-    const i32x8 af = lds_frag(sA, wm * 128 + mb * 16 + fr, fg);
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
-      acc[mb][nb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf[nb], af, acc[mb][nb], 0, 0, 0, 0, 0, 0);
-  }
-  // Schedule: the 8 weight-fragment reads and the first activation fragment,
-  // then for each block the next block's 2 fragment reads ahead of its 4
-  // MFMAs, so at most two activation fragments are live.
-  __builtin_amdgcn_sched_group_barrier(0x100, 10, 0);
-#pragma unroll
-  for (int mb = 0; mb < 7; ++mb) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-  }
-  __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-}
-
-// s_waitcnt vmcnt(0) (expcnt/lgkmcnt left at their maxima).
-OGA_DEVICE void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
-__global__ __launch_bounds__(512, 1) void k_fp8_gemm(GemmArgs g) {
-  __shared__ uint4 sA0[GM * GK / 16];
-  __shared__ uint4 sW0[GN * GK / 16];
-  __shared__ uint4 sA1[GM * GK / 16];
-  __shared__ uint4 sW1[GN * GK / 16];
+__global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2))) void k_fp8_gemm(
+    GemmArgs g) {
+  // Stage s: A tile at uint4 [2s*kStageU4, (2s+1)*kStageU4), W tile after it.
+  __shared__ uint4 smem[kLdsU4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -126,98 +123,206 @@ __global__ __launch_bounds__(512, 1) void k_fp8_gemm(GemmArgs g) {
   const int tn = (t % per_group) / gsize;
   const int64_t m0 = (int64_t)tm * GM, n0 = (int64_t)tn * GN;
 
-  // Per-lane byte offsets of the 8 rows this lane fetches per operand.
-  // Rows past the matrix edge re-read its last row (never stored).
-  StagePtrs sp;
-  {
-    const int pr = lane >> 3;
-    const int kc = (lane & 7) ^ (pr & 7);
+  // DMA: instruction i of this wave fills stage rows 16b .. 16b+15 of an
+  // operand (b = kDmaPerOp*wave + i), i.e. 1 KiB = LDS lines 4b .. 4b+3;
+  // lane p writes the 16 bytes at line 4b + p/16, chunk position p%16, which
+  // by the layout above hold row 4*(4b + p/16) + kc/4, chunk kc%4 with
+  // kc = (p%16) ^ ((4b + p/16) % 16). Rows past the matrix edge re-read
+  // its last row (their results are never stored). Offsets are bytes from
+  // the tile's first row.
+  uint32_t a_off[kDmaPerOp], w_off[kDmaPerOp];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = (wv * 4 + i) * 8 + pr;
-      const int64_t ar = min((int64_t)row, (int64_t)g.m - 1 - m0);
-      const int64_t wr = min((int64_t)row, (int64_t)g.n - 1 - n0);
-      sp.a_off[i] = (uint32_t)(ar * g.lda + kc * 16);
-      sp.w_off[i] = (uint32_t)(wr * g.ldw + kc * 16);
-    }
+  for (int i = 0; i < kDmaPerOp; ++i) {
+    const int line = (wv * kDmaPerOp + i) * 4 + (lane >> 4);
+    const int kc = (lane & 15) ^ (line & 15);
+    const int row = line * 4 + (kc >> 2);
+    const int lc = kc & 3;
+    const int64_t ar = min((int64_t)row, (int64_t)g.m - 1 - m0);
+    const int64_t wr = min((int64_t)row, (int64_t)g.n - 1 - n0);
+    a_off[i] = (uint32_t)(ar * g.lda + lc * 16);
+    w_off[i] = (uint32_t)(wr * g.ldw + lc * 16);
   }
-
-  f32x4 acc[8][4];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int fr = lane & 15, fg = lane >> 4;
-  const int ksteps = g.k / GK;  // >= 1
   const uint8_t* abase = g.a + m0 * g.lda;
   const uint8_t* wbase = g.w + n0 * g.ldw;
-  stage_issue(abase, wbase, sp, 0, sA0, sW0, wv);
-  // Steady state: two K steps per trip, no branches inside. At each barrier
-  // the buffer about to be read is complete (vmcnt(0) then s_barrier) and
-  // every wave has finished reading the buffer about to be refilled.
-  int ks = 0;
-  for (; ks + 2 < ksteps; ks += 2) {
-    wait_vm0();
-    __syncthreads();
-    stage_issue(abase, wbase, sp, (uint32_t)(ks + 1) * GK, sA1, sW1, wv);
-    stage_compute(sA0, sW0, acc, wm, wn, fr, fg);
-    wait_vm0();
-    __syncthreads();
-    stage_issue(abase, wbase, sp, (uint32_t)(ks + 2) * GK, sA0, sW0, wv);
-    stage_compute(sA1, sW1, acc, wm, wn, fr, fg);
-  }
-  // Tail: one or two steps remain; step ks is in buffer 0.
-  wait_vm0();
-  __syncthreads();
-  if (ks + 1 < ksteps) {
-    stage_issue(abase, wbase, sp, (uint32_t)(ks + 1) * GK, sA1, sW1, wv);
-    stage_compute(sA0, sW0, acc, wm, wn, fr, fg);
-    wait_vm0();
-    __syncthreads();
-    stage_compute(sA1, sW1, acc, wm, wn, fr, fg);
-  } else {
-    stage_compute(sA0, sW0, acc, wm, wn, fr, fg);
+  const int ksteps = g.k / GK;  // >= 1
+  // K steps are visited in a rotated order, starting at an even step that
+  // depends on the tile, so that the workgroups of one XCD, which would
+  // otherwise all read the same 64-byte column of their rows at the same
+  // time, spread their requests over the L2 channels. (The float32 sum over K
+  // is taken in a different order; the result stays within the contract.)
+  const int rot = ((4 * t) % ksteps) & ~1;
+  const int klast = ksteps - 1;
+  auto kphys = [&](int step) -> uint32_t {  // byte offset of logical step (clamped to K)
+    int s2 = min(step, klast) + rot;
+    if (s2 >= ksteps) s2 -= ksteps;
+    return (uint32_t)s2 * GK;
+  };
+  // DMA of logical step `step` into stage S (one group = 2*kDmaPerOp
+  // instructions per wave; groups complete in issue order).
+  auto issue = [&](int S, int step) {
+    uint4* d = smem + S * 2 * kStageU4;
+    const uint32_t k0 = kphys(step);
+#pragma unroll
+    for (int i = 0; i < kDmaPerOp; ++i) {
+      const int blk = wv * kDmaPerOp + i;
+      __builtin_amdgcn_global_load_lds((const void*)(abase + (a_off[i] + k0)), (lds_void*)(d + blk * 64), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(wbase + (w_off[i] + k0)), (lds_void*)(d + kStageU4 + blk * 64),
+                                       16, 0, 0);
+    }
+  };
+
+  // Fragment addressing: lane reads row (lane & 31) of a 32-row block,
+  // chunks 2h and 2h+1 (h = lane / 32). By the layout, block b's chunk
+  // positions depend on b's parity only, and blocks b and b + 2 are 4096
+  // bytes apart: so each lane keeps, per operand, the stage-0 byte addresses
+  // of its two chunks for an even and an odd block.
+  const int fr = lane & 31, fh = lane >> 5;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)smem;
+  const uint32_t wbyte = kStageU4 * 16;  // W follows A inside a stage
+  // W blocks of this wave: 2*wn + i (i = 0, 1); A blocks: 4*wm + j.
+  const uint32_t lw00 = lds0 + wbyte + wn * 4096 + lds_pos(fr, 2 * fh);
+  const uint32_t lw01 = lds0 + wbyte + wn * 4096 + lds_pos(fr, 2 * fh + 1);
+  const uint32_t lw10 = lds0 + wbyte + wn * 4096 + lds_pos(32 + fr, 2 * fh);
+  const uint32_t lw11 = lds0 + wbyte + wn * 4096 + lds_pos(32 + fr, 2 * fh + 1);
+  const uint32_t la00 = lds0 + wm * 8192 + lds_pos(fr, 2 * fh);
+  const uint32_t la01 = lds0 + wm * 8192 + lds_pos(fr, 2 * fh + 1);
+  const uint32_t la10 = lds0 + wm * 8192 + lds_pos(32 + fr, 2 * fh);
+  const uint32_t la11 = lds0 + wm * 8192 + lds_pos(32 + fr, 2 * fh + 1);
+  constexpr uint32_t kStageBytes = 2 * kStageU4 * 16;
+
+  f32x16 acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  // Software pipeline. Stage s % NST holds step s. Entering step ks, the
+  // first fragment set (w0, w1, a0, a1) of ks is already being read; the
+  // step reads its a2, a3 under its first four MFMAs, then (if step ks + 1
+  // exists) waits for its own DMA of ks + 1, joins the barrier that
+  // publishes stage ks + 1 and releases stage ks - 1 (every wave finished
+  // reading it before its previous second half), sends the DMA of step
+  // ks + 3 into the released stage, and reads the first fragments of ks + 1
+  // under its last four MFMAs. DMA groups in flight at the barrier wait:
+  // ks + 1 and ks + 2, so vmcnt(2*kDmaPerOp) leaves ks + 1 complete.
+  // Steps past the end of K (when K is not a multiple of NST*GK) run their
+  // MFMAs on zeroed fragments, so the accumulators have one path.
+  issue(0, 0);
+  issue(1, 1);
+  issue(2, 2);
+  OGA_WAIT_VM(4 * kDmaPerOp);
+  OGA_BARRIER();
+  i32x8 xw0 = frag<0>(lw00, lw01), xw1 = frag<0>(lw10, lw11);
+  i32x8 xa0 = frag<0>(la00, la01), xa1 = frag<0>(la10, la11);
+  i32x8 yw0, yw1, ya0, ya1;
+
+#define OGA_STEP(S, C, N)                                                                                      \
+  {                                                                                                            \
+    const int ks = kb + (S);                                                                                   \
+    const bool live = ks < ksteps;                                                                             \
+    const uint32_t so = (S) * kStageBytes;                                                                     \
+    i32x8 a2 = frag<4096>(la00 + so, la01 + so);                                                               \
+    i32x8 a3 = frag<4096>(la10 + so, la11 + so);                                                               \
+    OGA_LGKM_WAIT(4, "+v"(C##w0), "+v"(C##w1), "+v"(C##a0), "+v"(C##a1), "+v"(acc[0][2]), "+v"(acc[1][2]),     \
+                  "+v"(acc[0][3]), "+v"(acc[1][3]));                                                           \
+    if (!live) C##w0 = C##w1 = C##a0 = C##a1 = i32x8{0, 0, 0, 0, 0, 0, 0, 0};                                 \
+    acc[0][0] = mfma(C##w0, C##a0, acc[0][0]);                                                                 \
+    acc[1][0] = mfma(C##w1, C##a0, acc[1][0]);                                                                 \
+    acc[0][1] = mfma(C##w0, C##a1, acc[0][1]);                                                                 \
+    acc[1][1] = mfma(C##w1, C##a1, acc[1][1]);                                                                 \
+    if (ks + 1 < ksteps) {                                                                                     \
+      OGA_WAIT_VM(2 * kDmaPerOp);                                                                              \
+      asm volatile("s_barrier"                                                                                 \
+                   : "+v"(acc[0][0]), "+v"(acc[1][0]), "+v"(acc[0][1]), "+v"(acc[1][1])                        \
+                   :                                                                                           \
+                   : "memory");                                                                                \
+      issue(((S) + 3) % NST, ks + 3);                                                                          \
+    }                                                                                                          \
+    const uint32_t sn = (((S) + 1) % NST) * kStageBytes;                                                       \
+    N##w0 = frag<0>(lw00 + sn, lw01 + sn);                                                                     \
+    N##w1 = frag<0>(lw10 + sn, lw11 + sn);                                                                     \
+    N##a0 = frag<0>(la00 + sn, la01 + sn);                                                                     \
+    N##a1 = frag<0>(la10 + sn, la11 + sn);                                                                     \
+    OGA_LGKM_WAIT(8, "+v"(a2), "+v"(a3), "+v"(acc[0][0]), "+v"(acc[1][0]), "+v"(acc[0][1]), "+v"(acc[1][1]));  \
+    if (!live) a2 = a3 = i32x8{0, 0, 0, 0, 0, 0, 0, 0};                                                       \
+    acc[0][2] = mfma(C##w0, a2, acc[0][2]);                                                                    \
+    acc[1][2] = mfma(C##w1, a2, acc[1][2]);                                                                    \
+    acc[0][3] = mfma(C##w0, a3, acc[0][3]);                                                                    \
+    acc[1][3] = mfma(C##w1, a3, acc[1][3]);                                                                    \
   }
 
-  // Epilogue: lane holds out[m][n .. n+3] for each (mb, nb).
+  for (int kb = 0; kb < ksteps; kb += NST) {
+    OGA_STEP(0, x, y)
+    OGA_STEP(1, y, x)
+    OGA_STEP(2, x, y)
+    OGA_STEP(3, y, x)
+  }
+#undef OGA_STEP
+  OGA_LGKM_WAIT(0, "+v"(xw0), "+v"(xw1), "+v"(xa0), "+v"(xa1));
+
+  // Epilogue. Block (i, j): lane holds, for q in 0..3, output row
+  // m = wm*128 + 32j + (lane & 31) of the tile and columns n .. n+3 with
+  // n = wn*64 + 32i + 8q + 4*(lane >> 5), in acc[i][j][4q .. 4q+3]. The
+  // finished bf16 values go to this wave's LDS block, and are then written
+  // to HBM as whole 128-byte rows, 16 bytes per lane.
+  OGA_WAIT_VM(0);  // the last (clamped) DMA groups land before LDS is reused
+  OGA_BARRIER();   // every wave has finished reading the stages
   const float s = g.sa[0] * g.sb[0];
+  const bool has_bias = g.bias != nullptr;
+  const uint32_t ob = lds0 + wv * kOutWaveBytes;
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb) {
-    const int64_t ncol = n0 + wn * 64 + nb * 16 + 4 * fg;
-    float bv[4] = {0.f, 0.f, 0.f, 0.f};
-    const bool has_bias = g.bias != nullptr;
-    if (has_bias) {
+  for (int i = 0; i < 2; ++i) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t c = min(ncol + i, (int64_t)g.n - 1);
-        const float v = g.bias_dt == OGA_DT_BF16 ? __uint_as_float(((uint32_t)((const uint16_t*)g.bias)[c]) << 16)
-                                                 : ((const float*)g.bias)[c];
-        bv[i] = rbf(v);
+    for (int q = 0; q < 4; ++q) {
+      const int nl = i * 32 + q * 8 + 4 * fh;  // column inside the wave's block
+      float bv[4] = {0.f, 0.f, 0.f, 0.f};
+      if (has_bias) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t c = min(n0 + wn * 64 + nl + e, (int64_t)g.n - 1);
+          const float v = g.bias_dt == OGA_DT_BF16 ? __uint_as_float(((uint32_t)((const uint16_t*)g.bias)[c]) << 16)
+                                                   : ((const float*)g.bias)[c];
+          bv[e] = rbf(v);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float v = rbf(acc[i][j][q * 4 + e] * s);
+          if (has_bias) v = v + bv[e];
+          o[e] = v;
+        }
+        uint2 pk;
+        pk.x = pack_bf16(o[0], o[1]);
+        pk.y = pack_bf16(o[2], o[3]);
+        const uint32_t addr = ob + (j * 32 + fr) * kOutPitch + nl * 2;
+        asm volatile("ds_write_b64 %0, %1" ::"v"(addr), "v"(pk) : "memory");
       }
     }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  // Row r of the block: 8 lanes x 16 bytes; 8 rows per pass, 16 passes.
+  const int rsub = lane >> 3, cb = (lane & 7) * 8;  // column (bf16) inside the row
+  const int64_t ncol = n0 + wn * 64 + cb;
+#pragma unroll 4
+  for (int pass = 0; pass < 16; ++pass) {
+    const int r = pass * 8 + rsub;
+    uint4 v;
+    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(ob + r * kOutPitch + cb * 2) : "memory");
+    const int64_t mrow = m0 + wm * 128 + r;
+    if (mrow < g.m) {
+      uint16_t* dst = g.out + mrow * g.ldo + ncol;
+      if (ncol + 8 <= g.n) {
+        *(uint4*)dst = v;
+      } else {
+        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb) {
-      const int64_t mrow = m0 + wm * 128 + mb * 16 + fr;
-      float o[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float v = rbf(acc[mb][nb][i] * s);
-        if (has_bias) v = v + bv[i];
-        o[i] = v;
-      }
-      if (mrow < g.m) {
-        uint16_t* dst = g.out + mrow * g.ldo + ncol;
-        if (ncol + 3 < g.n) {
-          uint2 pk;
-          pk.x = pack_bf16(o[0], o[1]);
-          pk.y = pack_bf16(o[2], o[3]);
-          *(uint2*)dst = pk;
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (ncol + i < g.n) dst[i] = (uint16_t)(pack_bf16(o[i], 0.f) & 0xFFFF);
-        }
+        for (int e = 0; e < 8; ++e)
+          if (ncol + e < g.n) dst[e] = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
       }
     }
   }
@@ -237,9 +342,9 @@ extern "C" int oga_fp8_linear(const void* a, int64_t lda, const void* w, int64_t
   if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX) return unsupported("dimension too large");
   if (lda < k || ldw < k || ldo < n) return fail("leading dimension smaller than the row");
   if (!aligned(a, 16) || !aligned(w, 16) || lda % 16 || ldw % 16) return fail("a/w rows must be 16-byte aligned");
-  if (!aligned(out, 8) || ldo % 4) return fail("out rows must be 8-byte aligned");
-  // Per-lane offsets into one 256-row tile are 32-bit.
-  if (256 * lda + 16 > (int64_t)UINT32_MAX || 256 * ldw + 16 > (int64_t)UINT32_MAX)
+  if (!aligned(out, 16) || ldo % 8) return fail("out rows must be 16-byte aligned");
+  // Per-lane byte offsets inside one 256-row tile (plus K) are 32-bit.
+  if (256 * lda + k > (int64_t)UINT32_MAX || 256 * ldw + k > (int64_t)UINT32_MAX)
     return unsupported("row stride too large");
   if (bias && !dt_ok(bias_dtype)) return fail("bias dtype must be bf16 or f32");
   GemmArgs g{};
@@ -259,7 +364,8 @@ extern "C" int oga_fp8_linear(const void* a, int64_t lda, const void* w, int64_t
   g.tiles_m = (int)((m + GM - 1) / GM);
   g.tiles_n = (int)((n + GN - 1) / GN);
   const int64_t nt = (int64_t)g.tiles_m * g.tiles_n;
+  if (nt > INT32_MAX) return unsupported("too many tiles");
   g.xcd_remap = (nt % 8) == 0;
-  hipLaunchKernelGGL(k_fp8_gemm, dim3((unsigned)nt), dim3(512), 0, (hipStream_t)stream, g);
+  hipLaunchKernelGGL(k_fp8_gemm, dim3((unsigned)nt), dim3(64 * kWaves), 0, (hipStream_t)stream, g);
   return launch_status();
 }

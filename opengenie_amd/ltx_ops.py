@@ -771,7 +771,7 @@ def _can_use_fp8_gemm(qflat: torch.Tensor, weight: torch.Tensor, scale_a, scale_
         return False
     if qflat.stride(0) % 16 or weight.stride(0) % 16 or qflat.data_ptr() % 16 or weight.data_ptr() % 16:
         return False
-    if weight.shape[0] % 4:  # 8-byte output stores
+    if weight.shape[0] % 8:  # 16-byte output rows
         return False
     for s in (scale_a, scale_b):
         if not isinstance(s, torch.Tensor) or s.numel() != 1 or not s.is_cuda or s.dtype != torch.float32:
