@@ -60,6 +60,14 @@ OGA_DEVICE uint4 pack8(const float* f) {
   return u;
 }
 
+// 16-byte store of a streamed output: non-temporal, so it does not evict
+// the inputs still being read from the caches.
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+OGA_DEVICE void st_nt16(void* p, const uint4& v) {
+  const u32x4 w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, (u32x4*)p);
+}
+
 // ------------------------------------------------------ typed 8-wide loads
 // Loads 8 consecutive logical elements starting at element offset `off` with
 // element stride `sc`, converting to float. `vec` (uniform) says the 8
@@ -112,6 +120,34 @@ OGA_DEVICE void load8_t(const void* base, int64_t off, int64_t sc, float* f) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) f[i] = p[i * sc];
     }
+  }
+}
+
+// 8 consecutive elements of a bf16 (one 16-byte vector) or float32 (two)
+// tensor, held as loaded; `raw8_get` converts them to float.
+template <int DT>
+struct Raw8 {
+  uint4 u[DT == OGA_DT_BF16 ? 1 : 2];
+};
+template <int DT>
+OGA_DEVICE Raw8<DT> raw8_load(const void* base, int64_t off) {
+  Raw8<DT> r;
+  if (DT == OGA_DT_BF16) {
+    r.u[0] = *(const uint4*)((const uint16_t*)base + off);
+  } else {
+    r.u[0] = *(const uint4*)((const float*)base + off);
+    r.u[DT == OGA_DT_BF16 ? 0 : 1] = *(const uint4*)((const float*)base + off + 4);
+  }
+  return r;
+}
+template <int DT>
+OGA_DEVICE void raw8_get(const Raw8<DT>& r, float* f) {
+  if (DT == OGA_DT_BF16) {
+    unpack8(r.u[0], f);
+  } else {
+    const uint4 a = r.u[0], b = r.u[DT == OGA_DT_BF16 ? 0 : 1];
+    f[0] = __uint_as_float(a.x); f[1] = __uint_as_float(a.y); f[2] = __uint_as_float(a.z); f[3] = __uint_as_float(a.w);
+    f[4] = __uint_as_float(b.x); f[5] = __uint_as_float(b.y); f[6] = __uint_as_float(b.z); f[7] = __uint_as_float(b.w);
   }
 }
 

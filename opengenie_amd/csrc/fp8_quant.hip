@@ -50,7 +50,7 @@ __global__ __launch_bounds__(256) void k_fp8_quant(const uint16_t* x, const floa
     o.y = e4m3x4(f[4], f[5], f[6], f[7]);
     o.z = e4m3x4(f[8], f[9], f[10], f[11]);
     o.w = e4m3x4(f[12], f[13], f[14], f[15]);
-    *(uint4*)(q + i0) = o;
+    st_nt16(q + i0, o);
   } else {
     for (int64_t i = i0; i < n; ++i) {
       float v = pre<GELU>(__uint_as_float(((uint32_t)x[i]) << 16)) * r;
@@ -146,7 +146,7 @@ __global__ __launch_bounds__(256) void k_head_quant(const uint16_t* x, const flo
   o.y = e4m3x4(f[4], f[5], f[6], f[7]);
   o.z = e4m3x4(f[8], f[9], f[10], f[11]);
   o.w = e4m3x4(f[12], f[13], f[14], f[15]);
-  *(uint4*)(q + i0) = o;
+  st_nt16(q + i0, o);
 }
 
 // ------------------------------------------------------------ self-test

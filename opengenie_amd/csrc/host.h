@@ -40,4 +40,19 @@ inline bool vec8_ok(const void* p, int dt, int64_t offset, int64_t s0, int64_t s
 // Number of compute units of the current device (cached per device id).
 int cu_count();
 
+// Grid (workgroups per batch, batch) of 4-wave workgroups for kernels in
+// which each wave walks token rows t, t + 4*gridDim.x, ... of its batch:
+// about 16 waves per CU, sized so that every wave gets the same number of
+// rows (the last pass over the rows is not left part-empty).
+inline dim3 balanced_row_grid(int64_t batch, int64_t tokens) {
+  const int64_t target_waves = (int64_t)cu_count() * 16;
+  const int64_t rows = batch * tokens;
+  int64_t per_wave = (rows + target_waves - 1) / target_waves;
+  if (per_wave < 1) per_wave = 1;
+  int64_t waves = (tokens + per_wave - 1) / per_wave;  // per batch
+  int64_t wgs = (waves + 3) / 4;
+  if (wgs < 1) wgs = 1;
+  return dim3((unsigned)wgs, (unsigned)batch);
+}
+
 }  // namespace oga

@@ -172,21 +172,36 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rope(RopeArgs a) {
         if (NT == 2) x1[j] = add_bias8(x1[j], B1, j * 512 + lane * 8);
       }
     }
-    const float inv0 = row_inv<CH>(x0, a.eps);
-    const float inv1 = NT == 2 ? row_inv<CH>(x1, a.eps) : 0.0f;
+    // cos/sin of every head this lane touches go out with q/k, as loaded.
     const int64_t cbase = b * a.c_sb + t * a.c_st + hd0;
     const int64_t sbase = b * a.s_sb + t * a.s_st + hd0;
+    Raw8<CDT> cr[VEC ? CH : 1], sr[VEC ? CH : 1];
+    if (VEC) {
+#pragma unroll
+      for (int j = 0; j < CH; ++j) {
+        const int64_t head = j * 4 + (lane >> 4);
+        cr[j] = raw8_load<CDT>(a.cos, cbase + head * a.c_sh);
+        sr[j] = raw8_load<CDT>(a.sin, sbase + head * a.s_sh);
+      }
+    }
+    const float inv0 = row_inv<CH>(x0, a.eps);
+    const float inv1 = NT == 2 ? row_inv<CH>(x1, a.eps) : 0.0f;
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       const int c0 = j * 512 + lane * 8;
       const int64_t head = j * 4 + (lane >> 4);
       float cs[8], sn[8];
-      load8_t<CDT, VEC>(a.cos, cbase + head * a.c_sh, 1, cs);
-      load8_t<CDT, VEC>(a.sin, sbase + head * a.s_sh, 1, sn);
-      *(uint4*)(a.o0 + r * a.out_stride + c0) = rope8(norm8(x0[j], W0, c0, inv0), cs, sn, second, cs_bf);
+      if (VEC) {
+        raw8_get<CDT>(cr[VEC ? j : 0], cs);
+        raw8_get<CDT>(sr[VEC ? j : 0], sn);
+      } else {
+        load8_t<CDT, false>(a.cos, cbase + head * a.c_sh, 1, cs);
+        load8_t<CDT, false>(a.sin, sbase + head * a.s_sh, 1, sn);
+      }
+      st_nt16(a.o0 + r * a.out_stride + c0, rope8(norm8(x0[j], W0, c0, inv0), cs, sn, second, cs_bf));
       if (NT == 2)
-        *(uint4*)(a.o1 + r * a.out_stride + c0) = rope8(norm8(x1[j], W1, c0, inv1), cs, sn, second, cs_bf);
-      if (PACK) *(uint4*)(a.ov + r * a.out_stride + c0) = *(const uint4*)(a.v + r * C + c0);
+        st_nt16(a.o1 + r * a.out_stride + c0, rope8(norm8(x1[j], W1, c0, inv1), cs, sn, second, cs_bf));
+      if (PACK) st_nt16(a.ov + r * a.out_stride + c0, *(const uint4*)(a.v + r * C + c0));
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -196,12 +211,7 @@ template <int NT, bool BIAS, bool PACK>
 static int launch_rope(RopeArgs& a, int64_t batch, hipStream_t st) {
   if (batch == 0 || a.tokens == 0) return OGA_OK;
   if (batch > 65535) return unsupported("batch > 65535");
-  const int64_t target_waves = (int64_t)cu_count() * 16;
-  int64_t per_batch = ((target_waves + batch - 1) / batch + 3) / 4;
-  const int64_t need = (a.tokens + 3) / 4;
-  if (per_batch > need) per_batch = need;
-  if (per_batch < 1) per_batch = 1;
-  const dim3 grid((unsigned)per_batch, (unsigned)batch);
+  const dim3 grid = balanced_row_grid(batch, a.tokens);
   if (a.cols == 4096) {
     if (a.cs_dt == OGA_DT_BF16) {
       if (a.cs_vec)

@@ -178,6 +178,13 @@ __global__ __launch_bounds__(256) void k_row(RowArgs a) {
 
   const bool tab0 = a.s0.tab != nullptr;
   const bool tab1 = a.s1.tab != nullptr;
+  // Per-token Ada rows are read with the row's other inputs, as loaded
+  // vectors, when their columns are contiguous (VEC); otherwise gathered
+  // where used.
+  constexpr bool kPre = !UNIFORM && VEC;
+  constexpr bool kPre1 = kPre && Tr::kTwo;
+  Raw8<D0> p0[kPre ? CH : 1];
+  Raw8<D1> p1[kPre1 ? CH : 1];
   for (bool first = true; t < a.tokens; t += step, first = false) {
     const int64_t r = b * a.tokens + t;
     uint16_t* outr = a.out + r * C + lane * 8;
@@ -190,6 +197,14 @@ __global__ __launch_bounds__(256) void k_row(RowArgs a) {
 #pragma unroll
         for (int j = 0; j < CH; ++j) yv[j] = *(const uint4*)(a.y + r * C + j * 512 + lane * 8);
       }
+    }
+    if (kPre) {
+#pragma unroll
+      for (int j = 0; j < CH; ++j) p0[j] = raw8_load<D0>(a.s0.ts, ts0 + (int64_t)(j * 512 + lane * 8));
+    }
+    if (kPre1) {
+#pragma unroll
+      for (int j = 0; j < CH; ++j) p1[j] = raw8_load<D1>(a.s1.ts, ts1 + (int64_t)(j * 512 + lane * 8));
     }
 
     float inv = 1.0f;
@@ -216,14 +231,22 @@ __global__ __launch_bounds__(256) void k_row(RowArgs a) {
       if (Tr::kTwo) lds_load8(L1, col0, v1);
       if (!UNIFORM) {
         float tsv[8];
-        load8_t<D0, VEC>(a.s0.ts, ts0 + (int64_t)col0 * a.s0.ts_sc, a.s0.ts_sc, tsv);
+        if (kPre) {
+          raw8_get<D0>(p0[kPre ? j : 0], tsv);
+        } else {
+          load8_t<D0, false>(a.s0.ts, ts0 + (int64_t)col0 * a.s0.ts_sc, a.s0.ts_sc, tsv);
+        }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           float s = tab0 ? v0[i] + tsv[i] : tsv[i];
           v0[i] = (tab0 && B0) ? rbf(s) : s;
         }
         if (Tr::kTwo) {
-          load8_t<D1, VEC>(a.s1.ts, ts1 + (int64_t)col0 * a.s1.ts_sc, a.s1.ts_sc, tsv);
+          if (kPre1) {
+            raw8_get<D1>(p1[kPre1 ? j : 0], tsv);
+          } else {
+            load8_t<D1, false>(a.s1.ts, ts1 + (int64_t)col0 * a.s1.ts_sc, a.s1.ts_sc, tsv);
+          }
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
             float s = tab1 ? v1[i] + tsv[i] : tsv[i];
@@ -258,12 +281,161 @@ __global__ __launch_bounds__(256) void k_row(RowArgs a) {
           o[i] = xf[i] + p;
         }
       }
-      *(uint4*)(outr + j * 512) = pack8(o);
-      // Keep each vector step's constants live only within the step: the
-      // occupancy this buys hides the LDS latency better than hoisting.
+      st_nt16(outr + j * 512, pack8(o));
+      // Keep each vector step's LDS constants live only within the step
+      // (the row's HBM inputs were all requested above).
       __builtin_amdgcn_sched_barrier(0);
     }
   }
+}
+
+// ------------------------------------------------------ elementwise ops
+// The Ada ops with no row reduction (AdaLN affine, mul, residual gates).
+// A wave owns one 512-column chunk (lane l: columns chunk*512 + 8l .. +7)
+// of a group of consecutive token rows: its per-column constants (the
+// table rows, the bias, and the finished Ada values when the timestep row is
+// shared by all tokens) are computed once into registers, then the wave
+// streams its rows U at a time with every load of the U rows in flight
+// together. No LDS, no barrier.
+#ifndef OGA_ELEM_ROWS_IN_FLIGHT
+#define OGA_ELEM_ROWS_IN_FLIGHT 4
+#endif
+#ifndef OGA_ELEM_WAVES_PER_CU
+#define OGA_ELEM_WAVES_PER_CU 32
+#endif
+template <int CH, int OP, bool UNIFORM, int D0, int D1, bool VEC>
+__global__ __launch_bounds__(256) void k_elem(RowArgs a, int64_t rows_per_group) {
+  using Tr = RowTraits<OP>;
+  constexpr int C = CH * 512;
+  constexpr bool B0 = D0 == OGA_DT_BF16;
+  constexpr bool B1 = D1 == OGA_DT_BF16;
+  constexpr int U = OGA_ELEM_ROWS_IN_FLIGHT;
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
+  const int chunk = wid % CH;
+  const int64_t group = wid / CH;
+  const int64_t b = blockIdx.y;
+  const int col0 = chunk * 512 + lane * 8;
+  const int64_t t_begin = group * rows_per_group;
+  const int64_t t_end = min(t_begin + rows_per_group, a.tokens);
+  if (t_begin >= t_end) return;  // whole wave; the kernel has no barrier
+
+  const bool tab0 = a.s0.tab != nullptr;
+  const bool tab1 = a.s1.tab != nullptr;
+  float c0[8], c1[8], bb[8];
+  ada_table8(a.s0, col0, c0);
+  if (Tr::kTwo) ada_table8(a.s1, col0, c1);
+  if (UNIFORM) {
+    float v[8];
+    ada_value8(a.s0, c0, b, 0, col0, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c0[i] = v[i];
+    if (Tr::kTwo) {
+      ada_value8(a.s1, c1, b, 0, col0, v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float f = 1.0f + v[i];
+        c1[i] = B1 ? rbf(f) : f;
+      }
+    }
+  }
+  if (Tr::kBias) {
+    load8(a.bias, a.bias_dt, col0, 1, true, bb);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) bb[i] = rbf(bb[i]);
+  }
+
+  const int64_t tsc0 = a.s0.ts_off + b * a.s0.ts_sb + (int64_t)col0 * a.s0.ts_sc;
+  const int64_t tsc1 = a.s1.ts_off + b * a.s1.ts_sb + (int64_t)col0 * a.s1.ts_sc;
+  constexpr bool kPre = !UNIFORM && VEC;
+  for (int64_t t0 = t_begin; t0 < t_end; t0 += U) {
+    uint4 xv[U], yv[U];
+    Raw8<D0> p0[U];
+    Raw8<D1> p1[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t t = t0 + u;
+      if (t < t_end) {
+        const int64_t r = b * a.tokens + t;
+        xv[u] = *(const uint4*)(a.x + r * C + col0);
+        if (Tr::kY) yv[u] = *(const uint4*)(a.y + r * C + col0);
+        if (kPre) {
+          p0[u] = raw8_load<D0>(a.s0.ts, tsc0 + t * a.s0.ts_st);
+          if (Tr::kTwo) p1[u] = raw8_load<D1>(a.s1.ts, tsc1 + t * a.s1.ts_st);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t t = t0 + u;
+      if (t >= t_end) break;
+      const int64_t r = b * a.tokens + t;
+      float v0[8], v1[8], xf[8], o[8];
+      if (UNIFORM) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          v0[i] = c0[i];
+          v1[i] = Tr::kTwo ? c1[i] : 0.0f;
+        }
+      } else {
+        float tsv[8];
+        if (kPre) raw8_get<D0>(p0[u], tsv);
+        else load8_t<D0, false>(a.s0.ts, tsc0 + t * a.s0.ts_st, a.s0.ts_sc, tsv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float sum = tab0 ? c0[i] + tsv[i] : tsv[i];
+          v0[i] = (tab0 && B0) ? rbf(sum) : sum;
+        }
+        if (Tr::kTwo) {
+          if (kPre) raw8_get<D1>(p1[u], tsv);
+          else load8_t<D1, false>(a.s1.ts, tsc1 + t * a.s1.ts_st, a.s1.ts_sc, tsv);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            float sum = tab1 ? c1[i] + tsv[i] : tsv[i];
+            if (tab1 && B1) sum = rbf(sum);
+            const float f = 1.0f + sum;
+            v1[i] = B1 ? rbf(f) : f;
+          }
+        }
+      }
+      unpack8(xv[u], xf);
+      if (OP == OP_ADALN) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float p = xf[i] * v1[i];
+          if (B1) p = rbf(p);
+          o[i] = p + v0[i];
+        }
+      } else if (OP == OP_MUL) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = xf[i] * v0[i];
+      } else {
+        float yf[8];
+        unpack8(yv[u], yf);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float yy = yf[i];
+          if (Tr::kBias) yy = rbf(yy + bb[i]);
+          float p = yy * v0[i];
+          if (B0) p = rbf(p);
+          o[i] = xf[i] + p;
+        }
+      }
+      st_nt16(a.out + r * C + col0, pack8(o));
+    }
+  }
+}
+
+// Grid of k_elem: groups of consecutive rows of equal size (about
+// OGA_ELEM_WAVES_PER_CU waves per CU in all), CH waves per group.
+static void elem_grid(int64_t batch, int64_t tokens, int ch, dim3& grid, int64_t& rows_per_group) {
+  const int64_t target_waves = (int64_t)cu_count() * OGA_ELEM_WAVES_PER_CU;
+  int64_t groups = target_waves / (batch * ch);
+  if (groups < 1) groups = 1;
+  rows_per_group = (tokens + groups - 1) / groups;
+  groups = (tokens + rows_per_group - 1) / rows_per_group;
+  const int64_t waves = groups * ch;  // ch is 4 or 8: whole workgroups
+  grid = dim3((unsigned)(waves / 4), (unsigned)batch);
 }
 
 // ------------------------------------------------- generic-width elementwise
@@ -280,7 +452,7 @@ __global__ __launch_bounds__(256) void k_bias_add(const uint16_t* x, const void*
     load8(bias, bias_dt, col, 1, true, bf);
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = xf[i] + rbf(bf[i]);
-    *(uint4*)(out + i0) = pack8(o);
+    st_nt16(out + i0, pack8(o));
   } else {
     for (int64_t i = i0; i < min(i0 + 8, n); ++i) {
       const int64_t col = i % cols;
@@ -306,7 +478,7 @@ __global__ __launch_bounds__(256) void k_head_gate_mul(const uint16_t* x, const 
     unpack8(*(const uint4*)(x + i0), xf);
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = xf[i] * g;
-    *(uint4*)(out + i0) = pack8(o);
+    st_nt16(out + i0, pack8(o));
   } else {
     for (int64_t i = i0; i < hi; ++i) {
       const int64_t r = i / cols, c = i - (i / cols) * cols;
@@ -358,26 +530,23 @@ static void make_direct_src(AdaSrc& s, const void* p, int dt, const int64_t* st3
   s.ts_vec = vec8_ok(p, dt, 0, s.ts_sb, s.ts_st, s.ts_sc);
 }
 
-// Grid: enough 4-wave workgroups per batch that the whole launch holds about
-// four waves per SIMD (capped by the token count); each wave then strides
-// over its batch's tokens.
-static dim3 row_grid(int64_t batch, int64_t tokens) {
-  const int64_t target_waves = (int64_t)cu_count() * 16;
-  int64_t per_batch = (target_waves + batch - 1) / batch;
-  per_batch = (per_batch + 3) / 4;  // workgroups
-  const int64_t need = (tokens + 3) / 4;
-  if (per_batch > need) per_batch = need;
-  if (per_batch < 1) per_batch = 1;
-  return dim3((unsigned)per_batch, (unsigned)batch);
-}
-
 template <int CH, int OP, bool UNIFORM, int D0, int D1>
 static void launch_row_v(RowArgs& a, int64_t batch, bool vec, hipStream_t st) {
-  const dim3 grid = row_grid(batch, a.tokens);
-  if (vec)
-    hipLaunchKernelGGL((k_row<CH, OP, UNIFORM, D0, D1, true>), grid, dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL((k_row<CH, OP, UNIFORM, D0, D1, false>), grid, dim3(256), 0, st, a);
+  if constexpr (OP != OP_ADAZERO) {
+    dim3 grid;
+    int64_t rpg = 0;
+    elem_grid(batch, a.tokens, CH, grid, rpg);
+    if (vec)
+      hipLaunchKernelGGL((k_elem<CH, OP, UNIFORM, D0, D1, true>), grid, dim3(256), 0, st, a, rpg);
+    else
+      hipLaunchKernelGGL((k_elem<CH, OP, UNIFORM, D0, D1, false>), grid, dim3(256), 0, st, a, rpg);
+  } else {
+    const dim3 grid = balanced_row_grid(batch, a.tokens);
+    if (vec)
+      hipLaunchKernelGGL((k_row<CH, OP, UNIFORM, D0, D1, true>), grid, dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((k_row<CH, OP, UNIFORM, D0, D1, false>), grid, dim3(256), 0, st, a);
+  }
 }
 
 template <int CH, int OP, bool UNIFORM>
