@@ -65,7 +65,8 @@ __global__ __launch_bounds__(256) void k_fp8_quant(const uint16_t* x, const floa
 // Pass 1: partial amax over a block of tokens, for every head. Block
 // (b, chunk) covers tokens [chunk*TPB, chunk*TPB + TPB); each wave walks
 // TPB/4 token rows; lane l of vector step j sees head (j*512 + 8l) / D.
-// partial[b, chunk, h] = max |x| over the block.
+// partial[b, h, chunk] = max |x| over the block (a head's partials are
+// contiguous for the reduction in pass 2).
 template <int CH, int D>
 __global__ __launch_bounds__(256) void k_head_amax(const uint16_t* x, float* partial, int64_t tokens, int tpb,
                                                    int nchunk) {
@@ -103,50 +104,50 @@ __global__ __launch_bounds__(256) void k_head_amax(const uint16_t* x, float* par
   __syncthreads();
   for (int h = threadIdx.x; h < H; h += 256) {
     const float v = fmaxf(fmaxf(red[0][h], red[1][h]), fmaxf(red[2][h], red[3][h]));
-    partial[(b * nchunk + chunk) * H + h] = v;
+    partial[(b * H + h) * nchunk + chunk] = v;
   }
 }
 
-// Pass 2: scale[b, h] = max(amax, 1e-12) / 448 (IEEE division). One wave
-// per (b, h): lanes stride over the block partials, then a wave-wide max.
-__global__ __launch_bounds__(64) void k_head_scale(const float* partial, float* scale, int heads, int nchunk) {
-  const int64_t bh = blockIdx.x;
-  const int64_t b = bh / heads;
-  const int h = (int)(bh - b * heads);
-  const int lane = threadIdx.x;
+// Pass 2: quantize. Workgroup (token chunk, h, b) first reduces the amax
+// partials of head (b, h) to scale = max(amax, 1e-12) / 448 (IEEE division;
+// workgroup 0 of the head stores it), then quantizes its chunk of tokens:
+// q = e4m3(clamp(x / scale, +-448)). D/8 lanes cover one token's head slice
+// (16 bytes each), so every load is a whole 2*D-byte slice and every store
+// a whole D-byte slice.
+constexpr int kQuantTokens = 64;
+template <int D>
+__global__ __launch_bounds__(256) void k_head_scale_quant(const uint16_t* x, const float* partial, float* scale_out,
+                                                          uint8_t* q, int64_t tokens, int heads, int nchunk) {
+  constexpr int LPT = D / 8;      // lanes per token slice
+  constexpr int TPP = 256 / LPT;  // token slices per pass
+  __shared__ float red[4];
+  const int h = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   float m = 0.0f;
-  for (int c = lane; c < nchunk; c += 64) m = fmaxf(m, partial[(b * nchunk + c) * heads + h]);
+  for (int c = threadIdx.x; c < nchunk; c += 256) m = fmaxf(m, partial[(b * heads + h) * nchunk + c]);
   m = row16_max(m);
   m = fmaxf(m, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(m), 0x401F)));
   m = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0)),
             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32)));
-  if (lane == 0) scale[bh] = fmaxf(m, 1e-12f) / 448.0f;
-}
+  if (lane == 0) red[w] = m;
+  __syncthreads();
+  const float s = fmaxf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), 1e-12f) / 448.0f;
+  if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[b * heads + h] = s;
 
-// Pass 3: q = e4m3(clamp(x / scale[b, h], +-448)), 16 elements per thread
-// (16 consecutive elements never straddle a head for D in {64, 128}).
-__global__ __launch_bounds__(256) void k_head_quant(const uint16_t* x, const float* scale, uint8_t* q, int64_t n,
-                                                    int64_t tokens, int heads, int d) {
-  const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 16;
-  if (i0 >= n) return;
-  const int64_t row = (int64_t)heads * d;
-  const int64_t tok = i0 / row;
-  const int64_t h = (i0 - tok * row) / d;
-  const int64_t b = tok / tokens;
-  const float s = scale[b * heads + h];
-  const uint4 u0 = *(const uint4*)(x + i0);
-  const uint4 u1 = *(const uint4*)(x + i0 + 8);
-  float f[16];
-  unpack8(u0, f);
-  unpack8(u1, f + 8);
+  const int sub = threadIdx.x % LPT, tk = threadIdx.x / LPT;
+  const int64_t t0 = (int64_t)blockIdx.x * kQuantTokens;
+  const int64_t t1 = min(t0 + kQuantTokens, tokens);
+  for (int64_t t = t0 + tk; t < t1; t += TPP) {
+    const int64_t e0 = ((b * tokens + t) * heads + h) * D + sub * 8;
+    float f[8];
+    unpack8(*(const uint4*)(x + e0), f);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) f[i] = clamp448(f[i] / s);
-  uint4 o;
-  o.x = e4m3x4(f[0], f[1], f[2], f[3]);
-  o.y = e4m3x4(f[4], f[5], f[6], f[7]);
-  o.z = e4m3x4(f[8], f[9], f[10], f[11]);
-  o.w = e4m3x4(f[12], f[13], f[14], f[15]);
-  st_nt16(q + i0, o);
+    for (int i = 0; i < 8; ++i) f[i] = clamp448(f[i] / s);
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 o = {e4m3x4(f[0], f[1], f[2], f[3]), e4m3x4(f[4], f[5], f[6], f[7])};
+    __builtin_nontemporal_store(o, (u32x2*)(q + e0));
+  }
 }
 
 // ------------------------------------------------------------ self-test
@@ -227,14 +228,13 @@ extern "C" int oga_fp8_quantize_per_head(const void* x, void* q, float* scale_ou
   }
   int rc = launch_status();
   if (rc) return rc;
-  const int64_t bh = batch * heads;
-  hipLaunchKernelGGL(k_head_scale, dim3((unsigned)bh), dim3(64), 0, st, partial, scale_out, (int)heads,
-                     (int)head_chunks(tokens));
-  if ((rc = launch_status())) return rc;
-  const int64_t n = batch * tokens * row;
-  const int64_t threads = n / 16;
-  hipLaunchKernelGGL(k_head_quant, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, xs, scale_out,
-                     (uint8_t*)q, n, tokens, (int)heads, (int)head_dim);
+  const dim3 qgrid((unsigned)((tokens + kQuantTokens - 1) / kQuantTokens), (unsigned)heads, (unsigned)batch);
+  if (head_dim == 128)
+    hipLaunchKernelGGL(k_head_scale_quant<128>, qgrid, dim3(256), 0, st, xs, partial, scale_out, (uint8_t*)q, tokens,
+                       (int)heads, (int)head_chunks(tokens));
+  else
+    hipLaunchKernelGGL(k_head_scale_quant<64>, qgrid, dim3(256), 0, st, xs, partial, scale_out, (uint8_t*)q, tokens,
+                       (int)heads, (int)head_chunks(tokens));
   return launch_status();
 }
 

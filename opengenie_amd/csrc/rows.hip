@@ -426,6 +426,141 @@ __global__ __launch_bounds__(256) void k_elem(RowArgs a, int64_t rows_per_group)
   }
 }
 
+// ------------------------------------------------------------ AdaZero
+// y = R(R?(R(x * inv_rms) * R?(1 + scale)) + shift). A workgroup of CH waves
+// owns a block of up to RMAX consecutive token rows; wave w owns columns
+// w*512 + 8l .. +7 of every row of the block. Each wave computes its Ada
+// constants once, issues the loads of all its rows together, and adds up
+// the squares of its chunk per row (float64: squares of bf16 values are
+// exact); one barrier later every wave combines the CH partial sums of a
+// row into that row's normaliser and writes its chunk.
+constexpr int kAdaRows = 8;
+template <int CH, bool UNIFORM, int D0, int D1, bool VEC>
+__global__ __launch_bounds__(512) void k_adazero(RowArgs a, int rows_per_wg) {
+  constexpr int C = CH * 512;
+  constexpr bool B1 = D1 == OGA_DT_BF16;
+  constexpr bool B0 = D0 == OGA_DT_BF16;
+  __shared__ double part[kAdaRows][CH];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int64_t b = blockIdx.y;
+  const int col0 = wv * 512 + lane * 8;
+  const int64_t t0 = (int64_t)blockIdx.x * rows_per_wg;
+  const int nr = (int)min((int64_t)rows_per_wg, a.tokens - t0);  // >= 1 by the grid
+
+  const bool tab0 = a.s0.tab != nullptr;
+  const bool tab1 = a.s1.tab != nullptr;
+  float c0[8], c1[8];
+  ada_table8(a.s0, col0, c0);
+  ada_table8(a.s1, col0, c1);
+  if (UNIFORM) {
+    float v[8];
+    ada_value8(a.s0, c0, b, 0, col0, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c0[i] = v[i];
+    ada_value8(a.s1, c1, b, 0, col0, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float f = 1.0f + v[i];
+      c1[i] = B1 ? rbf(f) : f;
+    }
+  }
+  const int64_t tsc0 = a.s0.ts_off + b * a.s0.ts_sb + (int64_t)col0 * a.s0.ts_sc;
+  const int64_t tsc1 = a.s1.ts_off + b * a.s1.ts_sb + (int64_t)col0 * a.s1.ts_sc;
+  constexpr bool kPre = !UNIFORM && VEC;
+
+  uint4 xv[kAdaRows];
+  Raw8<D0> p0[kPre ? kAdaRows : 1];
+  Raw8<D1> p1[kPre ? kAdaRows : 1];
+#pragma unroll
+  for (int u = 0; u < kAdaRows; ++u) {
+    if (u < nr) {
+      const int64_t t = t0 + u;
+      xv[u] = *(const uint4*)(a.x + (b * a.tokens + t) * C + col0);
+      if (kPre) {
+        p0[kPre ? u : 0] = raw8_load<D0>(a.s0.ts, tsc0 + t * a.s0.ts_st);
+        p1[kPre ? u : 0] = raw8_load<D1>(a.s1.ts, tsc1 + t * a.s1.ts_st);
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kAdaRows; ++u) {
+    if (u < nr) {
+      float f[8];
+      unpack8(xv[u], f);
+      double ss[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const double d = (double)f[i];
+        ss[i & 3] = fma(d, d, ss[i & 3]);
+      }
+      const double w = wave_sum_d((ss[0] + ss[1]) + (ss[2] + ss[3]));
+      if (lane == 0) part[u][wv] = w;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < kAdaRows; ++u) {
+    if (u < nr) {
+      const int64_t t = t0 + u;
+      double tot = 0.0;
+#pragma unroll
+      for (int c = 0; c < CH; ++c) tot += part[u][c];
+      const float mean = (float)(tot / (double)C);
+      const float inv = 1.0f / sqrtf(mean + a.eps);
+      float v0[8], v1[8], xf[8], o[8];
+      if (UNIFORM) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          v0[i] = c0[i];
+          v1[i] = c1[i];
+        }
+      } else {
+        float tsv[8];
+        if (kPre) raw8_get<D0>(p0[kPre ? u : 0], tsv);
+        else load8_t<D0, false>(a.s0.ts, tsc0 + t * a.s0.ts_st, a.s0.ts_sc, tsv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float sum = tab0 ? c0[i] + tsv[i] : tsv[i];
+          v0[i] = (tab0 && B0) ? rbf(sum) : sum;
+        }
+        if (kPre) raw8_get<D1>(p1[kPre ? u : 0], tsv);
+        else load8_t<D1, false>(a.s1.ts, tsc1 + t * a.s1.ts_st, a.s1.ts_sc, tsv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float sum = tab1 ? c1[i] + tsv[i] : tsv[i];
+          if (tab1 && B1) sum = rbf(sum);
+          const float f = 1.0f + sum;
+          v1[i] = B1 ? rbf(f) : f;
+        }
+      }
+      unpack8(xv[u], xf);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float p = rbf(xf[i] * inv) * v1[i];
+        if (B1) p = rbf(p);
+        o[i] = p + v0[i];
+      }
+      st_nt16(a.out + (b * a.tokens + t) * C + col0, pack8(o));
+    }
+  }
+}
+
+// Grid of k_adazero: about OGA_ADA_WAVES_PER_CU waves per CU, blocks of
+// equal row counts.
+#ifndef OGA_ADA_WAVES_PER_CU
+#define OGA_ADA_WAVES_PER_CU 16
+#endif
+static void adazero_grid(int64_t batch, int64_t tokens, int ch, dim3& grid, int& rows_per_wg) {
+  const int64_t target_wgs = (int64_t)cu_count() * OGA_ADA_WAVES_PER_CU / ch;
+  int64_t per_batch = target_wgs / batch;
+  if (per_batch < 1) per_batch = 1;
+  int64_t rows = (tokens + per_batch - 1) / per_batch;
+  if (rows > kAdaRows) rows = kAdaRows;
+  rows_per_wg = (int)rows;
+  grid = dim3((unsigned)((tokens + rows - 1) / rows), (unsigned)batch);
+}
+
 // Grid of k_elem: groups of consecutive rows of equal size (about
 // OGA_ELEM_WAVES_PER_CU waves per CU in all), CH waves per group.
 static void elem_grid(int64_t batch, int64_t tokens, int ch, dim3& grid, int64_t& rows_per_group) {
@@ -541,11 +676,13 @@ static void launch_row_v(RowArgs& a, int64_t batch, bool vec, hipStream_t st) {
     else
       hipLaunchKernelGGL((k_elem<CH, OP, UNIFORM, D0, D1, false>), grid, dim3(256), 0, st, a, rpg);
   } else {
-    const dim3 grid = balanced_row_grid(batch, a.tokens);
+    dim3 grid;
+    int rpw = 0;
+    adazero_grid(batch, a.tokens, CH, grid, rpw);
     if (vec)
-      hipLaunchKernelGGL((k_row<CH, OP, UNIFORM, D0, D1, true>), grid, dim3(256), 0, st, a);
+      hipLaunchKernelGGL((k_adazero<CH, UNIFORM, D0, D1, true>), grid, dim3(64 * CH), 0, st, a, rpw);
     else
-      hipLaunchKernelGGL((k_row<CH, OP, UNIFORM, D0, D1, false>), grid, dim3(256), 0, st, a);
+      hipLaunchKernelGGL((k_adazero<CH, UNIFORM, D0, D1, false>), grid, dim3(64 * CH), 0, st, a, rpw);
   }
 }
 
