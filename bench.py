@@ -28,6 +28,7 @@ if ROOT not in sys.path:
 
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
 
 M, K, N = 9216, 4096, 16384
 
@@ -40,7 +41,7 @@ def _parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fused", action="store_true")
     ap.add_argument("--seed", type=int, default=20260100)
-    ap.add_argument("--only", choices=["gemm", "quant", "fused", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemm", "quant", "fused", "copy", "attention"], default=None,
                     help="run one workload --steps times and print its mean time (for profiler runs)")
     return ap.parse_args()
 
@@ -169,6 +170,56 @@ def fused_op_rows(seed: int) -> dict:
     return rows
 
 
+ATT_N, ATT_H, ATT_D = 9216, 32, 128
+
+
+def attention_rows(seed: int, reps: int = 10) -> dict:
+    """Dense video self-attention at 576p: q, k, v [1, 9216, 32, 128] bf16
+    ~N(0,1), softmax scale 1/sqrt(128); 4*N^2*H*D FLOP per call. Also the
+    per-head FP8 path (quantize Q/K/V per head, dequantize, attention)."""
+    import torch
+
+    from opengenie_amd import attention as A
+    from opengenie_amd import ltx_ops as L
+
+    g = _gen(seed + 5, "cuda")
+    q, k, v = (torch.randn((1, ATT_N, ATT_H, ATT_D), generator=g, device="cuda").to(torch.bfloat16) for _ in range(3))
+    flops = 4.0 * ATT_N * ATT_N * ATT_H * ATT_D
+    st = torch.cuda.current_stream()
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for _ in range(reps):
+            fn()
+        e1.record(st)
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1000.0 / reps
+
+    us = timed(lambda: A.flash_attn_func(q, k, v))
+    rows = {"bf16": {"shape": "q,k,v [1,9216,32,128]", "us": round(us, 1),
+                     "TFLOP/s": round(flops / (us * 1e-6) / 1e12, 1),
+                     "frac_bf16_peak": round(flops / (us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4)}}
+
+    def fp8_step():
+        q8, qs = L.fused_fp8_quantize_e4m3_per_head_4d(q)
+        k8, ks = L.fused_fp8_quantize_e4m3_per_head_4d(k)
+        v8, vs = L.fused_fp8_quantize_e4m3_per_head_4d(v)
+        return A.flash_attn_func(q8, k8, v8, q_descale=qs, k_descale=ks, v_descale=vs)
+
+    us8 = timed(fp8_step)
+    ref = A.flash_attn_func(q, k, v).float()
+    diff = (fp8_step().float() - ref).abs()
+    rows["fp8_per_head"] = {"us": round(us8, 1), "path": "per-head e4m3 quantize Q/K/V, dequantize, bf16 kernel",
+                            "err_vs_bf16": {"max_abs": round(float(diff.max()), 5),
+                                            "rms": round(float(diff.square().mean().sqrt()), 6),
+                                            "rms_over_ref_rms": round(float(diff.square().mean().sqrt() /
+                                                                            ref.square().mean().sqrt()), 4)}}
+    return rows
+
+
 def copy_reference() -> dict:
     """Achievable streaming bandwidth on this GPU: torch's device copy of a
     bf16 tensor (read + write), for calibration next to the fused ops."""
@@ -259,6 +310,9 @@ def main() -> None:
         return
     if args.only == "copy":
         print(json.dumps(copy_reference()))
+        return
+    if args.only == "attention":
+        print(json.dumps(attention_rows(args.seed)))
         return
     x, s_in, w, s_w, bias = make_fp8_linear_inputs(args.seed, dev)
     if args.only in ("gemm", "quant"):

@@ -182,6 +182,28 @@ int oga_fp8_linear(const void* a, int64_t lda, const void* w, int64_t ldw, const
                    int64_t m, int64_t n, int64_t k, void* stream);
 
 /*
+ * Dense non-causal attention: the video self-attention that the reference
+ * runs through FlashAttention-3 flash_attn_func(q, k, v) on [B, N, H, D]
+ * views (benchmarks/official_ltx23_benchmark.py:3294-3369).
+ * q [B, Nq, H, D], k/v [B, Nk, H, D], o [B, Nq, H, D] bf16, D == 128; each
+ * given by element strides (batch, token, head) with unit stride along D
+ * (multiples of 8, 16-byte aligned bases). o = softmax(q k^T * scale) v with
+ * float32 softmax and accumulation, P rounded to bf16 before the P.V product.
+ */
+int oga_attention(const void* q, const int64_t q_strides[3], const void* k, const int64_t k_strides[3],
+                  const void* v, const int64_t v_strides[3], void* o, const int64_t o_strides[3], int64_t batch,
+                  int64_t nq, int64_t nk, int64_t heads, int64_t head_dim, float softmax_scale, void* stream);
+
+/*
+ * FP8 inputs of the attention (benchmarks/official_ltx23_benchmark.py
+ * :3333-3340, descales from `fused_fp8_quantize_e4m3_per_head_4d`):
+ * out[b, n, h, :] = R(e4m3(x8[b, n, h, :]) * descale[b, h]) as bf16;
+ * x8/out contiguous [B, N, H, D], D a multiple of 16.
+ */
+int oga_fp8_dequant_per_head(const void* x8, const float* descale, void* out, int64_t batch, int64_t tokens,
+                             int64_t heads, int64_t head_dim, void* stream);
+
+/*
  * Conversion self-test: runs the device rounding primitives every kernel
  * uses on n float32 inputs: bf16_out[i] = bf16 bits of R(in[i]) and
  * e4m3_out[i] = e4m3fn(clamp(in[i], +-448)). No reference counterpart; it

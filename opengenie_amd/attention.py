@@ -1,0 +1,118 @@
+"""Dense video self-attention on MI355X: drop-in for the FlashAttention-3 call
+the reference makes in the LTX video self-attention.
+
+The reference replaces `ltx_core`'s `FlashAttention3.__call__(q, k, v, heads)`
+with a function that views q/k/v (B, N, H*D) as [B, N, H, D], calls
+`flash_attn_interface.flash_attn_func(q, k, v, q_descale=..., k_descale=...,
+v_descale=..., window_size=...)` and reshapes the [B, N, H, D] result back
+(benchmarks/official_ltx23_benchmark.py:3294-3369). FP8 inputs come from the
+per-head quantizer (`_to_fp8_per_head`, :3333-3340) with descales [B, H].
+
+`flash_attn_func` here takes the same arguments for the configuration the
+reference uses (non-causal, no window) and runs the gfx950 HIP kernel
+`oga_attention` on torch's current stream. Inputs the kernel does not cover
+(CPU tensors, head_dim != 128, causal or windowed attention, other dtypes)
+take torch's scaled_dot_product_attention, like the fused ops' torch paths;
+under OPENGENIE_AMD_STRICT=1 a GPU input that would fall back raises instead.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .ltx_ops import _fallback, _hip, _stream
+
+__all__ = ["flash_attn_func", "attention_video"]
+
+_FP8 = torch.float8_e4m3fn
+
+
+def _strides3(t: torch.Tensor):
+    return _lib.strides([t.stride(0), t.stride(1), t.stride(2)])
+
+
+def _kernel_ok(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
+    for t in (q, k, v):
+        if not t.is_cuda or t.ndim != 4 or t.shape[-1] != 128 or t.stride(-1) != 1:
+            return False
+        if any(s % 8 for s in t.stride()[:3]) or t.data_ptr() % 16:
+            return False
+    if q.shape[0] != k.shape[0] or k.shape != v.shape or q.shape[2] != k.shape[2]:
+        return False
+    return k.shape[1] > 0
+
+
+def _dequant(x: torch.Tensor, descale: torch.Tensor) -> torch.Tensor:
+    """e4m3 [B, N, H, D] with float32 descale [B, H] -> bf16, one rounding."""
+    b, n, h, d = x.shape
+    out = torch.empty((b, n, h, d), device=x.device, dtype=torch.bfloat16)
+    xc = x.contiguous()
+    ds = descale.to(torch.float32).reshape(b, h).contiguous()
+    _lib.call("oga_fp8_dequant_per_head", xc.data_ptr(), ds.data_ptr(), out.data_ptr(), b, n, h, d, _stream(x))
+    return out
+
+
+def _torch_attention(q, k, v, softmax_scale, causal):
+    qf, kf, vf = (t.float().transpose(1, 2) for t in (q, k, v))
+    o = torch.nn.functional.scaled_dot_product_attention(qf, kf, vf, is_causal=causal, scale=softmax_scale)
+    return o.transpose(1, 2).to(torch.bfloat16)
+
+
+def flash_attn_func(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    softmax_scale: float | None = None,
+    causal: bool = False,
+    q_descale: torch.Tensor | None = None,
+    k_descale: torch.Tensor | None = None,
+    v_descale: torch.Tensor | None = None,
+    window_size: tuple[int, int] = (-1, -1),
+    attention_chunk: int = 0,
+    num_splits: int = 1,
+    sm_margin: int = 0,
+) -> torch.Tensor:
+    """softmax(q k^T * scale) v for q [B, Nq, H, D], k/v [B, Nk, H, D] -> [B, Nq, H, D] bf16.
+
+    e4m3 inputs are dequantized with their [B, H] descales (value * descale,
+    rounded to bf16) before the bf16 kernel. `attention_chunk`, `num_splits`
+    and `sm_margin` are FA3 scheduling knobs with no effect on the result.
+    """
+    del attention_chunk, num_splits, sm_margin
+    if softmax_scale is None:
+        softmax_scale = q.shape[-1] ** -0.5
+    deq = []
+    for t, ds in ((q, q_descale), (k, k_descale), (v, v_descale)):
+        if t.dtype == _FP8:
+            if ds is None:
+                raise ValueError("float8_e4m3fn attention inputs need their descale")
+            if t.is_cuda and t.ndim == 4 and t.shape[-1] % 16 == 0:
+                _hip("fp8_dequant_per_head")
+                t = _dequant(t, ds)
+            else:
+                t = (t.float() * ds.float()[:, None, :, None]).to(torch.bfloat16)
+        deq.append(t)
+    q, k, v = deq
+    unsupported = causal or tuple(window_size) != (-1, -1)
+    if unsupported or any(t.dtype != torch.bfloat16 for t in (q, k, v)) or not _kernel_ok(q, k, v):
+        _fallback("flash_attn_func", q, k, v)
+        return _torch_attention(q, k, v, softmax_scale, causal)
+    b, nq, h, d = q.shape
+    nk = k.shape[1]
+    out = torch.empty((b, nq, h, d), device=q.device, dtype=torch.bfloat16)
+    _hip("flash_attn_func")
+    _lib.call("oga_attention", q.data_ptr(), _strides3(q), k.data_ptr(), _strides3(k), v.data_ptr(), _strides3(v),
+              out.data_ptr(), _strides3(out), b, nq, nk, h, d, float(softmax_scale), _stream(q))
+    return out
+
+
+def attention_video(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, heads: int, *,
+                    q_descale=None, k_descale=None, v_descale=None) -> torch.Tensor:
+    """`FlashAttention3.__call__(q, k, v, heads)` as patched by the reference
+    (official_ltx23_benchmark.py:3294-3369): (B, N, H*D) in and out."""
+    b = q.shape[0]
+    dim_head = q.shape[-1] // heads
+    qv, kv, vv = (t.view(b, -1, heads, dim_head) for t in (q, k, v))
+    out = flash_attn_func(qv, kv, vv, q_descale=q_descale, k_descale=k_descale, v_descale=v_descale)
+    return out.reshape(b, -1, heads * dim_head)

@@ -266,6 +266,14 @@ def video_qkv_rmsnorm_rope_pack(q: T, k: T, v: T, q_weight: T, k_weight: T, eps,
 # --------------------------------------------------------------------------
 # Dense attention
 # --------------------------------------------------------------------------
+def fp8_dequant_per_head(codes: np.ndarray, descale: np.ndarray) -> np.ndarray:
+    """e4m3 codes [B, N, H, D] times float32 descale [B, H], rounded to bf16
+    (the dequantization of FP8 attention inputs, official_ltx23_benchmark.py
+    :3333-3340 descales): R(float32(e4m3) * descale)."""
+    v = e4m3_decode(codes) * f32(descale)[:, None, :, None]
+    return bf16_round(f32(v))
+
+
 def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float | None = None) -> np.ndarray:
     """softmax(q k^T * scale) v in float64 for [B, H, N, D] arrays (non-causal)."""
     q = q.astype(np.float64)
