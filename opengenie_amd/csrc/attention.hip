@@ -23,8 +23,9 @@
 //    in registers for the whole key loop. Lane l then holds 16 scores of
 //    query l % 32 per block (keys 8g + 4(l/32) + r for accumulator 4g + r),
 //    so a query's max and sum need one exchange with lane l ^ 32.
-//  * online softmax in base 2 (the scale folded with log2 e), P rounded to
-//    bf16 as FlashAttention does before the P.V product.
+//  * online softmax in base 2 (the scale folded with log2 e) with lazy
+//    rescaling of O (only when a running max grows by more than 2^8), P
+//    rounded to bf16 as FlashAttention does before the P.V product.
 //  * O^T = V^T P^T as four 32-d x 32-query blocks over four 16-key chunks:
 //    operand B = P^T straight from the score accumulators, operand A = V^T
 //    read with ds_read_b64_tr_b16 (transposing reads) from the row-major V
@@ -68,31 +69,103 @@ OGA_DEVICE f32x16 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
 }
 
 // Byte offset of (key row r, element d) in a swizzled LDS tile.
-OGA_DEVICE int tile_off(int r, int d) { return r * 256 + ((((d >> 3) ^ (r & 15)) << 4) | ((d & 7) << 1)); }
+constexpr int tile_off(int r, int d) { return r * 256 + ((((d >> 3) ^ (r & 15)) << 4) | ((d & 7) << 1)); }
 
-OGA_DEVICE float exchange32(float v) { return __shfl_xor(v, 32); }
+// The kernel folds tile_off into per-lane bases plus immediate offsets:
+//  K fragment of lane (ql, hl), d-step s, key block j:
+//    j*8192 + ql*256 + ((2s ^ hl ^ (ql % 16)) << 4);
+//  V^T transposing read of lane (a4, j4, g2, hl), chunk c2, half u, d-block dblk:
+//    c2*4096 + u*2048 + y*256 + ((z ^ 4 (dblk ^ 2u)) << 4) + 8 (a4 & 1)
+//    with y = 4hl + j4, z = (2g2 + a4/2) ^ y.
+// Checked here for every lane and step.
+constexpr bool folded_offsets_match() {
+  for (int lane = 0; lane < 64; ++lane) {
+    const int hl = lane >> 5, ql = lane & 31;
+    for (int j = 0; j < 2; ++j)
+      for (int s = 0; s < 8; ++s)
+        if (tile_off(32 * j + ql, 16 * s + 8 * hl) != j * 8192 + ql * 256 + (((2 * s) ^ hl ^ (ql & 15)) << 4))
+          return false;
+    const int a4 = lane & 3, j4 = (lane & 15) >> 2, g2 = (lane >> 4) & 1;
+    const int y = 4 * hl + j4, z = (2 * g2 + (a4 >> 1)) ^ y;
+    for (int c2 = 0; c2 < 4; ++c2)
+      for (int u = 0; u < 2; ++u)
+        for (int dblk = 0; dblk < 4; ++dblk) {
+          const int want = tile_off(16 * c2 + 8 * u + 4 * hl + j4, 32 * dblk + 16 * g2 + 4 * a4);
+          const int got = c2 * 4096 + u * 2048 + y * 256 + ((z ^ (4 * (dblk ^ (2 * u)))) << 4) + (a4 & 1) * 8;
+          if (want != got) return false;
+        }
+  }
+  return true;
+}
+static_assert(folded_offsets_match(), "folded LDS offsets differ from tile_off");
 
 // DMA of one 64-key tile of K or V (bf16 rows of kAD elements) into LDS:
 // instruction i of wave w fills tile rows 4b .. 4b+3 (b = 4w + i); lane p
 // writes the 16 bytes at row 4b + p/16, physical chunk p%16, i.e. logical
-// chunk (p%16) ^ (row%16). Rows past the last key re-read the last key.
-OGA_DEVICE void tile_dma(const uint16_t* base, int64_t row_stride, int64_t key0, int64_t nk, uint4* dst, int wv,
-                         int lane) {
+// chunk (p%16) ^ (row%16). `off[i]` is that source's byte offset from the
+// tile's first key row; in the last, partial step rows past the last key
+// re-read the last key.
+struct TileSrc {
+  uint32_t off[4];
+};
+OGA_DEVICE TileSrc tile_src(int64_t row_stride, int64_t first_key, int64_t nk, int wv, int lane, bool clamp) {
+  TileSrc t;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int blk = wv * 4 + i;
-    const int row = blk * 4 + (lane >> 4);
+    const int row = (wv * 4 + i) * 4 + (lane >> 4);
     const int chunk = (lane & 15) ^ (row & 15);
-    const int64_t key = min(key0 + row, nk - 1);
-    __builtin_amdgcn_global_load_lds((const void*)(base + key * row_stride + chunk * 8), (lds_void*)(dst + blk * 64),
-                                     16, 0, 0);
+    const int64_t r = clamp ? min((int64_t)row, nk - 1 - first_key) : (int64_t)row;
+    t.off[i] = (uint32_t)(r * row_stride * 2 + chunk * 16);
   }
+  return t;
+}
+OGA_DEVICE void tile_dma(const char* tile_base, const TileSrc& t, uint4* dst, int wv) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    __builtin_amdgcn_global_load_lds((const void*)(tile_base + t.off[i]), (lds_void*)(dst + (wv * 4 + i) * 64), 16,
+                                     0, 0);
 }
 
 OGA_DEVICE uint32_t pack2(float a, float b) { return pack_bf16(a, b); }
 
-__global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
-  __shared__ uint4 sK0[kATileU4], sV0[kATileU4], sK1[kATileU4], sV1[kATileU4];
+// LDS reads issued as inline assembly with immediate offsets, so that groups
+// of them stay in flight together and need no address arithmetic;
+// OGA_LGKM names the registers a wait makes valid.
+template <int OFF>
+OGA_DEVICE bf16x8 lds_b128(uint32_t addr) {
+  uint4 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return __builtin_bit_cast(bf16x8, v);
+}
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+template <int OFF>
+OGA_DEVICE u32x2 lds_tr16(uint32_t addr) {
+  u32x2 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return v;
+}
+#define OGA_LGKM(N, ...) asm volatile("s_waitcnt lgkmcnt(" #N ")" : __VA_ARGS__)
+
+// max / sum of a value over lanes l and l ^ 32 (v_permlane32_swap).
+OGA_DEVICE float max_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+OGA_DEVICE float sum_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <int N>
+struct IC {
+  static constexpr int value = N;
+};
+
+// LDS: [K0 | V0 | K1 | V1], 16 KiB each; step st uses buffer pair st % 2.
+constexpr int kKBuf = 0, kVBuf = 16384, kParBytes = 32768;
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attention(AttnArgs a) {
+  __shared__ uint4 smem[4 * kATileU4];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int h = blockIdx.y;
@@ -120,104 +193,177 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[i][e] = 0.0f;
+  // m_run: running max of the scaled (base-2) scores of query q0 + ql;
+  // l_run: this lane's part of the running sum (keys of lane half hl).
   float m_run = -INFINITY, l_run = 0.0f;
 
-  tile_dma(kbase, a.k_sn, 0, a.nk, sK0, wv, lane);
-  tile_dma(vbase, a.v_sn, 0, a.nk, sV0, wv, lane);
+  const TileSrc ksrc = tile_src(a.k_sn, 0, a.nk, wv, lane, false);
+  const TileSrc vsrc = tile_src(a.v_sn, 0, a.nk, wv, lane, false);
+  auto dma_step = [&](int64_t s2, uint4* dK, uint4* dV) {
+    const int64_t key0 = s2 * kAK;
+    const char* kt = (const char*)(kbase + key0 * a.k_sn);
+    const char* vt = (const char*)(vbase + key0 * a.v_sn);
+    if (key0 + kAK <= a.nk) {
+      tile_dma(kt, ksrc, dK, wv);
+      tile_dma(vt, vsrc, dV, wv);
+    } else {
+      tile_dma(kt, tile_src(a.k_sn, key0, a.nk, wv, lane, true), dK, wv);
+      tile_dma(vt, tile_src(a.v_sn, key0, a.nk, wv, lane, true), dV, wv);
+    }
+  };
+  dma_step(0, smem, smem + kATileU4);
 
-  auto step = [&](const uint4* sK, const uint4* sV, uint4* nK, uint4* nV, int64_t st) {
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's DMA of step st landed
-    __syncthreads();                     // ... every wave's; the other buffers are free
-    if (st + 1 < nsteps) {
-      tile_dma(kbase, a.k_sn, (st + 1) * kAK, a.nk, nK, wv, lane);
-      tile_dma(vbase, a.v_sn, (st + 1) * kAK, a.nk, nV, wv, lane);
-    }
-    const char* kb = (const char*)sK;
-    // S^T blocks: key block j (keys 32j .. 32j+31), lane key row 32j + ql.
+  // LDS read addresses (tile_off with the XOR folded per lane):
+  //  K fragment (key row 32j + ql, d = 16s + 8hl): kaddr[s] + 8192 j;
+  //  V^T read (key row 16c2 + 8u + 4hl + j4, d = 32dblk + 16g2 + 4a4):
+  //  vaddr[dblk ^ 2u] + 4096 c2 + 2048 u.
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
+  uint32_t kaddr[8], vaddr[4];
+  {
+    const int x = hl ^ (ql & 15);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) kaddr[s] = lds0 + ql * 256 + (((2 * s) ^ x) << 4);
+    const int a4 = lane & 3, j4 = (lane & 15) >> 2, g2 = (lane >> 4) & 1;
+    const int y = 4 * hl + j4;
+    const int z = (2 * g2 + (a4 >> 1)) ^ y;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) vaddr[t] = lds0 + kVBuf + y * 256 + ((z ^ (4 * t)) << 4) + (a4 & 1) * 8;
+  }
+  // Key offset of accumulator e within a 32-key block, minus this lane's 4 hl.
+  const int hl4 = 4 * hl;
+
+  auto step = [&](auto par_c, int64_t st) {
+    constexpr int PAR = decltype(par_c)::value;
+    constexpr int KB = PAR * kParBytes + kKBuf;
+    constexpr int VB = PAR * kParBytes;  // vaddr already includes kVBuf
+    __syncthreads();  // this wave's DMA of step st landed (vmcnt(0)), and every wave's; other pair free
+    if (st + 1 < nsteps) dma_step(st + 1, smem + (2 - 2 * PAR) * kATileU4, smem + (3 - 2 * PAR) * kATileU4);
+
+    // S^T blocks: key block j (keys 32j .. 32j+31) x the wave's 32 queries.
     f32x16 sacc[2];
+    auto s_block = [&](auto j_c) {
+      constexpr int OFF = KB + 8192 * decltype(j_c)::value;
+      bf16x8 kf[8];
+      kf[0] = lds_b128<OFF>(kaddr[0]);
+      kf[1] = lds_b128<OFF>(kaddr[1]);
+      kf[2] = lds_b128<OFF>(kaddr[2]);
+      kf[3] = lds_b128<OFF>(kaddr[3]);
+      kf[4] = lds_b128<OFF>(kaddr[4]);
+      kf[5] = lds_b128<OFF>(kaddr[5]);
+      kf[6] = lds_b128<OFF>(kaddr[6]);
+      kf[7] = lds_b128<OFF>(kaddr[7]);
+      OGA_LGKM(0, "+v"(kf[0]), "+v"(kf[1]), "+v"(kf[2]), "+v"(kf[3]), "+v"(kf[4]), "+v"(kf[5]), "+v"(kf[6]),
+               "+v"(kf[7]));
+      f32x16 acc;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+      for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) sacc[j][e] = 0.0f;
-      const int r = 32 * j + ql;
+      for (int s = 0; s < 8; ++s) acc = mfma_bf16(kf[s], qf[s], acc);
+      return acc;
+    };
+    sacc[0] = s_block(IC<0>{});
+    sacc[1] = s_block(IC<1>{});
+    // V^T fragments of 16-key chunk C (4 d-blocks x 2 transposing reads).
+    auto read_v = [&](auto c_c, u32x2(&vr)[8]) {
+      constexpr int C = decltype(c_c)::value;
+      constexpr int OFF = VB + 4096 * C;
+      vr[0] = lds_tr16<OFF>(vaddr[0]);
+      vr[1] = lds_tr16<OFF + 2048>(vaddr[2]);
+      vr[2] = lds_tr16<OFF>(vaddr[1]);
+      vr[3] = lds_tr16<OFF + 2048>(vaddr[3]);
+      vr[4] = lds_tr16<OFF>(vaddr[2]);
+      vr[5] = lds_tr16<OFF + 2048>(vaddr[0]);
+      vr[6] = lds_tr16<OFF>(vaddr[3]);
+      vr[7] = lds_tr16<OFF + 2048>(vaddr[1]);
+    };
+    u32x2 vr0[8], vr1[8];
+    read_v(IC<0>{}, vr0);  // in flight under the softmax
+
+    // Keys past nk (last step only) get score -inf.
+    const int64_t rem64 = a.nk - st * kAK;
+    if (rem64 < kAK) {
+      const int remh = (int)rem64 - hl4;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const bf16x8 kf = __builtin_bit_cast(bf16x8, *(const uint4*)(kb + tile_off(r, 16 * s + 8 * hl)));
-        sacc[j] = mfma_bf16(kf, qf[s], sacc[j]);
-      }
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          if (32 * j + 8 * (e >> 2) + (e & 3) >= remh) sacc[j][e] = -INFINITY;
     }
-    // Scores in base 2; keys past nk masked.
-    const int64_t key0 = st * kAK;
-    float mx = -INFINITY;
+    float mx = sacc[0][0];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int key = 32 * j + 8 * (e >> 2) + 4 * hl + (e & 3);
-        float sv = sacc[j][e] * a.scale_log2;
-        if (key0 + key >= a.nk) sv = -INFINITY;
-        sacc[j][e] = sv;
-        mx = fmaxf(mx, sv);
-      }
-    mx = fmaxf(mx, exchange32(mx));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = exp2f(m_run - m_new);  // 0 on the first step (m_run = -inf)
-    float psum = 0.0f;
-    uint32_t pb[2][8];  // P as packed bf16: block j, 8 words (16 values)
+      for (int e = (j == 0 ? 1 : 0); e < 16; ++e) mx = __builtin_fmaxf(mx, sacc[j][e]);
+    // Base-2 scores s * scale_log2 (scale_log2 > 0, so the max commutes).
+    const float ms = max_halves(mx) * a.scale_log2;
+    // Lazy rescaling: m_run moves only when some query of the wave sees a
+    // score more than 8 above it (always on the first step), so
+    // P = 2^(s - m_run) <= 256 and O, l are rescaled rarely.
+    if (__any(ms > m_run + 8.0f)) {
+      const float m_new = __builtin_fmaxf(m_run, ms);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first step (m_run = -inf)
+      l_run *= alpha;
+      m_run = m_new;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
+    }
+    // P = 2^(s scale_log2 - m_run): the float32 values feed l, their bf16
+    // roundings feed the P.V product (as FlashAttention does).
+    const float nm = -m_run;
+    uint32_t pb[2][8];
+    float ps0 = 0.0f, ps1 = 0.0f;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int e = 0; e < 16; e += 2) {
-        const float p0 = rbf(exp2f(sacc[j][e] - m_new));
-        const float p1 = rbf(exp2f(sacc[j][e + 1] - m_new));
-        psum += p0 + p1;
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j][e], a.scale_log2, nm));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j][e + 1], a.scale_log2, nm));
+        ps0 += p0;
+        ps1 += p1;
         pb[j][e >> 1] = pack2(p0, p1);
       }
-    psum += exchange32(psum);
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
+    l_run += ps0 + ps1;
 
-    // O^T += V^T P^T over 16-key chunks c2 (keys 16 c2 .. 16 c2 + 15).
-    const int a4 = lane & 3, j4 = (lane & 15) >> 2, g2 = (lane >> 4) & 1;
-    const char* vb = (const char*)sV;
-#pragma unroll
-    for (int c2 = 0; c2 < 4; ++c2) {
-      // B = P^T: accumulators 8(c2 % 2) .. +7 of block c2 / 2.
-      const uint32_t* pw = &pb[c2 >> 1][4 * (c2 & 1)];
-      uint4 pu;
-      pu.x = pw[0]; pu.y = pw[1]; pu.z = pw[2]; pu.w = pw[3];
+    // O^T += V^T P^T over 16-key chunks c2 (keys 16 c2 .. 16 c2 + 15); the
+    // next chunk's V^T reads go out before this chunk's MFMAs.
+    auto pv = [&](auto c_c, u32x2(&cur)[8], u32x2(&nxt)[8]) {
+      constexpr int C = decltype(c_c)::value;
+      if constexpr (C + 1 < 4) {
+        read_v(IC<C + 1>{}, nxt);
+        OGA_LGKM(8, "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3]), "+v"(cur[4]), "+v"(cur[5]),
+                 "+v"(cur[6]), "+v"(cur[7]));
+      } else {
+        OGA_LGKM(0, "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3]), "+v"(cur[4]), "+v"(cur[5]),
+                 "+v"(cur[6]), "+v"(cur[7]));
+      }
+      // B = P^T: accumulators 8(C % 2) .. +7 of block C / 2.
+      const uint32_t* pw = &pb[C >> 1][4 * (C & 1)];
+      const uint4 pu = {pw[0], pw[1], pw[2], pw[3]};
       const bf16x8 pf = __builtin_bit_cast(bf16x8, pu);
 #pragma unroll
       for (int dblk = 0; dblk < 4; ++dblk) {
-        // A = V^T: two transposing reads; read c supplies keys 16 c2 + 8c + 4 hl + j4
-        // at d = 32 dblk + 16 g2 + 4 a4 .. +3.
-        bf16x4 v0, v1;
-        {
-          const int d = 32 * dblk + 16 * g2 + 4 * a4;
-          const int r0 = 16 * c2 + 4 * hl + j4;
-          const int r1 = r0 + 8;
-          v0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(vb + tile_off(r0, d)));
-          v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(vb + tile_off(r1, d)));
-        }
-        const bf16x8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-        o[dblk] = mfma_bf16(vf, pf, o[dblk]);
+        const uint4 vu = {cur[2 * dblk][0], cur[2 * dblk][1], cur[2 * dblk + 1][0], cur[2 * dblk + 1][1]};
+        o[dblk] = mfma_bf16(__builtin_bit_cast(bf16x8, vu), pf, o[dblk]);
       }
-    }
+    };
+    pv(IC<0>{}, vr0, vr1);
+    pv(IC<1>{}, vr1, vr0);
+    pv(IC<2>{}, vr0, vr1);
+    pv(IC<3>{}, vr1, vr0);
   };
 
   for (int64_t st = 0; st < nsteps; st += 2) {
-    step(sK0, sV0, sK1, sV1, st);
-    if (st + 1 < nsteps) step(sK1, sV1, sK0, sV0, st + 1);
+    step(IC<0>{}, st);
+    if (st + 1 < nsteps) step(IC<1>{}, st + 1);
   }
 
   // O = O^T / l: lane holds query q0 + ql, d = 32 dblk + 8 (e/4) + 4 hl + e%4.
+  const float l_tot = sum_halves(l_run);
   const int64_t qi = q0 + ql;
   if (qi < a.nq) {
-    const float inv = 1.0f / l_run;
+    const float inv = 1.0f / l_tot;
     uint16_t* orow = a.o + b * a.o_sb + qi * a.o_sn + (int64_t)h * a.o_sh;
 #pragma unroll
     for (int dblk = 0; dblk < 4; ++dblk)
@@ -292,6 +438,7 @@ extern "C" int oga_attention(const void* q, const int64_t q_strides[3], const vo
       if (s[i] % 8) return fail("strides must be multiples of 8 elements");
   if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(o, 16))
     return fail("q/k/v/o must be 16-byte aligned");
+  if (!(softmax_scale > 0.0f) || !__builtin_isfinite(softmax_scale)) return unsupported("softmax_scale must be positive");
   AttnArgs a{};
   a.q = q; a.k = k; a.v = v; a.o = (uint16_t*)o;
   a.q_sb = q_strides[0]; a.q_sn = q_strides[1]; a.q_sh = q_strides[2];
