@@ -8,10 +8,13 @@ resident in HBM. The JSON line also carries:
   roofline      the FP8 GEMM kernel alone, timed with HIP events on its stream
   fused_ops     every fused elementwise/norm op at its own shape: achieved
                 HBM GB/s (algorithmic bytes / kernel time) and fraction of peak
+  attention     dense video self-attention q, k, v [1, 9216, 32, 128]: TFLOP/s
+                and fraction of the bf16 MFMA peak, plus the per-head FP8 path
   cpu_baseline  the numpy oracle of the same step on a bounded row sample,
                 on this host's cores
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-fused]
+       python bench.py --only {gemm,quant,fused,copy,attention}   (one part, for profiling)
 """
 
 from __future__ import annotations
@@ -31,6 +34,15 @@ FP8_PEAK_TFLOPS = 5000.0
 BF16_PEAK_TFLOPS = 2500.0
 
 M, K, N = 9216, 4096, 16384
+
+# HBM-side bytes per k_fp8_gemm launch at 9216 x 4096 -> 16384, from two
+# rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE) over
+# `bench.py --only gemm`, each scaled by what the same counter reads for an
+# eager 128 MiB device copy (`bench.py --only copy`): FETCH_SIZE x 2.000,
+# WRITE_SIZE x 1.000. Source: profiles/fp8_gemm_9216x4096x16384.txt.
+GEMM_TRAFFIC_FETCH = 1.7090e9
+GEMM_TRAFFIC_WRITE = 0.3020e9
+GEMM_ALGORITHMIC_BYTES = M * K + N * K + N * 2 + M * N * 2  # A, W, bias read once; out written once
 
 
 def _parse():
@@ -220,18 +232,35 @@ def attention_rows(seed: int, reps: int = 10) -> dict:
     return rows
 
 
-def copy_reference() -> dict:
+COPY_ELEMS = 64 * 1024 * 1024  # bf16 elements per calibration copy: 128 MiB read + 128 MiB written
+
+
+def copy_reference(graph: bool = True, reps: int = 10) -> dict:
     """Achievable streaming bandwidth on this GPU: torch's device copy of a
-    bf16 tensor (read + write), for calibration next to the fused ops."""
+    bf16 tensor (read + write), for calibration next to the fused ops. With
+    graph=False the copies are plain eager launches (one kernel each), the
+    known-size workload that scales the FETCH_SIZE / WRITE_SIZE counters."""
     import torch
 
     out = {}
-    for n in (37_748_736 // 2, 461_373_440 // 4):
+    sizes = (37_748_736 // 2, 461_373_440 // 4) if graph else (COPY_ELEMS,)
+    for n in sizes:
         a = torch.empty(n, device="cuda", dtype=torch.bfloat16).normal_()
         b = torch.empty_like(a)
-        us = _graph_time_us(lambda: b.copy_(a), reps=10, inner=10)
+        if graph:
+            us = _graph_time_us(lambda: b.copy_(a), reps=10, inner=10)
+        else:
+            st = torch.cuda.current_stream()
+            b.copy_(a)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            for _ in range(reps):
+                b.copy_(a)
+            e1.record(st)
+            e1.synchronize()
+            us = e0.elapsed_time(e1) * 1000.0 / reps
         gbs = 2 * n * 2 / (us * 1e-6) / 1e9
-        out[f"copy_{2 * n * 2 // 1_000_000}MB"] = {"us": round(us, 3), "GB/s": round(gbs, 1),
+        out[f"copy_{2 * n * 2 // 1_000_000}MB"] = {"bytes": 2 * n * 2, "us": round(us, 3), "GB/s": round(gbs, 1),
                                                     "frac": round(gbs / HBM_PEAK_GBS, 4)}
     return out
 
@@ -309,7 +338,7 @@ def main() -> None:
         print(json.dumps(fused_op_rows(args.seed)))
         return
     if args.only == "copy":
-        print(json.dumps(copy_reference()))
+        print(json.dumps(copy_reference(graph=False)))
         return
     if args.only == "attention":
         print(json.dumps(attention_rows(args.seed)))
@@ -372,6 +401,7 @@ def main() -> None:
     fused = {} if args.no_fused else fused_op_rows(args.seed)
     if fused:
         fused["copy_reference"] = copy_reference()
+    attention = {} if args.no_fused else attention_rows(args.seed)
     cpu = None if args.no_cpu else cpu_baseline(x, s_in, w, s_w, bias)
 
     line = {
@@ -392,8 +422,12 @@ def main() -> None:
                    "outliers": "0.1% x50"},
         "roofline": {"bound": "mfma", "kernel": "k_fp8_gemm", "achieved": round(achieved, 1),
                      "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
-                     "traffic": None, "us_per_launch": round(gemm_us, 2)},
+                     "traffic": GEMM_TRAFFIC_FETCH + GEMM_TRAFFIC_WRITE,
+                     "traffic_split": {"fetch": GEMM_TRAFFIC_FETCH, "write": GEMM_TRAFFIC_WRITE,
+                                       "algorithmic": GEMM_ALGORITHMIC_BYTES, "unit": "bytes/launch"},
+                     "us_per_launch": round(gemm_us, 2)},
         "fused_ops": fused,
+        "attention": attention,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

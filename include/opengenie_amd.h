@@ -174,7 +174,7 @@ int oga_video_qkv_rmsnorm_rope_pack(const void* q, const void* k, const void* v,
  * ldw (K-contiguous); scale_a, scale_b device float32 scalars.
  * out [M, N] bf16 (row stride ldo) = R(acc * (scale_a*scale_b)), then, if
  * bias (N,) is given, R(out + R(bias)) — the two roundings of `_scaled_mm`
- * followed by the separate bias add. K must be a multiple of 64; a, w rows
+ * followed by the separate bias add. K must be a multiple of 128; a, w rows
  * 16-byte aligned; out 16-byte aligned with ldo a multiple of 8.
  */
 int oga_fp8_linear(const void* a, int64_t lda, const void* w, int64_t ldw, const float* scale_a,

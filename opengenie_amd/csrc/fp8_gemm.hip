@@ -7,31 +7,39 @@
 //   out = R(acc * (scale_a * scale_b));  out = R(out + R(bias))  (if bias)
 // acc is the float32 sum over k of a[m,k]*w[n,k] (each product exact).
 //
-// Tiling (gfx950). A workgroup of 8 waves, two per SIMD, owns a 256 (M) x
-// 256 (N) output tile; wave (wm, wn) owns 128 (M) x 64 (N) of it as 2 x 4
-// blocks of v_mfma_f32_32x32x64_f8f6f4, whose 128 float32 accumulators per
-// lane live in the accumulation registers. K advances 64 bytes per step through a ring of
-// four LDS stages (4 x (256x64 A + 256x64 W) = 128 KiB) filled by LDS-DMA
-// (global_load_lds_dwordx4), so tiles never pass through VGPRs and three
-// steps of loads are in flight while one is consumed. Each stage is a
-// separate LDS object so the compiler can tell a DMA into one stage from the
-// fragment reads of another.
+// Tiling (gfx950). A workgroup of 4 waves, one per SIMD, owns a 256 (M) x
+// 256 (N) output tile; wave (wm, wn) owns 128 (M) x 128 (N) of it as 4 x 4
+// blocks of v_mfma_f32_32x32x64_f8f6f4, whose 256 float32 accumulators per
+// lane live in the accumulation registers. One MFMA step covers 64 bytes of
+// K; the operands move through LDS in slabs of 128 bytes of K (two steps)
+// and two slab buffers (2 x (256x128 A + 256x128 W) = 128 KiB), filled by
+// LDS-DMA (global_load_lds_dwordx4) so tiles never pass through VGPRs. Each
+// DMA instruction fetches eight whole 128-byte rows: full-line requests
+// halve the address and tag work of the load path compared with 64-byte
+// half lines.
 //
-// Per step (software-pipelined): 4 MFMAs on fragments read during the
-// previous step, then one barrier that publishes the next stage and
-// releases the previous one, the DMA for three steps ahead into the released
-// stage, and 4 more MFMAs under which the next step's fragments are read.
+// Step pair (2d, 2d+1) consumes slab d. Fragments are read one step ahead
+// (double-buffered in VGPRs) between the step's first eight MFMAs. At the
+// odd step 2d+1 every wave waits for its DMA of slab d+1 and joins one
+// barrier, which publishes slab d+1 and tells that every wave has finished
+// reading slab d (its last fragments were read during step 2d); the DMA of
+// slab d+2 then goes into slab d's buffer, spread one instruction per MFMA
+// over that step.
 //
-// LDS layout of an operand stage (256 rows x 64 bytes): four rows share one
-// 256-byte line of the 64 LDS banks, row m's 16-byte chunk k0 sitting at
-//   (m / 4) * 256 + ((4 * (m % 4) + k0) ^ ((m / 4) % 16)) * 16,
-// which makes the 128-bit fragment reads (32 rows x 2 chunks per
-// instruction) and the 1 KiB DMA writes free of bank conflicts.
+// LDS layout of an operand slab (256 rows x 128 bytes): two rows share one
+// 256-byte line of the 64 LDS banks; row r's 16-byte chunk c (c = 0..7)
+// sits at byte
+//   (r / 2) * 256 + ((8 * (r % 2) + c) ^ ((r / 2) % 8)) * 16,
+// which keeps the 128-bit fragment reads (32 rows x 2 chunks per
+// instruction) free of bank conflicts and lets each 1 KiB DMA write fill
+// four whole lines. The two A slabs fill LDS bytes [0, 64 KiB) and the two W
+// slabs [64 KiB, 128 KiB), so every fragment read is a per-lane base plus an
+// immediate offset.
 //
 // The weight tile is the MFMA's A operand and the activation tile its B
 // operand, so each lane's accumulators hold 4 consecutive output columns of
 // one output row per group. The epilogue stages each wave's finished bf16
-// block in LDS and writes whole 128-byte rows, so HBM sees full lines.
+// block in LDS and writes whole rows, so HBM sees full lines.
 // Workgroups are numbered so that the eight XCDs (which receive workgroups
 // round-robin) each own a contiguous, M-grouped range of tiles.
 #include "common.h"
@@ -39,17 +47,21 @@
 
 namespace oga {
 
-constexpr int GM = 256, GN = 256, GK = 64, NST = 4;
+constexpr int GM = 256, GN = 256;
+constexpr int GK = 64;                    // bytes of K per MFMA step
+constexpr int GKS = 128;                  // bytes of K per LDS slab (two steps)
 constexpr int kGroupM = 8;
-constexpr int kStageU4 = GM * GK / 16;  // uint4 per operand stage (1024 = 16 KiB)
-constexpr int kWaves = 8;
-// Epilogue staging: each wave's 128 x 64 bf16 block in LDS with a padded row
-// pitch (128 + 16 bytes) so the 8-byte writes of 32 rows hit distinct banks.
-constexpr int kOutPitch = 144;
+constexpr int kSlabBytes = GM * GKS;      // one operand slab: 32 KiB
+constexpr int kWBase = 2 * kSlabBytes;    // W slabs follow the two A slabs (64 KiB)
+constexpr int kWaves = 4;
+// Epilogue staging: each wave's 128 x 128 bf16 block in LDS with a padded row
+// pitch (256 + 16 bytes) so the 8-byte writes of 32 rows spread over the banks.
+constexpr int kOutPitch = 272;
 constexpr int kOutWaveBytes = 128 * kOutPitch;
-constexpr int kLdsU4 = (NST * 2 * kStageU4 > kWaves * kOutWaveBytes / 16) ? NST * 2 * kStageU4
-                                                                          : kWaves * kOutWaveBytes / 16;
-constexpr int kDmaPerOp = GM / 16 / kWaves;  // 1 KiB DMA instructions per wave per operand per stage
+constexpr int kLdsBytes = (4 * kSlabBytes > kWaves * kOutWaveBytes) ? 4 * kSlabBytes : kWaves * kOutWaveBytes;
+constexpr int kDmaPerOp = GM * GKS / 1024 / kWaves;  // 1 KiB DMA instructions per wave per operand per slab (8)
+static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+static_assert(kSlabBytes + 3 * 4096 < 65536, "fragment offsets must fit the 16-bit immediate");
 
 struct GemmArgs {
   const uint8_t* a;
@@ -67,14 +79,14 @@ struct GemmArgs {
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-// Byte offset in an operand stage of row m's 16-byte chunk k0.
-OGA_DEVICE int lds_pos(int m, int k0) { return (m >> 2) * 256 + (((m & 3) * 4 + k0) ^ ((m >> 2) & 15)) * 16; }
+// Byte offset in an operand slab of row r's 16-byte chunk c (0..7).
+constexpr int slab_pos(int r, int c) { return (r >> 1) * 256 + (((r & 1) * 8 + c) ^ ((r >> 1) & 7)) * 16; }
 
-// One 32-row MFMA operand fragment: lane l reads its row's logical chunks
-// 2h and 2h+1 (h = l / 32), at LDS byte addresses a0 + OFF and a1 + OFF.
-// The reads are issued as inline assembly so that the compiler, which does
-// not see them, adds no DMA-ordering waits of its own: the kernel orders LDS
-// explicitly (vmcnt before the barrier, lgkm_wait before the MFMAs).
+// One 32-row MFMA operand fragment: lane l reads 32 bytes of its row at LDS
+// byte addresses a0 + OFF and a1 + OFF. The reads are issued as inline
+// assembly so that the compiler, which does not see them, adds no
+// DMA-ordering waits of its own: the kernel orders LDS explicitly (vmcnt
+// before the barrier, OGA_LGKM_WAIT before the MFMAs).
 template <int OFF>
 OGA_DEVICE i32x8 frag(uint32_t a0, uint32_t a1) {
   uint4 lo, hi;
@@ -88,28 +100,54 @@ OGA_DEVICE i32x8 frag(uint32_t a0, uint32_t a1) {
 // s_waitcnt vmcnt(N) (expcnt/lgkmcnt left at their maxima); N < 64.
 #define OGA_WAIT_VM(N) __builtin_amdgcn_s_waitcnt(0x0F70 | ((N) & 15) | ((((N) >> 4) & 3) << 14))
 // s_waitcnt lgkmcnt(N) that also names the fragments it makes valid, so no
-// use of them can be scheduled before it; naming accumulators as well keeps
-// the MFMAs that update them from being scheduled after it.
+// use of them can be scheduled before it.
 #define OGA_LGKM_WAIT(N, ...) asm volatile("s_waitcnt lgkmcnt(" #N ")" : __VA_ARGS__)
 // Workgroup barrier without the release fence of __syncthreads(), which
-// would drain every outstanding DMA (vmcnt(0)) and empty the prefetch ring.
-// Callers first wait for their own DMA group and LDS reads; the memory
-// clobber keeps the compiler from moving memory accesses across it.
+// would also wait for every outstanding DMA. Callers first wait for their
+// own DMA and LDS reads; the memory clobber keeps the compiler from moving
+// memory accesses across it.
 #define OGA_BARRIER() asm volatile("s_barrier" ::: "memory")
 
 OGA_DEVICE f32x16 mfma(const i32x8& w, const i32x8& a, const f32x16& c) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w, a, c, 0, 0, 0, 0, 0, 0);
 }
 
-__global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2))) void k_fp8_gemm(
+template <int N>
+struct IC {
+  static constexpr int value = N;
+};
+
+// Fragment read addresses folded into per-lane bases (checked for every lane,
+// block, step parity and chunk pair): block b (rows 32b .. 32b+31), step
+// parity p (chunks 4p .. 4p+3), lane (fr, fh) reading chunk 4p + 2fh + q:
+//   slab_pos(32b + fr, 4p + 2fh + q)
+//     = 4096 b + (fr/2)*256 + (8 (fr%2) + ((4p + 2fh + q) ^ ((fr/2) % 8))) * 16.
+constexpr bool frag_bases_match() {
+  for (int lane = 0; lane < 64; ++lane) {
+    const int fr = lane & 31, fh = lane >> 5;
+    for (int b = 0; b < 8; ++b)
+      for (int p = 0; p < 2; ++p)
+        for (int q = 0; q < 2; ++q) {
+          const int c = 4 * p + 2 * fh + q;
+          const int got = 4096 * b + (fr >> 1) * 256 + (8 * (fr & 1) + (c ^ ((fr >> 1) & 7))) * 16;
+          if (slab_pos(32 * b + fr, c) != got) return false;
+        }
+  }
+  return true;
+}
+static_assert(frag_bases_match(), "folded fragment addresses differ from slab_pos");
+
+// ODD: the slab count K / 128 is odd (slab 0 then runs alone before the
+// slab pairs); each instantiation is one straight path plus one loop.
+template <bool ODD>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1))) void k_fp8_gemm(
     GemmArgs g) {
-  // Stage s: A tile at uint4 [2s*kStageU4, (2s+1)*kStageU4), W tile after it.
-  __shared__ uint4 smem[kLdsU4];
+  __shared__ uint4 smem[kLdsBytes / 16];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
-  const int wm = wv >> 2, wn = wv & 3;
+  const int wm = wv >> 1, wn = wv & 1;
 
   // Tile index: XCD-contiguous ranges, M-grouped inside each range.
   const int nt = g.tiles_m * g.tiles_n;
@@ -123,157 +161,179 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_pe
   const int tn = (t % per_group) / gsize;
   const int64_t m0 = (int64_t)tm * GM, n0 = (int64_t)tn * GN;
 
-  // DMA: instruction i of this wave fills stage rows 16b .. 16b+15 of an
-  // operand (b = kDmaPerOp*wave + i), i.e. 1 KiB = LDS lines 4b .. 4b+3;
-  // lane p writes the 16 bytes at line 4b + p/16, chunk position p%16, which
-  // by the layout above hold row 4*(4b + p/16) + kc/4, chunk kc%4 with
-  // kc = (p%16) ^ ((4b + p/16) % 16). Rows past the matrix edge re-read
-  // its last row (their results are never stored). Offsets are bytes from
-  // the tile's first row.
+  // DMA: instruction i of this wave fills slab rows 8b .. 8b+7 of an operand
+  // (b = kDmaPerOp*wave + i), i.e. 1 KiB = LDS lines 4b .. 4b+3; lane p
+  // writes the 16 bytes at line L = 4b + p/16, position p%16, which by the
+  // layout hold row 2L + v/8, chunk v%8 with v = (p%16) ^ (L%8): the eight
+  // lanes of each row cover its whole 128-byte line. Rows past the matrix
+  // edge re-read its last row (their results are never stored). Offsets are
+  // bytes from the tile's first row.
   uint32_t a_off[kDmaPerOp], w_off[kDmaPerOp];
 #pragma unroll
   for (int i = 0; i < kDmaPerOp; ++i) {
     const int line = (wv * kDmaPerOp + i) * 4 + (lane >> 4);
-    const int kc = (lane & 15) ^ (line & 15);
-    const int row = line * 4 + (kc >> 2);
-    const int lc = kc & 3;
+    const int v = (lane & 15) ^ (line & 7);
+    const int row = 2 * line + (v >> 3);
+    const int c = v & 7;
     const int64_t ar = min((int64_t)row, (int64_t)g.m - 1 - m0);
     const int64_t wr = min((int64_t)row, (int64_t)g.n - 1 - n0);
-    a_off[i] = (uint32_t)(ar * g.lda + lc * 16);
-    w_off[i] = (uint32_t)(wr * g.ldw + lc * 16);
+    a_off[i] = (uint32_t)(ar * g.lda + c * 16);
+    w_off[i] = (uint32_t)(wr * g.ldw + c * 16);
   }
   const uint8_t* abase = g.a + m0 * g.lda;
   const uint8_t* wbase = g.w + n0 * g.ldw;
-  const int ksteps = g.k / GK;  // >= 1
-  // K steps are visited in a rotated order, starting at an even step that
-  // depends on the tile, so that the workgroups of one XCD, which would
-  // otherwise all read the same 64-byte column of their rows at the same
-  // time, spread their requests over the L2 channels. (The float32 sum over K
-  // is taken in a different order; the result stays within the contract.)
-  const int rot = ((4 * t) % ksteps) & ~1;
-  const int klast = ksteps - 1;
-  auto kphys = [&](int step) -> uint32_t {  // byte offset of logical step (clamped to K)
-    int s2 = min(step, klast) + rot;
-    if (s2 >= ksteps) s2 -= ksteps;
-    return (uint32_t)s2 * GK;
+  const int ksteps = g.k / GK;  // even, >= 2
+  const int nslab = ksteps >> 1;
+  uint8_t* lds_bytes = (uint8_t*)smem;
+  // DMA instruction I (0..7: A, 8..15: W) of slab d into buffer B. Slabs
+  // past the last are clamped to it: such a DMA lands in a buffer that is
+  // never read again, and keeps every odd step on one path.
+  auto dma = [&](auto i_c, int B, int d) {
+    constexpr int I = decltype(i_c)::value;
+    // readfirstlane hides the slab offset from loop strength reduction,
+    // which would otherwise keep a 64-bit address per instruction live.
+    const uint32_t k0 = __builtin_amdgcn_readfirstlane((uint32_t)min(d, nslab - 1) * GKS);
+    const int blk = wv * kDmaPerOp + (I % kDmaPerOp);
+    if constexpr (I < kDmaPerOp)
+      __builtin_amdgcn_global_load_lds((const void*)(abase + (a_off[I] + k0)),
+                                       (lds_void*)(lds_bytes + B * kSlabBytes + blk * 1024), 16, 0, 0);
+    else
+      __builtin_amdgcn_global_load_lds((const void*)(wbase + (w_off[I - kDmaPerOp] + k0)),
+                                       (lds_void*)(lds_bytes + kWBase + B * kSlabBytes + blk * 1024), 16, 0, 0);
   };
-  // DMA of logical step `step` into stage S (one group = 2*kDmaPerOp
-  // instructions per wave; groups complete in issue order).
-  auto issue = [&](int S, int step) {
-    uint4* d = smem + S * 2 * kStageU4;
-    const uint32_t k0 = kphys(step);
-#pragma unroll
-    for (int i = 0; i < kDmaPerOp; ++i) {
-      const int blk = wv * kDmaPerOp + i;
-      __builtin_amdgcn_global_load_lds((const void*)(abase + (a_off[i] + k0)), (lds_void*)(d + blk * 64), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(wbase + (w_off[i] + k0)), (lds_void*)(d + kStageU4 + blk * 64),
-                                       16, 0, 0);
-    }
-  };
+  static_assert(kDmaPerOp == 8, "the DMA schedule below covers 8 instructions per operand");
 
-  // Fragment addressing: lane reads row (lane & 31) of a 32-row block,
-  // chunks 2h and 2h+1 (h = lane / 32). By the layout, block b's chunk
-  // positions depend on b's parity only, and blocks b and b + 2 are 4096
-  // bytes apart: so each lane keeps, per operand, the stage-0 byte addresses
-  // of its two chunks for an even and an odd block.
+  // Per-lane fragment bases (frag_bases_match): [parity][chunk of the pair].
+  // The wave's W blocks are 4wn + i and its A blocks 4wm + j (i, j = 0..3).
   const int fr = lane & 31, fh = lane >> 5;
-  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)smem;
-  const uint32_t wbyte = kStageU4 * 16;  // W follows A inside a stage
-  // W blocks of this wave: 2*wn + i (i = 0, 1); A blocks: 4*wm + j.
-  const uint32_t lw00 = lds0 + wbyte + wn * 4096 + lds_pos(fr, 2 * fh);
-  const uint32_t lw01 = lds0 + wbyte + wn * 4096 + lds_pos(fr, 2 * fh + 1);
-  const uint32_t lw10 = lds0 + wbyte + wn * 4096 + lds_pos(32 + fr, 2 * fh);
-  const uint32_t lw11 = lds0 + wbyte + wn * 4096 + lds_pos(32 + fr, 2 * fh + 1);
-  const uint32_t la00 = lds0 + wm * 8192 + lds_pos(fr, 2 * fh);
-  const uint32_t la01 = lds0 + wm * 8192 + lds_pos(fr, 2 * fh + 1);
-  const uint32_t la10 = lds0 + wm * 8192 + lds_pos(32 + fr, 2 * fh);
-  const uint32_t la11 = lds0 + wm * 8192 + lds_pos(32 + fr, 2 * fh + 1);
-  constexpr uint32_t kStageBytes = 2 * kStageU4 * 16;
-
-  f32x16 acc[2][4];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
+  uint32_t lw[2][2], la[2][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t in_line = (fr >> 1) * 256 + (8 * (fr & 1) + ((4 * p + 2 * fh + q) ^ ((fr >> 1) & 7))) * 16;
+      lw[p][q] = lds0 + kWBase + wn * 16384 + in_line;
+      la[p][q] = lds0 + wm * 16384 + in_line;
+    }
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  // Software pipeline. Stage s % NST holds step s. Entering step ks, the
-  // first fragment set (w0, w1, a0, a1) of ks is already being read; the
-  // step reads its a2, a3 under its first four MFMAs, then (if step ks + 1
-  // exists) waits for its own DMA of ks + 1, joins the barrier that
-  // publishes stage ks + 1 and releases stage ks - 1 (every wave finished
-  // reading it before its previous second half), sends the DMA of step
-  // ks + 3 into the released stage, and reads the first fragments of ks + 1
-  // under its last four MFMAs. DMA groups in flight at the barrier wait:
-  // ks + 1 and ks + 2, so vmcnt(2*kDmaPerOp) leaves ks + 1 complete.
-  // Steps past the end of K (when K is not a multiple of NST*GK) run their
-  // MFMAs on zeroed fragments, so the accumulators have one path.
-  issue(0, 0);
-  issue(1, 1);
-  issue(2, 2);
-  OGA_WAIT_VM(4 * kDmaPerOp);
+  // Fragments of buffer B, step parity P: W block i / A block j.
+#define OGA_FRAG_W(B, P, i) frag<(B) * kSlabBytes + (i) * 4096>(lw[P][0], lw[P][1])
+#define OGA_FRAG_A(B, P, j) frag<(B) * kSlabBytes + (j) * 4096>(la[P][0], la[P][1])
+
+  // Prologue: slabs 0 and 1 in flight, slab 0 published, step 0's fragments read.
+  auto issue_all = [&](int B, int d) {
+    dma(IC<0>{}, B, d);  dma(IC<1>{}, B, d);  dma(IC<2>{}, B, d);  dma(IC<3>{}, B, d);
+    dma(IC<4>{}, B, d);  dma(IC<5>{}, B, d);  dma(IC<6>{}, B, d);  dma(IC<7>{}, B, d);
+    dma(IC<8>{}, B, d);  dma(IC<9>{}, B, d);  dma(IC<10>{}, B, d); dma(IC<11>{}, B, d);
+    dma(IC<12>{}, B, d); dma(IC<13>{}, B, d); dma(IC<14>{}, B, d); dma(IC<15>{}, B, d);
+  };
+  issue_all(0, 0);
+  issue_all(1, 1);
+  OGA_WAIT_VM(2 * kDmaPerOp);
   OGA_BARRIER();
-  i32x8 xw0 = frag<0>(lw00, lw01), xw1 = frag<0>(lw10, lw11);
-  i32x8 xa0 = frag<0>(la00, la01), xa1 = frag<0>(la10, la11);
-  i32x8 yw0, yw1, ya0, ya1;
+  i32x8 xw[4], xa[4], yw[4], ya[4];
+  xw[0] = OGA_FRAG_W(0, 0, 0);
+  xw[1] = OGA_FRAG_W(0, 0, 1);
+  xw[2] = OGA_FRAG_W(0, 0, 2);
+  xw[3] = OGA_FRAG_W(0, 0, 3);
+  xa[0] = OGA_FRAG_A(0, 0, 0);
+  xa[1] = OGA_FRAG_A(0, 0, 1);
+  xa[2] = OGA_FRAG_A(0, 0, 2);
+  xa[3] = OGA_FRAG_A(0, 0, 3);
+  OGA_LGKM_WAIT(0, "+v"(xw[0]), "+v"(xw[1]), "+v"(xw[2]), "+v"(xw[3]), "+v"(xa[0]), "+v"(xa[1]), "+v"(xa[2]),
+                "+v"(xa[3]));
 
-#define OGA_STEP(S, C, N)                                                                                      \
-  {                                                                                                            \
-    const int ks = kb + (S);                                                                                   \
-    const bool live = ks < ksteps;                                                                             \
-    const uint32_t so = (S) * kStageBytes;                                                                     \
-    i32x8 a2 = frag<4096>(la00 + so, la01 + so);                                                               \
-    i32x8 a3 = frag<4096>(la10 + so, la11 + so);                                                               \
-    OGA_LGKM_WAIT(4, "+v"(C##w0), "+v"(C##w1), "+v"(C##a0), "+v"(C##a1), "+v"(acc[0][2]), "+v"(acc[1][2]),     \
-                  "+v"(acc[0][3]), "+v"(acc[1][3]));                                                           \
-    if (!live) C##w0 = C##w1 = C##a0 = C##a1 = i32x8{0, 0, 0, 0, 0, 0, 0, 0};                                 \
-    acc[0][0] = mfma(C##w0, C##a0, acc[0][0]);                                                                 \
-    acc[1][0] = mfma(C##w1, C##a0, acc[1][0]);                                                                 \
-    acc[0][1] = mfma(C##w0, C##a1, acc[0][1]);                                                                 \
-    acc[1][1] = mfma(C##w1, C##a1, acc[1][1]);                                                                 \
-    if (ks + 1 < ksteps) {                                                                                     \
-      OGA_WAIT_VM(2 * kDmaPerOp);                                                                              \
-      asm volatile("s_barrier"                                                                                 \
-                   : "+v"(acc[0][0]), "+v"(acc[1][0]), "+v"(acc[0][1]), "+v"(acc[1][1])                        \
-                   :                                                                                           \
-                   : "memory");                                                                                \
-      issue(((S) + 3) % NST, ks + 3);                                                                          \
-    }                                                                                                          \
-    const uint32_t sn = (((S) + 1) % NST) * kStageBytes;                                                       \
-    N##w0 = frag<0>(lw00 + sn, lw01 + sn);                                                                     \
-    N##w1 = frag<0>(lw10 + sn, lw11 + sn);                                                                     \
-    N##a0 = frag<0>(la00 + sn, la01 + sn);                                                                     \
-    N##a1 = frag<0>(la10 + sn, la11 + sn);                                                                     \
-    OGA_LGKM_WAIT(8, "+v"(a2), "+v"(a3), "+v"(acc[0][0]), "+v"(acc[1][0]), "+v"(acc[0][1]), "+v"(acc[1][1]));  \
-    if (!live) a2 = a3 = i32x8{0, 0, 0, 0, 0, 0, 0, 0};                                                       \
-    acc[0][2] = mfma(C##w0, a2, acc[0][2]);                                                                    \
-    acc[1][2] = mfma(C##w1, a2, acc[1][2]);                                                                    \
-    acc[0][3] = mfma(C##w0, a3, acc[0][3]);                                                                    \
-    acc[1][3] = mfma(C##w1, a3, acc[1][3]);                                                                    \
-  }
+#define OGA_MF(i, j) acc[i][j] = mfma(cw[i], ca[j], acc[i][j])
+  // Even step 2d (buffer B, parity 0): its 16 MFMAs, with the 8 fragments of
+  // step 2d+1 (same buffer, parity 1, published together with this one) read
+  // between the first eight.
+  auto even_step = [&](auto b_c, i32x8(&cw)[4], i32x8(&ca)[4], i32x8(&nw)[4], i32x8(&na)[4]) {
+    constexpr int B = decltype(b_c)::value;
+    OGA_MF(0, 0); nw[0] = OGA_FRAG_W(B, 1, 0); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(0, 1); nw[1] = OGA_FRAG_W(B, 1, 1); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(0, 2); nw[2] = OGA_FRAG_W(B, 1, 2); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(0, 3); nw[3] = OGA_FRAG_W(B, 1, 3); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 0); na[0] = OGA_FRAG_A(B, 1, 0); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 1); na[1] = OGA_FRAG_A(B, 1, 1); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 2); na[2] = OGA_FRAG_A(B, 1, 2); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 3); na[3] = OGA_FRAG_A(B, 1, 3); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(2, 0); OGA_MF(2, 1); OGA_MF(2, 2); OGA_MF(2, 3);
+    OGA_MF(3, 0); OGA_MF(3, 1); OGA_MF(3, 2); OGA_MF(3, 3);
+    __builtin_amdgcn_sched_barrier(0);
+    OGA_LGKM_WAIT(0, "+v"(nw[0]), "+v"(nw[1]), "+v"(nw[2]), "+v"(nw[3]), "+v"(na[0]), "+v"(na[1]), "+v"(na[2]),
+                  "+v"(na[3]));
+  };
+  // Odd step 2d+1 (buffer B): wait for this wave's DMA of slab d+1, barrier
+  // (slab d+1 published in buffer B^1; every wave done with buffer B), then
+  // its 16 MFMAs with the DMA of slab d+2 into buffer B one instruction
+  // after each, and the fragments of step 2d+2 (buffer B^1, parity 0) read
+  // between the first eight. (After the last step the reads re-read settled
+  // LDS or the clamped last slab; the values go unused.)
+  auto odd_step = [&](auto b_c, int d, i32x8(&cw)[4], i32x8(&ca)[4], i32x8(&nw)[4], i32x8(&na)[4]) {
+    constexpr int B = decltype(b_c)::value;
+    constexpr int BN = B ^ 1;
+    OGA_WAIT_VM(0);
+    OGA_BARRIER();
+    __builtin_amdgcn_sched_barrier(0);
+    const int dn = d + 2;
+    OGA_MF(0, 0); dma(IC<0>{}, B, dn);  nw[0] = OGA_FRAG_W(BN, 0, 0); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(0, 1); dma(IC<8>{}, B, dn);  nw[1] = OGA_FRAG_W(BN, 0, 1); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(0, 2); dma(IC<1>{}, B, dn);  nw[2] = OGA_FRAG_W(BN, 0, 2); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(0, 3); dma(IC<9>{}, B, dn);  nw[3] = OGA_FRAG_W(BN, 0, 3); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 0); dma(IC<2>{}, B, dn);  na[0] = OGA_FRAG_A(BN, 0, 0); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 1); dma(IC<10>{}, B, dn); na[1] = OGA_FRAG_A(BN, 0, 1); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 2); dma(IC<3>{}, B, dn);  na[2] = OGA_FRAG_A(BN, 0, 2); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 3); dma(IC<11>{}, B, dn); na[3] = OGA_FRAG_A(BN, 0, 3); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(2, 0); dma(IC<4>{}, B, dn);  __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(2, 1); dma(IC<12>{}, B, dn); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(2, 2); dma(IC<5>{}, B, dn);  __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(2, 3); dma(IC<13>{}, B, dn); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(3, 0); dma(IC<6>{}, B, dn);  __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(3, 1); dma(IC<14>{}, B, dn); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(3, 2); dma(IC<7>{}, B, dn);  __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(3, 3); dma(IC<15>{}, B, dn); __builtin_amdgcn_sched_barrier(0);
+    OGA_LGKM_WAIT(0, "+v"(nw[0]), "+v"(nw[1]), "+v"(nw[2]), "+v"(nw[3]), "+v"(na[0]), "+v"(na[1]), "+v"(na[2]),
+                  "+v"(na[3]));
+  };
+#undef OGA_MF
 
-  for (int kb = 0; kb < ksteps; kb += NST) {
-    OGA_STEP(0, x, y)
-    OGA_STEP(1, y, x)
-    OGA_STEP(2, x, y)
-    OGA_STEP(3, y, x)
+  // Slab d lives in buffer d % 2. With an odd slab count slab 0 runs alone,
+  // then slab pairs (d, d + 1) follow in buffers (1, 0); otherwise in (0, 1).
+  constexpr int B0 = ODD ? 1 : 0;
+  if constexpr (ODD) {
+    even_step(IC<0>{}, xw, xa, yw, ya);
+    odd_step(IC<0>{}, 0, yw, ya, xw, xa);
   }
-#undef OGA_STEP
-  OGA_LGKM_WAIT(0, "+v"(xw0), "+v"(xw1), "+v"(xa0), "+v"(xa1));
+  for (int d = ODD ? 1 : 0; d < nslab; d += 2) {
+    even_step(IC<B0>{}, xw, xa, yw, ya);
+    odd_step(IC<B0>{}, d, yw, ya, xw, xa);
+    even_step(IC<B0 ^ 1>{}, xw, xa, yw, ya);
+    odd_step(IC<B0 ^ 1>{}, d + 1, yw, ya, xw, xa);
+  }
+#undef OGA_FRAG_W
+#undef OGA_FRAG_A
 
   // Epilogue. Block (i, j): lane holds, for q in 0..3, output row
   // m = wm*128 + 32j + (lane & 31) of the tile and columns n .. n+3 with
-  // n = wn*64 + 32i + 8q + 4*(lane >> 5), in acc[i][j][4q .. 4q+3]. The
+  // n = wn*128 + 32i + 8q + 4*(lane >> 5), in acc[i][j][4q .. 4q+3]. The
   // finished bf16 values go to this wave's LDS block, and are then written
-  // to HBM as whole 128-byte rows, 16 bytes per lane.
-  OGA_WAIT_VM(0);  // the last (clamped) DMA groups land before LDS is reused
+  // to HBM as whole 256-byte rows, 16 bytes per lane.
+  OGA_WAIT_VM(0);  // no DMA is in flight into LDS that is about to be reused
   OGA_BARRIER();   // every wave has finished reading the stages
-  const float s = g.sa[0] * g.sb[0];
+  const float sc = g.sa[0] * g.sb[0];
   const bool has_bias = g.bias != nullptr;
   const uint32_t ob = lds0 + wv * kOutWaveBytes;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < 4; ++i) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int nl = i * 32 + q * 8 + 4 * fh;  // column inside the wave's block
@@ -281,7 +341,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_pe
       if (has_bias) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int64_t c = min(n0 + wn * 64 + nl + e, (int64_t)g.n - 1);
+          const int64_t c = min(n0 + wn * 128 + nl + e, (int64_t)g.n - 1);
           const float v = g.bias_dt == OGA_DT_BF16 ? __uint_as_float(((uint32_t)((const uint16_t*)g.bias)[c]) << 16)
                                                    : ((const float*)g.bias)[c];
           bv[e] = rbf(v);
@@ -292,7 +352,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_pe
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float v = rbf(acc[i][j][q * 4 + e] * s);
+          float v = rbf(acc[i][j][q * 4 + e] * sc);
           if (has_bias) v = v + bv[e];
           o[e] = v;
         }
@@ -305,12 +365,12 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_pe
     }
   }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  // Row r of the block: 8 lanes x 16 bytes; 8 rows per pass, 16 passes.
-  const int rsub = lane >> 3, cb = (lane & 7) * 8;  // column (bf16) inside the row
-  const int64_t ncol = n0 + wn * 64 + cb;
+  // Row r of the block: 16 lanes x 16 bytes; 4 rows per pass, 32 passes.
+  const int rsub = lane >> 4, cb = (lane & 15) * 8;  // column (bf16) inside the row
+  const int64_t ncol = n0 + wn * 128 + cb;
 #pragma unroll 4
-  for (int pass = 0; pass < 16; ++pass) {
-    const int r = pass * 8 + rsub;
+  for (int pass = 0; pass < 32; ++pass) {
+    const int r = pass * 4 + rsub;
     uint4 v;
     asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(ob + r * kOutPitch + cb * 2) : "memory");
     const int64_t mrow = m0 + wm * 128 + r;
@@ -338,7 +398,7 @@ extern "C" int oga_fp8_linear(const void* a, int64_t lda, const void* w, int64_t
   if (!a || !w || !scale_a || !scale_b || !out) return fail("null pointer");
   if (m < 0 || n < 0 || k < 0) return fail("bad shape");
   if (m == 0 || n == 0) return OGA_OK;
-  if (k == 0 || k % GK) return unsupported("K must be a positive multiple of %d (got %lld)", GK, (long long)k);
+  if (k == 0 || k % GKS) return unsupported("K must be a positive multiple of %d (got %lld)", GKS, (long long)k);
   if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX) return unsupported("dimension too large");
   if (lda < k || ldw < k || ldo < n) return fail("leading dimension smaller than the row");
   if (!aligned(a, 16) || !aligned(w, 16) || lda % 16 || ldw % 16) return fail("a/w rows must be 16-byte aligned");
@@ -366,6 +426,9 @@ extern "C" int oga_fp8_linear(const void* a, int64_t lda, const void* w, int64_t
   const int64_t nt = (int64_t)g.tiles_m * g.tiles_n;
   if (nt > INT32_MAX) return unsupported("too many tiles");
   g.xcd_remap = (nt % 8) == 0;
-  hipLaunchKernelGGL(k_fp8_gemm, dim3((unsigned)nt), dim3(64 * kWaves), 0, (hipStream_t)stream, g);
+  if ((k / GKS) % 2)
+    hipLaunchKernelGGL(k_fp8_gemm<true>, dim3((unsigned)nt), dim3(64 * kWaves), 0, (hipStream_t)stream, g);
+  else
+    hipLaunchKernelGGL(k_fp8_gemm<false>, dim3((unsigned)nt), dim3(64 * kWaves), 0, (hipStream_t)stream, g);
   return launch_status();
 }
