@@ -52,16 +52,18 @@ constexpr int GK = 64;                    // bytes of K per MFMA step
 constexpr int GKS = 128;                  // bytes of K per LDS slab (two steps)
 constexpr int kGroupM = 8;
 constexpr int kSlabBytes = GM * GKS;      // one operand slab: 32 KiB
-constexpr int kWBase = 2 * kSlabBytes;    // W slabs follow the two A slabs (64 KiB)
+constexpr int kABufs = 3, kWBufs = 2;     // slab buffers per operand
+constexpr int kWBase = kABufs * kSlabBytes;  // W buffers follow the A buffers (96 KiB)
 constexpr int kWaves = 4;
 // Epilogue staging: each wave's 128 x 128 bf16 block in LDS with a padded row
 // pitch (256 + 16 bytes) so the 8-byte writes of 32 rows spread over the banks.
 constexpr int kOutPitch = 272;
 constexpr int kOutWaveBytes = 128 * kOutPitch;
-constexpr int kLdsBytes = (4 * kSlabBytes > kWaves * kOutWaveBytes) ? 4 * kSlabBytes : kWaves * kOutWaveBytes;
+constexpr int kLdsBytes = ((kABufs + kWBufs) * kSlabBytes > kWaves * kOutWaveBytes) ? (kABufs + kWBufs) * kSlabBytes
+                                                                                    : kWaves * kOutWaveBytes;
 constexpr int kDmaPerOp = GM * GKS / 1024 / kWaves;  // 1 KiB DMA instructions per wave per operand per slab (8)
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
-static_assert(kSlabBytes + 3 * 4096 < 65536, "fragment offsets must fit the 16-bit immediate");
+static_assert(3 * 4096 < 65536, "fragment offsets must fit the 16-bit immediate");
 
 struct GemmArgs {
   const uint8_t* a;
@@ -137,9 +139,6 @@ constexpr bool frag_bases_match() {
 }
 static_assert(frag_bases_match(), "folded fragment addresses differ from slab_pos");
 
-// ODD: the slab count K / 128 is odd (slab 0 then runs alone before the
-// slab pairs); each instantiation is one straight path plus one loop.
-template <bool ODD>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1))) void k_fp8_gemm(
     GemmArgs g) {
   __shared__ uint4 smem[kLdsBytes / 16];
@@ -185,26 +184,34 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
   const int ksteps = g.k / GK;  // even, >= 2
   const int nslab = ksteps >> 1;
   uint8_t* lds_bytes = (uint8_t*)smem;
-  // DMA instruction I (0..7: A, 8..15: W) of slab d into buffer B. Slabs
-  // past the last are clamped to it: such a DMA lands in a buffer that is
-  // never read again, and keeps every odd step on one path.
-  auto dma = [&](auto i_c, int B, int d) {
+  // DMA instruction I (0..7) of operand A or W for slab d (< nslab) into
+  // byte offset `buf` of LDS.
+  auto dma = [&](auto i_c, auto w_c, uint32_t buf, int d) {
     constexpr int I = decltype(i_c)::value;
+    constexpr bool W = decltype(w_c)::value;
     // readfirstlane hides the slab offset from loop strength reduction,
     // which would otherwise keep a 64-bit address per instruction live.
-    const uint32_t k0 = __builtin_amdgcn_readfirstlane((uint32_t)min(d, nslab - 1) * GKS);
-    const int blk = wv * kDmaPerOp + (I % kDmaPerOp);
-    if constexpr (I < kDmaPerOp)
-      __builtin_amdgcn_global_load_lds((const void*)(abase + (a_off[I] + k0)),
-                                       (lds_void*)(lds_bytes + B * kSlabBytes + blk * 1024), 16, 0, 0);
+    const uint32_t k0 = __builtin_amdgcn_readfirstlane((uint32_t)d * GKS);
+    const int blk = wv * kDmaPerOp + I;
+    if constexpr (!W)
+      __builtin_amdgcn_global_load_lds((const void*)(abase + (a_off[I] + k0)), (lds_void*)(lds_bytes + buf + blk * 1024),
+                                       16, 0, 0);
     else
-      __builtin_amdgcn_global_load_lds((const void*)(wbase + (w_off[I - kDmaPerOp] + k0)),
-                                       (lds_void*)(lds_bytes + kWBase + B * kSlabBytes + blk * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(wbase + (w_off[I] + k0)), (lds_void*)(lds_bytes + buf + blk * 1024),
+                                       16, 0, 0);
   };
   static_assert(kDmaPerOp == 8, "the DMA schedule below covers 8 instructions per operand");
+  auto issue_all = [&](auto w_c, uint32_t buf, int d) {
+    dma(IC<0>{}, w_c, buf, d); dma(IC<1>{}, w_c, buf, d); dma(IC<2>{}, w_c, buf, d); dma(IC<3>{}, w_c, buf, d);
+    dma(IC<4>{}, w_c, buf, d); dma(IC<5>{}, w_c, buf, d); dma(IC<6>{}, w_c, buf, d); dma(IC<7>{}, w_c, buf, d);
+  };
+  // Buffers: A slab d in A buffer d % 3, W slab d in W buffer d % 2.
+  auto abuf = [&](int d) { return (uint32_t)((d % kABufs) * kSlabBytes); };
+  auto wbuf = [&](int d) { return (uint32_t)(kWBase + (d % kWBufs) * kSlabBytes); };
 
-  // Per-lane fragment bases (frag_bases_match): [parity][chunk of the pair].
-  // The wave's W blocks are 4wn + i and its A blocks 4wm + j (i, j = 0..3).
+  // Per-lane fragment bases (frag_bases_match): [parity][chunk of the pair],
+  // relative to the slab buffer. The wave's W blocks are 4wn + i and its A
+  // blocks 4wm + j (i, j = 0..3).
   const int fr = lane & 31, fh = lane >> 5;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
   uint32_t lw[2][2], la[2][2];
@@ -213,7 +220,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const uint32_t in_line = (fr >> 1) * 256 + (8 * (fr & 1) + ((4 * p + 2 * fh + q) ^ ((fr >> 1) & 7))) * 16;
-      lw[p][q] = lds0 + kWBase + wn * 16384 + in_line;
+      lw[p][q] = lds0 + wn * 16384 + in_line;
       la[p][q] = lds0 + wm * 16384 + in_line;
     }
 
@@ -225,100 +232,117 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  // Fragments of buffer B, step parity P: W block i / A block j.
-#define OGA_FRAG_W(B, P, i) frag<(B) * kSlabBytes + (i) * 4096>(lw[P][0], lw[P][1])
-#define OGA_FRAG_A(B, P, j) frag<(B) * kSlabBytes + (j) * 4096>(la[P][0], la[P][1])
+  // Fragments of step parity P from the slab buffers at byte offsets ab (A)
+  // and wb (W): W block i / A block j.
+#define OGA_FRAG_W(P, i) frag<(i) * 4096>(lw[P][0] + wb, lw[P][1] + wb)
+#define OGA_FRAG_A(P, j) frag<(j) * 4096>(la[P][0] + ab, la[P][1] + ab)
 
-  // Prologue: slabs 0 and 1 in flight, slab 0 published, step 0's fragments read.
-  auto issue_all = [&](int B, int d) {
-    dma(IC<0>{}, B, d);  dma(IC<1>{}, B, d);  dma(IC<2>{}, B, d);  dma(IC<3>{}, B, d);
-    dma(IC<4>{}, B, d);  dma(IC<5>{}, B, d);  dma(IC<6>{}, B, d);  dma(IC<7>{}, B, d);
-    dma(IC<8>{}, B, d);  dma(IC<9>{}, B, d);  dma(IC<10>{}, B, d); dma(IC<11>{}, B, d);
-    dma(IC<12>{}, B, d); dma(IC<13>{}, B, d); dma(IC<14>{}, B, d); dma(IC<15>{}, B, d);
-  };
-  issue_all(0, 0);
-  issue_all(1, 1);
-  OGA_WAIT_VM(2 * kDmaPerOp);
+  // Issue order of the DMA groups (8 instructions per wave each): A0 W0 A1
+  // W1 in the prologue, then A(d+2) at even step 2d and W(d+2) at odd step
+  // 2d+1. Prologue: slab 0 landed (A1, W1 may stay in flight), published,
+  // step 0's fragments read.
+  issue_all(IC<0>{}, abuf(0), 0);
+  issue_all(IC<1>{}, wbuf(0), 0);
+  if (nslab > 1) {
+    issue_all(IC<0>{}, abuf(1), 1);
+    issue_all(IC<1>{}, wbuf(1), 1);
+    OGA_WAIT_VM(2 * kDmaPerOp);
+  } else {
+    OGA_WAIT_VM(0);
+  }
   OGA_BARRIER();
   i32x8 xw[4], xa[4], yw[4], ya[4];
-  xw[0] = OGA_FRAG_W(0, 0, 0);
-  xw[1] = OGA_FRAG_W(0, 0, 1);
-  xw[2] = OGA_FRAG_W(0, 0, 2);
-  xw[3] = OGA_FRAG_W(0, 0, 3);
-  xa[0] = OGA_FRAG_A(0, 0, 0);
-  xa[1] = OGA_FRAG_A(0, 0, 1);
-  xa[2] = OGA_FRAG_A(0, 0, 2);
-  xa[3] = OGA_FRAG_A(0, 0, 3);
+  {
+    const uint32_t ab = abuf(0), wb = wbuf(0);
+    xw[0] = OGA_FRAG_W(0, 0);
+    xw[1] = OGA_FRAG_W(0, 1);
+    xw[2] = OGA_FRAG_W(0, 2);
+    xw[3] = OGA_FRAG_W(0, 3);
+    xa[0] = OGA_FRAG_A(0, 0);
+    xa[1] = OGA_FRAG_A(0, 1);
+    xa[2] = OGA_FRAG_A(0, 2);
+    xa[3] = OGA_FRAG_A(0, 3);
+  }
   OGA_LGKM_WAIT(0, "+v"(xw[0]), "+v"(xw[1]), "+v"(xw[2]), "+v"(xw[3]), "+v"(xa[0]), "+v"(xa[1]), "+v"(xa[2]),
                 "+v"(xa[3]));
 
 #define OGA_MF(i, j) acc[i][j] = mfma(cw[i], ca[j], acc[i][j])
-  // Even step 2d (buffer B, parity 0): its 16 MFMAs, with the 8 fragments of
-  // step 2d+1 (same buffer, parity 1, published together with this one) read
-  // between the first eight.
-  auto even_step = [&](auto b_c, i32x8(&cw)[4], i32x8(&ca)[4], i32x8(&nw)[4], i32x8(&na)[4]) {
-    constexpr int B = decltype(b_c)::value;
-    OGA_MF(0, 0); nw[0] = OGA_FRAG_W(B, 1, 0); __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(0, 1); nw[1] = OGA_FRAG_W(B, 1, 1); __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(0, 2); nw[2] = OGA_FRAG_W(B, 1, 2); __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(0, 3); nw[3] = OGA_FRAG_W(B, 1, 3); __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(1, 0); na[0] = OGA_FRAG_A(B, 1, 0); __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(1, 1); na[1] = OGA_FRAG_A(B, 1, 1); __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(1, 2); na[2] = OGA_FRAG_A(B, 1, 2); __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(1, 3); na[3] = OGA_FRAG_A(B, 1, 3); __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(2, 0); OGA_MF(2, 1); OGA_MF(2, 2); OGA_MF(2, 3);
-    OGA_MF(3, 0); OGA_MF(3, 1); OGA_MF(3, 2); OGA_MF(3, 3);
-    __builtin_amdgcn_sched_barrier(0);
+  // Even step 2d: its 16 MFMAs; the 8 fragments of step 2d+1 (same slab,
+  // parity 1, published with it) read between the first eight, and the DMA
+  // of A slab d+2 (into the A buffer of slab d-1, released by the barrier of
+  // step 2d-1) one instruction after each of the last eight.
+  // D: slab d + 2 exists (the last two slabs send no DMA).
+  auto even_step = [&](auto d_c, int d, i32x8(&cw)[4], i32x8(&ca)[4], i32x8(&nw)[4], i32x8(&na)[4]) {
+    constexpr bool D = decltype(d_c)::value;
+    const uint32_t ab = abuf(d), wb = wbuf(d), an = abuf(d + 2);
+    const int dn = d + 2;
+    OGA_MF(0, 0); nw[0] = OGA_FRAG_W(1, 0); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(0, 1); nw[1] = OGA_FRAG_W(1, 1); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(0, 2); nw[2] = OGA_FRAG_W(1, 2); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(0, 3); nw[3] = OGA_FRAG_W(1, 3); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 0); na[0] = OGA_FRAG_A(1, 0); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 1); na[1] = OGA_FRAG_A(1, 1); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 2); na[2] = OGA_FRAG_A(1, 2); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 3); na[3] = OGA_FRAG_A(1, 3); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(2, 0); if constexpr (D) dma(IC<0>{}, IC<0>{}, an, dn); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(2, 1); if constexpr (D) dma(IC<1>{}, IC<0>{}, an, dn); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(2, 2); if constexpr (D) dma(IC<2>{}, IC<0>{}, an, dn); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(2, 3); if constexpr (D) dma(IC<3>{}, IC<0>{}, an, dn); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(3, 0); if constexpr (D) dma(IC<4>{}, IC<0>{}, an, dn); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(3, 1); if constexpr (D) dma(IC<5>{}, IC<0>{}, an, dn); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(3, 2); if constexpr (D) dma(IC<6>{}, IC<0>{}, an, dn); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(3, 3); if constexpr (D) dma(IC<7>{}, IC<0>{}, an, dn); __builtin_amdgcn_sched_barrier(0);
     OGA_LGKM_WAIT(0, "+v"(nw[0]), "+v"(nw[1]), "+v"(nw[2]), "+v"(nw[3]), "+v"(na[0]), "+v"(na[1]), "+v"(na[2]),
                   "+v"(na[3]));
   };
-  // Odd step 2d+1 (buffer B): wait for this wave's DMA of slab d+1, barrier
-  // (slab d+1 published in buffer B^1; every wave done with buffer B), then
-  // its 16 MFMAs with the DMA of slab d+2 into buffer B one instruction
-  // after each, and the fragments of step 2d+2 (buffer B^1, parity 0) read
-  // between the first eight. (After the last step the reads re-read settled
-  // LDS or the clamped last slab; the values go unused.)
-  auto odd_step = [&](auto b_c, int d, i32x8(&cw)[4], i32x8(&ca)[4], i32x8(&nw)[4], i32x8(&na)[4]) {
-    constexpr int B = decltype(b_c)::value;
-    constexpr int BN = B ^ 1;
-    OGA_WAIT_VM(0);
+  // Odd step 2d+1: wait until this wave's A and W of slab d+1 landed (only
+  // A slab d+2, sent at step 2d, may stay in flight), barrier (slab d+1
+  // published; every wave done with slab d), then its 16 MFMAs with the
+  // fragments of step 2d+2 (slab d+1, parity 0) read between the first
+  // eight and the DMA of W slab d+2 (into slab d's W buffer) one instruction
+  // after each of the last eight. (After the last step the reads re-read
+  // settled LDS: every DMA has landed; the values go unused.)
+  auto odd_step = [&](auto d_c, int d, i32x8(&cw)[4], i32x8(&ca)[4], i32x8(&nw)[4], i32x8(&na)[4]) {
+    constexpr bool D = decltype(d_c)::value;
+    const uint32_t ab = abuf(d + 1), wb = wbuf(d + 1), wn2 = wbuf(d + 2);
+    const int dn = d + 2;
+    if constexpr (D) OGA_WAIT_VM(kDmaPerOp);
+    else OGA_WAIT_VM(0);  // no A slab d + 2 was sent
     OGA_BARRIER();
     __builtin_amdgcn_sched_barrier(0);
-    const int dn = d + 2;
-    OGA_MF(0, 0); dma(IC<0>{}, B, dn);  nw[0] = OGA_FRAG_W(BN, 0, 0); __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(0, 1); dma(IC<8>{}, B, dn);  nw[1] = OGA_FRAG_W(BN, 0, 1); __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(0, 2); dma(IC<1>{}, B, dn);  nw[2] = OGA_FRAG_W(BN, 0, 2); __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(0, 3); dma(IC<9>{}, B, dn);  nw[3] = OGA_FRAG_W(BN, 0, 3); __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(1, 0); dma(IC<2>{}, B, dn);  na[0] = OGA_FRAG_A(BN, 0, 0); __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(1, 1); dma(IC<10>{}, B, dn); na[1] = OGA_FRAG_A(BN, 0, 1); __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(1, 2); dma(IC<3>{}, B, dn);  na[2] = OGA_FRAG_A(BN, 0, 2); __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(1, 3); dma(IC<11>{}, B, dn); na[3] = OGA_FRAG_A(BN, 0, 3); __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(2, 0); dma(IC<4>{}, B, dn);  __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(2, 1); dma(IC<12>{}, B, dn); __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(2, 2); dma(IC<5>{}, B, dn);  __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(2, 3); dma(IC<13>{}, B, dn); __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(3, 0); dma(IC<6>{}, B, dn);  __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(3, 1); dma(IC<14>{}, B, dn); __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(3, 2); dma(IC<7>{}, B, dn);  __builtin_amdgcn_sched_barrier(0);
-    OGA_MF(3, 3); dma(IC<15>{}, B, dn); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(0, 0); nw[0] = OGA_FRAG_W(0, 0); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(0, 1); nw[1] = OGA_FRAG_W(0, 1); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(0, 2); nw[2] = OGA_FRAG_W(0, 2); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(0, 3); nw[3] = OGA_FRAG_W(0, 3); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 0); na[0] = OGA_FRAG_A(0, 0); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 1); na[1] = OGA_FRAG_A(0, 1); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 2); na[2] = OGA_FRAG_A(0, 2); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 3); na[3] = OGA_FRAG_A(0, 3); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(2, 0); if constexpr (D) dma(IC<0>{}, IC<1>{}, wn2, dn); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(2, 1); if constexpr (D) dma(IC<1>{}, IC<1>{}, wn2, dn); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(2, 2); if constexpr (D) dma(IC<2>{}, IC<1>{}, wn2, dn); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(2, 3); if constexpr (D) dma(IC<3>{}, IC<1>{}, wn2, dn); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(3, 0); if constexpr (D) dma(IC<4>{}, IC<1>{}, wn2, dn); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(3, 1); if constexpr (D) dma(IC<5>{}, IC<1>{}, wn2, dn); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(3, 2); if constexpr (D) dma(IC<6>{}, IC<1>{}, wn2, dn); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(3, 3); if constexpr (D) dma(IC<7>{}, IC<1>{}, wn2, dn); __builtin_amdgcn_sched_barrier(0);
     OGA_LGKM_WAIT(0, "+v"(nw[0]), "+v"(nw[1]), "+v"(nw[2]), "+v"(nw[3]), "+v"(na[0]), "+v"(na[1]), "+v"(na[2]),
                   "+v"(na[3]));
   };
 #undef OGA_MF
 
-  // Slab d lives in buffer d % 2. With an odd slab count slab 0 runs alone,
-  // then slab pairs (d, d + 1) follow in buffers (1, 0); otherwise in (0, 1).
-  constexpr int B0 = ODD ? 1 : 0;
-  if constexpr (ODD) {
-    even_step(IC<0>{}, xw, xa, yw, ya);
-    odd_step(IC<0>{}, 0, yw, ya, xw, xa);
+  int d = 0;
+  for (; d + 2 < nslab; ++d) {
+    even_step(IC<1>{}, d, xw, xa, yw, ya);
+    odd_step(IC<1>{}, d, yw, ya, xw, xa);
   }
-  for (int d = ODD ? 1 : 0; d < nslab; d += 2) {
-    even_step(IC<B0>{}, xw, xa, yw, ya);
-    odd_step(IC<B0>{}, d, yw, ya, xw, xa);
-    even_step(IC<B0 ^ 1>{}, xw, xa, yw, ya);
-    odd_step(IC<B0 ^ 1>{}, d + 1, yw, ya, xw, xa);
+  if (d + 1 < nslab) {
+    even_step(IC<0>{}, d, xw, xa, yw, ya);
+    odd_step(IC<0>{}, d, yw, ya, xw, xa);
+    ++d;
   }
+  even_step(IC<0>{}, d, xw, xa, yw, ya);
+  odd_step(IC<0>{}, d, yw, ya, xw, xa);
 #undef OGA_FRAG_W
 #undef OGA_FRAG_A
 
@@ -327,33 +351,74 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
   // n = wn*128 + 32i + 8q + 4*(lane >> 5), in acc[i][j][4q .. 4q+3]. The
   // finished bf16 values go to this wave's LDS block, and are then written
   // to HBM as whole 256-byte rows, 16 bytes per lane.
-  OGA_WAIT_VM(0);  // no DMA is in flight into LDS that is about to be reused
-  OGA_BARRIER();   // every wave has finished reading the stages
-  const float sc = g.sa[0] * g.sb[0];
+  //
+  // Bias: the lane's 16 groups of 4 consecutive columns, loaded before the
+  // DMA drain below so the two latencies overlap (one 8- or 16-byte load per
+  // group when the wave's 128 columns are inside N and the bias is aligned).
   const bool has_bias = g.bias != nullptr;
+  const int64_t ncol0 = n0 + wn * 128;  // first output column of the wave's block
+  float bv[4][4][4];
+  if (has_bias) {
+    const bool bf = g.bias_dt == OGA_DT_BF16;
+    const bool vec = ncol0 + 128 <= g.n && ((uintptr_t)g.bias % (bf ? 8 : 16)) == 0;
+    if (vec) {
+      if (bf) {
+        uint2 raw[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) raw[i][q] = *(const uint2*)((const uint16_t*)g.bias + ncol0 + i * 32 + q * 8 + 4 * fh);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            bv[i][q][0] = __uint_as_float(raw[i][q].x << 16);
+            bv[i][q][1] = __uint_as_float(raw[i][q].x & 0xFFFF0000u);
+            bv[i][q][2] = __uint_as_float(raw[i][q].y << 16);
+            bv[i][q][3] = __uint_as_float(raw[i][q].y & 0xFFFF0000u);
+          }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float4 f = *(const float4*)((const float*)g.bias + ncol0 + i * 32 + q * 8 + 4 * fh);
+            bv[i][q][0] = rbf(f.x);
+            bv[i][q][1] = rbf(f.y);
+            bv[i][q][2] = rbf(f.z);
+            bv[i][q][3] = rbf(f.w);
+          }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int64_t c = min(ncol0 + i * 32 + q * 8 + 4 * fh + e, (int64_t)g.n - 1);
+            const float v = bf ? __uint_as_float(((uint32_t)((const uint16_t*)g.bias)[c]) << 16)
+                               : ((const float*)g.bias)[c];
+            bv[i][q][e] = rbf(v);
+          }
+    }
+  }
+  const float sc = g.sa[0] * g.sb[0];
+  OGA_WAIT_VM(0);  // no DMA is in flight into LDS that is about to be reused
+  OGA_BARRIER();   // every wave has finished reading the slabs
   const uint32_t ob = lds0 + wv * kOutWaveBytes;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int nl = i * 32 + q * 8 + 4 * fh;  // column inside the wave's block
-      float bv[4] = {0.f, 0.f, 0.f, 0.f};
-      if (has_bias) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int64_t c = min(n0 + wn * 128 + nl + e, (int64_t)g.n - 1);
-          const float v = g.bias_dt == OGA_DT_BF16 ? __uint_as_float(((uint32_t)((const uint16_t*)g.bias)[c]) << 16)
-                                                   : ((const float*)g.bias)[c];
-          bv[e] = rbf(v);
-        }
-      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           float v = rbf(acc[i][j][q * 4 + e] * sc);
-          if (has_bias) v = v + bv[e];
+          if (has_bias) v = v + bv[i][q][e];
           o[e] = v;
         }
         uint2 pk;
@@ -365,24 +430,32 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
     }
   }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  // Row r of the block: 16 lanes x 16 bytes; 4 rows per pass, 32 passes.
+  // Row r of the block: 16 lanes x 16 bytes; 4 rows per pass, 32 passes in
+  // groups of 8 (8 LDS reads in flight, then 8 stores).
   const int rsub = lane >> 4, cb = (lane & 15) * 8;  // column (bf16) inside the row
-  const int64_t ncol = n0 + wn * 128 + cb;
-#pragma unroll 4
-  for (int pass = 0; pass < 32; ++pass) {
-    const int r = pass * 4 + rsub;
-    uint4 v;
-    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(ob + r * kOutPitch + cb * 2) : "memory");
-    const int64_t mrow = m0 + wm * 128 + r;
-    if (mrow < g.m) {
-      uint16_t* dst = g.out + mrow * g.ldo + ncol;
-      if (ncol + 8 <= g.n) {
-        *(uint4*)dst = v;
-      } else {
-        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+  const int64_t ncol = ncol0 + cb;
+  const uint32_t rd0 = ob + rsub * kOutPitch + cb * 2;
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (ncol + e < g.n) dst[e] = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
+  for (int grp8 = 0; grp8 < 4; ++grp8) {
+    u32x4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v[u]) : "v"(rd0), "i"((grp8 * 8 + u) * 4 * kOutPitch));
+    OGA_LGKM_WAIT(0, "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int r = (grp8 * 8 + u) * 4 + rsub;
+      const int64_t mrow = m0 + wm * 128 + r;
+      if (mrow < g.m) {
+        uint16_t* dst = g.out + mrow * g.ldo + ncol;
+        if (ncol + 8 <= g.n) {
+          *(u32x4*)dst = v[u];
+        } else {
+          const uint32_t w4[4] = {v[u][0], v[u][1], v[u][2], v[u][3]};
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (ncol + e < g.n) dst[e] = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
+        }
       }
     }
   }
@@ -426,9 +499,6 @@ extern "C" int oga_fp8_linear(const void* a, int64_t lda, const void* w, int64_t
   const int64_t nt = (int64_t)g.tiles_m * g.tiles_n;
   if (nt > INT32_MAX) return unsupported("too many tiles");
   g.xcd_remap = (nt % 8) == 0;
-  if ((k / GKS) % 2)
-    hipLaunchKernelGGL(k_fp8_gemm<true>, dim3((unsigned)nt), dim3(64 * kWaves), 0, (hipStream_t)stream, g);
-  else
-    hipLaunchKernelGGL(k_fp8_gemm<false>, dim3((unsigned)nt), dim3(64 * kWaves), 0, (hipStream_t)stream, g);
+  hipLaunchKernelGGL(k_fp8_gemm, dim3((unsigned)nt), dim3(64 * kWaves), 0, (hipStream_t)stream, g);
   return launch_status();
 }
