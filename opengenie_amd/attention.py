@@ -11,7 +11,8 @@ per-head quantizer (`_to_fp8_per_head`, :3333-3340) with descales [B, H].
 `flash_attn_func` here takes the same arguments for the configuration the
 reference uses (non-causal, no window) and runs the gfx950 HIP kernel
 `oga_attention` on torch's current stream. Inputs the kernel does not cover
-(CPU tensors, head_dim != 128, causal or windowed attention, other dtypes)
+(CPU tensors, head_dim != 128, causal or windowed attention, a softmax scale
+that is not positive, other dtypes)
 take torch's scaled_dot_product_attention, like the fused ops' torch paths;
 under OPENGENIE_AMD_STRICT=1 a GPU input that would fall back raises instead.
 """
@@ -94,7 +95,9 @@ def flash_attn_func(
                 t = (t.float() * ds.float()[:, None, :, None]).to(torch.bfloat16)
         deq.append(t)
     q, k, v = deq
-    unsupported = causal or tuple(window_size) != (-1, -1)
+    # The kernel takes the scale into its base-2 exponent with the running
+    # max, which needs a positive scale.
+    unsupported = causal or tuple(window_size) != (-1, -1) or not (0.0 < float(softmax_scale) < float("inf"))
     if unsupported or any(t.dtype != torch.bfloat16 for t in (q, k, v)) or not _kernel_ok(q, k, v):
         _fallback("flash_attn_func", q, k, v)
         return _torch_attention(q, k, v, softmax_scale, causal)

@@ -1,13 +1,15 @@
 // Token-row kernels: AdaZero (RMSNorm + Ada scale/shift) and the Ada-gated
 // elementwise fusions, for hidden sizes 2048 and 4096.
 //
-// Layout: one wavefront owns one token row at a time. Lane l of the wave owns
-// columns {j*512 + 8l .. j*512 + 8l + 7 : j < C/512}, so every HBM access is
-// a 128-bit load or store and the 64 lanes of one instruction cover 1 KiB of
-// contiguous memory. Per-column constants (table rows, bias, and, when the
-// timestep row is shared by all tokens, the finished Ada values) live in
-// registers for all rows the wave processes. The RMS reduction is a per-lane
-// float64 accumulation followed by a DPP/ds_swizzle butterfly.
+// Layout: a wave owns a 512-column chunk of token rows; lane l owns columns
+// chunk*512 + 8l .. +7, so every HBM access is a 128-bit load or store and
+// the 64 lanes of one instruction cover 1 KiB of contiguous memory.
+// Per-column constants (table rows, bias, and, when the timestep row is
+// shared by all tokens, the finished Ada values) are computed once per wave
+// into registers. k_elem (no row reduction) streams a group of rows per wave
+// with several rows' loads in flight and no LDS; k_adazero puts the CH
+// chunk-waves of a row block in one workgroup and combines their float64
+// partial sums of squares through LDS with one barrier.
 //
 // Reference semantics: ltx_serve/triton_ltx_ops.py :8-141 (AdaZero, AdaLN
 // affine), :204-262 (residual gate + bias), :590-611 (residual gate),
@@ -62,8 +64,8 @@ OGA_DEVICE void ada_value8(const AdaSrc& s, const float* tabv, int64_t b, int64_
 
 OGA_DEVICE int64_t wave_id() { return (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); }
 
-// ------------------------------------------------------------- row kernel
-// One kernel family for AdaZero and the Ada-gated elementwise ops:
+// ------------------------------------------------------------- row ops
+// One family for AdaZero and the Ada-gated elementwise ops:
 //   ADAZERO:    y = R( R?(n * R?(1 + scale)) + shift ),  n = R(x * inv_rms)
 //   ADALN:      y = R( R?(x * R?(1 + scale)) + shift )
 //   MUL:        y = R( x * gate )
@@ -71,13 +73,6 @@ OGA_DEVICE int64_t wave_id() { return (int64_t)blockIdx.x * (blockDim.x >> 6) + 
 //   RESID_BIAS: y = R( x + R?(R(y_in + R(bias)) * gate) )
 // R? rounds iff the Ada values are bf16 (torch: bf16 op bf16 -> bf16).
 // s0 is the shift (ADAZERO/ADALN) or the gate; s1 the scale.
-//
-// Grid (blocks_per_batch, batch): a workgroup of 4 waves owns tokens of one
-// batch. It first stages the per-column constants in LDS -- the finished Ada
-// values when the timestep row is shared by all tokens (UNIFORM), otherwise
-// the (rounded) table rows -- plus the rounded bias, then each wave streams
-// token rows: 8 (or 4) 128-bit loads per tensor row, constants read back
-// from LDS 8 columns at a time.
 enum RowOp { OP_ADAZERO = 0, OP_ADALN = 1, OP_MUL = 2, OP_RESID = 3, OP_RESID_BIAS = 4 };
 
 struct RowArgs {
@@ -98,196 +93,6 @@ struct RowTraits {
   static constexpr bool kY = OP == OP_RESID || OP == OP_RESID_BIAS;
   static constexpr bool kBias = OP == OP_RESID_BIAS;
 };
-
-OGA_DEVICE void lds_store8(float* s, int col0, const float* v) {
-  *(float4*)(s + col0) = make_float4(v[0], v[1], v[2], v[3]);
-  *(float4*)(s + col0 + 4) = make_float4(v[4], v[5], v[6], v[7]);
-}
-OGA_DEVICE void lds_load8(const float* s, int col0, float* v) {
-  const float4 a = *(const float4*)(s + col0);
-  const float4 b = *(const float4*)(s + col0 + 4);
-  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-}
-
-template <int CH, int OP, bool UNIFORM, int D0, int D1, bool VEC>
-__global__ __launch_bounds__(256) void k_row(RowArgs a) {
-  using Tr = RowTraits<OP>;
-  constexpr int C = CH * 512;
-  // torch dtypes of the two Ada values (s0: shift or gate, s1: scale); a
-  // product with a bf16 value is bf16, with a float32 value float32.
-  constexpr bool B0 = D0 == OGA_DT_BF16;
-  constexpr bool B1 = D1 == OGA_DT_BF16;
-  __shared__ float L0[C];
-  __shared__ float L1[Tr::kTwo ? C : 1];
-  __shared__ float LB[Tr::kBias ? C : 1];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int64_t b = blockIdx.y;
-  const int64_t step = (int64_t)gridDim.x * 4;
-  int64_t t = (int64_t)blockIdx.x * 4 + w;
-
-  // The first row's loads go out before the staging so their latency
-  // overlaps it.
-  uint4 xv[CH], yv[CH];
-  if (t < a.tokens) {
-    const int64_t r = b * a.tokens + t;
-#pragma unroll
-    for (int j = 0; j < CH; ++j) xv[j] = *(const uint4*)(a.x + r * C + j * 512 + lane * 8);
-    if (Tr::kY) {
-#pragma unroll
-      for (int j = 0; j < CH; ++j) yv[j] = *(const uint4*)(a.y + r * C + j * 512 + lane * 8);
-    }
-  }
-
-  // Stage per-column constants.
-#pragma unroll 1
-  for (int c0 = tid * 8; c0 < C; c0 += 256 * 8) {
-    float t[8], v[8];
-    ada_table8(a.s0, c0, t);
-    if (UNIFORM) {
-      ada_value8(a.s0, t, b, 0, c0, v);
-      lds_store8(L0, c0, v);
-    } else {
-      lds_store8(L0, c0, t);
-    }
-    if (Tr::kTwo) {
-      ada_table8(a.s1, c0, t);
-      if (UNIFORM) {
-        ada_value8(a.s1, t, b, 0, c0, v);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float f = 1.0f + v[i];
-          v[i] = B1 ? rbf(f) : f;
-        }
-        lds_store8(L1, c0, v);
-      } else {
-        lds_store8(L1, c0, t);
-      }
-    }
-    if (Tr::kBias) {
-      load8(a.bias, a.bias_dt, c0, 1, true, v);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = rbf(v[i]);
-      lds_store8(LB, c0, v);
-    }
-  }
-  __syncthreads();
-
-  const bool tab0 = a.s0.tab != nullptr;
-  const bool tab1 = a.s1.tab != nullptr;
-  // Per-token Ada rows are read with the row's other inputs, as loaded
-  // vectors, when their columns are contiguous (VEC); otherwise gathered
-  // where used.
-  constexpr bool kPre = !UNIFORM && VEC;
-  constexpr bool kPre1 = kPre && Tr::kTwo;
-  Raw8<D0> p0[kPre ? CH : 1];
-  Raw8<D1> p1[kPre1 ? CH : 1];
-  for (bool first = true; t < a.tokens; t += step, first = false) {
-    const int64_t r = b * a.tokens + t;
-    uint16_t* outr = a.out + r * C + lane * 8;
-    const int64_t ts0 = a.s0.ts_off + b * a.s0.ts_sb + t * a.s0.ts_st;
-    const int64_t ts1 = a.s1.ts_off + b * a.s1.ts_sb + t * a.s1.ts_st;
-    if (!first) {
-#pragma unroll
-      for (int j = 0; j < CH; ++j) xv[j] = *(const uint4*)(a.x + r * C + j * 512 + lane * 8);
-      if (Tr::kY) {
-#pragma unroll
-        for (int j = 0; j < CH; ++j) yv[j] = *(const uint4*)(a.y + r * C + j * 512 + lane * 8);
-      }
-    }
-    if (kPre) {
-#pragma unroll
-      for (int j = 0; j < CH; ++j) p0[j] = raw8_load<D0>(a.s0.ts, ts0 + (int64_t)(j * 512 + lane * 8));
-    }
-    if (kPre1) {
-#pragma unroll
-      for (int j = 0; j < CH; ++j) p1[j] = raw8_load<D1>(a.s1.ts, ts1 + (int64_t)(j * 512 + lane * 8));
-    }
-
-    float inv = 1.0f;
-    if (OP == OP_ADAZERO) {
-      double ss[4] = {0.0, 0.0, 0.0, 0.0};
-#pragma unroll
-      for (int j = 0; j < CH; ++j) {
-        float f[8];
-        unpack8(xv[j], f);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const double d = (double)f[i];
-          ss[i & 3] = fma(d, d, ss[i & 3]);
-        }
-      }
-      inv = rms_inv((ss[0] + ss[1]) + (ss[2] + ss[3]), C, a.eps);
-    }
-
-#pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      const int col0 = j * 512 + lane * 8;
-      float v0[8], v1[8], xf[8], o[8];
-      lds_load8(L0, col0, v0);
-      if (Tr::kTwo) lds_load8(L1, col0, v1);
-      if (!UNIFORM) {
-        float tsv[8];
-        if (kPre) {
-          raw8_get<D0>(p0[kPre ? j : 0], tsv);
-        } else {
-          load8_t<D0, false>(a.s0.ts, ts0 + (int64_t)col0 * a.s0.ts_sc, a.s0.ts_sc, tsv);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          float s = tab0 ? v0[i] + tsv[i] : tsv[i];
-          v0[i] = (tab0 && B0) ? rbf(s) : s;
-        }
-        if (Tr::kTwo) {
-          if (kPre1) {
-            raw8_get<D1>(p1[kPre1 ? j : 0], tsv);
-          } else {
-            load8_t<D1, false>(a.s1.ts, ts1 + (int64_t)col0 * a.s1.ts_sc, a.s1.ts_sc, tsv);
-          }
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            float s = tab1 ? v1[i] + tsv[i] : tsv[i];
-            if (tab1 && B1) s = rbf(s);
-            const float f = 1.0f + s;
-            v1[i] = B1 ? rbf(f) : f;
-          }
-        }
-      }
-      unpack8(xv[j], xf);
-      if (OP == OP_ADAZERO || OP == OP_ADALN) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float n = OP == OP_ADAZERO ? rbf(xf[i] * inv) : xf[i];
-          float p = n * v1[i];
-          if (B1) p = rbf(p);
-          o[i] = p + v0[i];
-        }
-      } else if (OP == OP_MUL) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = xf[i] * v0[i];
-      } else {
-        float yf[8], bb[8];
-        unpack8(yv[j], yf);
-        if (Tr::kBias) lds_load8(LB, col0, bb);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          float yy = yf[i];
-          if (Tr::kBias) yy = rbf(yy + bb[i]);
-          float p = yy * v0[i];
-          if (B0) p = rbf(p);
-          o[i] = xf[i] + p;
-        }
-      }
-      st_nt16(outr + j * 512, pack8(o));
-      // Keep each vector step's LDS constants live only within the step
-      // (the row's HBM inputs were all requested above).
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  }
-}
 
 // ------------------------------------------------------ elementwise ops
 // The Ada ops with no row reduction (AdaLN affine, mul, residual gates).

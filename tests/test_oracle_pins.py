@@ -294,3 +294,29 @@ def test_attention_matches_torch_sdpa_float64():
     v = randn((1, 2, 37, 64), 72, dtype=torch.float64)
     ref = torch.nn.functional.scaled_dot_product_attention(q, k, v).numpy()
     np.testing.assert_allclose(O.attention(q.numpy(), k.numpy(), v.numpy()), ref, rtol=1e-10, atol=1e-12)
+
+
+def test_attention_closed_forms():
+    """One key: every query returns that key's value. Identical keys: the
+    softmax is uniform, so every query returns the mean of the values."""
+    rng = np.random.default_rng(73)
+    q = rng.standard_normal((2, 3, 11, 64))
+    v1 = rng.standard_normal((2, 3, 1, 64))
+    k1 = rng.standard_normal((2, 3, 1, 64))
+    np.testing.assert_allclose(O.attention(q, k1, v1), np.broadcast_to(v1, q.shape), rtol=0, atol=1e-14)
+    k = np.repeat(rng.standard_normal((2, 3, 1, 64)), 9, axis=2)
+    v = rng.standard_normal((2, 3, 9, 64))
+    np.testing.assert_allclose(O.attention(q, k, v), np.broadcast_to(v.mean(axis=2, keepdims=True), q.shape),
+                               rtol=1e-12, atol=1e-12)
+
+
+def test_fp8_dequant_per_head_matches_torch():
+    """codes x descale with one rounding, against torch's own e4m3 decode."""
+    rng = np.random.default_rng(74)
+    codes = rng.integers(0, 256, size=(2, 5, 3, 16), dtype=np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0  # skip the NaN encodings
+    descale = (rng.random((2, 3)) * 0.1 + 1e-3).astype(np.float32)
+    t = torch.from_numpy(codes).view(torch.float8_e4m3fn).float()
+    ref = (t * torch.from_numpy(descale)[:, None, :, None]).to(torch.bfloat16).float().numpy()
+    got = O.fp8_dequant_per_head(codes, descale)
+    np.testing.assert_array_equal(np.asarray(got, dtype=np.float32), ref)
