@@ -32,8 +32,8 @@
 //    tile. The k-slot order of both operands is the same permutation of the
 //    16 keys of a chunk, so they pair up without moving P between lanes.
 // LDS tiles: key row r (256 bytes = 16 chunks of 16 B) keeps chunk c at
-// physical chunk c ^ (r % 16), so the 32-row fragment reads and the
-// transposing reads hit distinct bank groups.
+// physical chunk c ^ swz(r % 16), so both the 32-row fragment reads and the
+// transposing reads are free of bank conflicts.
 #include "common.h"
 #include "host.h"
 
@@ -68,41 +68,66 @@ OGA_DEVICE f32x16 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// Swizzle of key row r's 16 chunks: chunk c sits at physical chunk c ^ swz(r).
+// swz is a bijection on r % 16 (so the 16 rows a K fragment read takes
+// together hit 16 different 16-byte bank groups) whose bits 2-3 take four
+// different values over any four consecutive rows (so the 4 rows x 64 bytes
+// that 32 lanes of a transposing V read take together cover all 64 banks).
+constexpr int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 // Byte offset of (key row r, element d) in a swizzled LDS tile.
-constexpr int tile_off(int r, int d) { return r * 256 + ((((d >> 3) ^ (r & 15)) << 4) | ((d & 7) << 1)); }
+constexpr int tile_off(int r, int d) { return r * 256 + ((((d >> 3) ^ swz(r & 15)) << 4) | ((d & 7) << 1)); }
 
 // The kernel folds tile_off into per-lane bases plus immediate offsets:
 //  K fragment of lane (ql, hl), d-step s, key block j:
-//    j*8192 + ql*256 + ((2s ^ hl ^ (ql % 16)) << 4);
+//    j*8192 + ql*256 + ((2s ^ hl ^ swz(ql % 16)) << 4);
 //  V^T transposing read of lane (a4, j4, g2, hl), chunk c2, half u, d-block dblk:
-//    c2*4096 + u*2048 + y*256 + ((z ^ 4 (dblk ^ 2u)) << 4) + 8 (a4 & 1)
-//    with y = 4hl + j4, z = (2g2 + a4/2) ^ y.
+//    c2*4096 + u*2048 + (4hl + j4)*256
+//      + ((4 (dblk ^ j4) + ((2g2 + a4/2) ^ (2u + hl))) << 4) + 8 (a4 & 1).
 // Checked here for every lane and step.
+constexpr int v_fold(int lane, int u, int dblk) {
+  const int a4 = lane & 3, j4 = (lane & 15) >> 2, g2 = (lane >> 4) & 1, hl = lane >> 5;
+  return u * 2048 + (4 * hl + j4) * 256 + ((4 * (dblk ^ j4) + ((2 * g2 + (a4 >> 1)) ^ (2 * u + hl))) << 4) +
+         (a4 & 1) * 8;
+}
 constexpr bool folded_offsets_match() {
   for (int lane = 0; lane < 64; ++lane) {
     const int hl = lane >> 5, ql = lane & 31;
     for (int j = 0; j < 2; ++j)
       for (int s = 0; s < 8; ++s)
-        if (tile_off(32 * j + ql, 16 * s + 8 * hl) != j * 8192 + ql * 256 + (((2 * s) ^ hl ^ (ql & 15)) << 4))
+        if (tile_off(32 * j + ql, 16 * s + 8 * hl) != j * 8192 + ql * 256 + (((2 * s) ^ hl ^ swz(ql & 15)) << 4))
           return false;
     const int a4 = lane & 3, j4 = (lane & 15) >> 2, g2 = (lane >> 4) & 1;
-    const int y = 4 * hl + j4, z = (2 * g2 + (a4 >> 1)) ^ y;
     for (int c2 = 0; c2 < 4; ++c2)
       for (int u = 0; u < 2; ++u)
         for (int dblk = 0; dblk < 4; ++dblk) {
           const int want = tile_off(16 * c2 + 8 * u + 4 * hl + j4, 32 * dblk + 16 * g2 + 4 * a4);
-          const int got = c2 * 4096 + u * 2048 + y * 256 + ((z ^ (4 * (dblk ^ (2 * u)))) << 4) + (a4 & 1) * 8;
-          if (want != got) return false;
+          if (want != c2 * 4096 + v_fold(lane, u, dblk)) return false;
         }
   }
   return true;
 }
+// Bank check: the 32 lanes of a transposing read (one half, fixed chunk c2,
+// half u, d-block) read 32 distinct 8-byte pieces covering all 64 banks.
+constexpr bool v_reads_conflict_free() {
+  for (int half = 0; half < 2; ++half)
+    for (int u = 0; u < 2; ++u)
+      for (int dblk = 0; dblk < 4; ++dblk) {
+        unsigned long long banks = 0;
+        for (int l = 32 * half; l < 32 * half + 32; ++l) {
+          const int b = (v_fold(l, u, dblk) >> 2) & 63;
+          banks |= 3ull << b;
+        }
+        if (banks != ~0ull) return false;
+      }
+  return true;
+}
+static_assert(v_reads_conflict_free(), "transposing V reads would conflict");
 static_assert(folded_offsets_match(), "folded LDS offsets differ from tile_off");
 
 // DMA of one 64-key tile of K or V (bf16 rows of kAD elements) into LDS:
 // instruction i of wave w fills tile rows 4b .. 4b+3 (b = 4w + i); lane p
 // writes the 16 bytes at row 4b + p/16, physical chunk p%16, i.e. logical
-// chunk (p%16) ^ (row%16). `off[i]` is that source's byte offset from the
+// chunk (p%16) ^ swz(row%16). `off[i]` is that source's byte offset from the
 // tile's first key row; in the last, partial step rows past the last key
 // re-read the last key.
 struct TileSrc {
@@ -113,7 +138,7 @@ OGA_DEVICE TileSrc tile_src(int64_t row_stride, int64_t first_key, int64_t nk, i
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = (wv * 4 + i) * 4 + (lane >> 4);
-    const int chunk = (lane & 15) ^ (row & 15);
+    const int chunk = (lane & 15) ^ swz(row & 15);
     const int64_t r = clamp ? min((int64_t)row, nk - 1 - first_key) : (int64_t)row;
     t.off[i] = (uint32_t)(r * row_stride * 2 + chunk * 16);
   }
@@ -213,21 +238,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   };
   dma_step(0, smem, smem + kATileU4);
 
-  // LDS read addresses (tile_off with the XOR folded per lane):
+  // LDS read addresses (tile_off with the swizzle folded per lane):
   //  K fragment (key row 32j + ql, d = 16s + 8hl): kaddr[s] + 8192 j;
   //  V^T read (key row 16c2 + 8u + 4hl + j4, d = 32dblk + 16g2 + 4a4):
-  //  vaddr[dblk ^ 2u] + 4096 c2 + 2048 u.
+  //  vaddr[dblk][u] + 4096 c2 + 2048 u.
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
-  uint32_t kaddr[8], vaddr[4];
+  uint32_t kaddr[8], vaddr[4][2];
   {
-    const int x = hl ^ (ql & 15);
+    const int x = hl ^ swz(ql & 15);
 #pragma unroll
     for (int s = 0; s < 8; ++s) kaddr[s] = lds0 + ql * 256 + (((2 * s) ^ x) << 4);
     const int a4 = lane & 3, j4 = (lane & 15) >> 2, g2 = (lane >> 4) & 1;
-    const int y = 4 * hl + j4;
-    const int z = (2 * g2 + (a4 >> 1)) ^ y;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) vaddr[t] = lds0 + kVBuf + y * 256 + ((z ^ (4 * t)) << 4) + (a4 & 1) * 8;
+    for (int dblk = 0; dblk < 4; ++dblk)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        vaddr[dblk][u] = lds0 + kVBuf + (4 * hl + j4) * 256 +
+                         ((4 * (dblk ^ j4) + ((2 * g2 + (a4 >> 1)) ^ (2 * u + hl))) << 4) + (a4 & 1) * 8;
   }
   // Key offset of accumulator e within a 32-key block, minus this lane's 4 hl.
   const int hl4 = 4 * hl;
@@ -267,14 +294,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     auto read_v = [&](auto c_c, u32x2(&vr)[8]) {
       constexpr int C = decltype(c_c)::value;
       constexpr int OFF = VB + 4096 * C;
-      vr[0] = lds_tr16<OFF>(vaddr[0]);
-      vr[1] = lds_tr16<OFF + 2048>(vaddr[2]);
-      vr[2] = lds_tr16<OFF>(vaddr[1]);
-      vr[3] = lds_tr16<OFF + 2048>(vaddr[3]);
-      vr[4] = lds_tr16<OFF>(vaddr[2]);
-      vr[5] = lds_tr16<OFF + 2048>(vaddr[0]);
-      vr[6] = lds_tr16<OFF>(vaddr[3]);
-      vr[7] = lds_tr16<OFF + 2048>(vaddr[1]);
+      vr[0] = lds_tr16<OFF>(vaddr[0][0]);
+      vr[1] = lds_tr16<OFF + 2048>(vaddr[0][1]);
+      vr[2] = lds_tr16<OFF>(vaddr[1][0]);
+      vr[3] = lds_tr16<OFF + 2048>(vaddr[1][1]);
+      vr[4] = lds_tr16<OFF>(vaddr[2][0]);
+      vr[5] = lds_tr16<OFF + 2048>(vaddr[2][1]);
+      vr[6] = lds_tr16<OFF>(vaddr[3][0]);
+      vr[7] = lds_tr16<OFF + 2048>(vaddr[3][1]);
     };
     u32x2 vr0[8], vr1[8];
     read_v(IC<0>{}, vr0);  // in flight under the softmax
