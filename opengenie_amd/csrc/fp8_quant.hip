@@ -67,9 +67,8 @@ __global__ __launch_bounds__(256) void k_fp8_quant(const uint16_t* x, const floa
 // TPB/4 token rows; lane l of vector step j sees head (j*512 + 8l) / D.
 // partial[b, h, chunk] = max |x| over the block (a head's partials are
 // contiguous for the reduction in pass 2).
-template <int CH, int D>
-__global__ __launch_bounds__(256) void k_head_amax(const uint16_t* x, float* partial, int64_t tokens, int tpb,
-                                                   int nchunk) {
+template <int CH, int D, int TPB>
+__global__ __launch_bounds__(256) void k_head_amax(const uint16_t* x, float* partial, int64_t tokens, int nchunk) {
   constexpr int H = CH * 512 / D;
   constexpr int LPH = D / 8;  // lanes per head inside one vector step
   __shared__ float red[4][H];
@@ -79,16 +78,30 @@ __global__ __launch_bounds__(256) void k_head_amax(const uint16_t* x, float* par
   float m[CH];
 #pragma unroll
   for (int j = 0; j < CH; ++j) m[j] = 0.0f;
-  const int64_t t0 = (int64_t)chunk * tpb;
-  const int64_t t1 = min(t0 + tpb, tokens);
-  for (int64_t t = t0 + w; t < t1; t += 4) {
-    const uint16_t* row = x + (b * tokens + t) * (int64_t)(CH * 512);
+  // The wave's TPB/4 token rows (CH 16-byte loads each) are all in flight
+  // together before the maxima are taken.
+  const int64_t t0 = (int64_t)chunk * TPB;
+  constexpr int NR = TPB / 4;
+  uint4 xv[NR][CH];
 #pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      float f[8];
-      unpack8(*(const uint4*)(row + j * 512 + lane * 8), f);
+  for (int u = 0; u < NR; ++u) {
+    const int64_t t = t0 + w + 4 * u;
+    if (t < tokens) {
+      const uint16_t* row = x + (b * tokens + t) * (int64_t)(CH * 512);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) m[j] = fmaxf(m[j], fabsf(f[i]));
+      for (int j = 0; j < CH; ++j) xv[u][j] = *(const uint4*)(row + j * 512 + lane * 8);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < NR; ++u) {
+    if (t0 + w + 4 * u < tokens) {
+#pragma unroll
+      for (int j = 0; j < CH; ++j) {
+        float f[8];
+        unpack8(xv[u][j], f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m[j] = fmaxf(m[j], fabsf(f[i]));
+      }
     }
   }
   // Reduce over the lanes of one head: 16 lanes (D=128) or 8 lanes (D=64).
@@ -166,8 +179,8 @@ static int64_t head_chunks(int64_t tokens) { return (tokens + kHeadTokensPerBloc
 template <int CH, int D>
 static void launch_head_amax(const uint16_t* x, float* partial, int64_t batch, int64_t tokens, hipStream_t st) {
   const int nchunk = (int)head_chunks(tokens);
-  hipLaunchKernelGGL((k_head_amax<CH, D>), dim3((unsigned)nchunk, (unsigned)batch), dim3(256), 0, st, x, partial,
-                     tokens, kHeadTokensPerBlock, nchunk);
+  hipLaunchKernelGGL((k_head_amax<CH, D, kHeadTokensPerBlock>), dim3((unsigned)nchunk, (unsigned)batch), dim3(256), 0,
+                     st, x, partial, tokens, nchunk);
 }
 
 }  // namespace oga
