@@ -61,6 +61,8 @@ struct AttnArgs {
   int64_t o_sb, o_sn, o_sh;
   int64_t nq, nk;
   int heads;
+  int nqb;        // query blocks of kAQ per (batch, head)
+  int xcd_remap;  // workgroup count divisible by the 8 XCDs
   float scale_log2;  // softmax scale * log2(e)
 };
 
@@ -193,9 +195,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ uint4 smem[4 * kATileU4];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const int h = blockIdx.y;
-  const int64_t b = blockIdx.z;
-  const int64_t q0 = (int64_t)blockIdx.x * kAQ + wv * 32;
+  // Workgroups go to the 8 XCDs round-robin. With the remap, XCD x runs a
+  // contiguous range of (b, h, query block) triples, query block fastest, so
+  // all query blocks of a head run together on one XCD and read that head's
+  // K/V tiles through one L2.
+  int64_t wg = blockIdx.x;
+  if (a.xcd_remap) wg = (wg & 7) * (int64_t)(gridDim.x >> 3) + (wg >> 3);
+  const int qb = (int)(wg % a.nqb);
+  const int64_t bh = wg / a.nqb;
+  const int h = (int)(bh % a.heads);
+  const int64_t b = bh / a.heads;
+  const int64_t q0 = (int64_t)qb * kAQ + wv * 32;
   const int hl = lane >> 5;  // lane half
   const int ql = lane & 31;
 
@@ -459,7 +469,7 @@ extern "C" int oga_attention(const void* q, const int64_t q_strides[3], const vo
   if (batch < 0 || nq < 0 || nk < 0 || heads < 0) return fail("bad shape");
   if (batch == 0 || nq == 0 || heads == 0) return OGA_OK;
   if (nk == 0) return unsupported("no keys");
-  if (batch > 65535 || heads > 65535) return unsupported("batch/heads too large");
+  if (heads > INT32_MAX) return unsupported("too many heads");
   for (const int64_t* s : {q_strides, k_strides, v_strides, o_strides})
     for (int i = 0; i < 3; ++i)
       if (s[i] % 8) return fail("strides must be multiples of 8 elements");
@@ -474,7 +484,11 @@ extern "C" int oga_attention(const void* q, const int64_t q_strides[3], const vo
   a.o_sb = o_strides[0]; a.o_sn = o_strides[1]; a.o_sh = o_strides[2];
   a.nq = nq; a.nk = nk; a.heads = (int)heads;
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
-  const dim3 grid((unsigned)((nq + kAQ - 1) / kAQ), (unsigned)heads, (unsigned)batch);
-  hipLaunchKernelGGL(k_attention, grid, dim3(256), 0, (hipStream_t)stream, a);
+  const int64_t nqb = (nq + kAQ - 1) / kAQ;
+  const int64_t wgs = nqb * heads * batch;
+  if (nqb > INT32_MAX || wgs > UINT32_MAX) return unsupported("too many query blocks");
+  a.nqb = (int)nqb;
+  a.xcd_remap = wgs % 8 == 0;
+  hipLaunchKernelGGL(k_attention, dim3((unsigned)wgs), dim3(256), 0, (hipStream_t)stream, a);
   return launch_status();
 }
