@@ -35,13 +35,13 @@ BF16_PEAK_TFLOPS = 2500.0
 
 M, K, N = 9216, 4096, 16384
 
-# HBM-side bytes per k_fp8_gemm launch at 9216 x 4096 -> 16384, from two
+# HBM-side bytes per k_fp8_gemm_ring launch at 9216 x 4096 -> 16384, from two
 # rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE) over
 # `bench.py --only gemm`, each scaled by what the same counter reads for an
 # eager 128 MiB device copy (`bench.py --only copy`): FETCH_SIZE x 2.000,
 # WRITE_SIZE x 1.000. Source: profiles/fp8_gemm_9216x4096x16384.txt.
-GEMM_TRAFFIC_FETCH = 0.9140e9
-GEMM_TRAFFIC_WRITE = 0.3067e9
+GEMM_TRAFFIC_FETCH = 0.9269e9
+GEMM_TRAFFIC_WRITE = 0.3036e9
 GEMM_ALGORITHMIC_BYTES = M * K + N * K + N * 2 + M * N * 2  # A, W, bias read once; out written once
 
 
@@ -420,7 +420,7 @@ def main() -> None:
         "config": {"workload": "FP8 input quant + FP8Linear (exact bf16 bias) 576p FFN up-proj",
                    "m_tokens": M, "k_in": K, "n_out": N, "input_scale": "amax/448 0-dim",
                    "outliers": "0.1% x50"},
-        "roofline": {"bound": "mfma", "kernel": "k_fp8_gemm", "achieved": round(achieved, 1),
+        "roofline": {"bound": "mfma", "kernel": "k_fp8_gemm_ring", "achieved": round(achieved, 1),
                      "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
                      "traffic": GEMM_TRAFFIC_FETCH + GEMM_TRAFFIC_WRITE,
                      "traffic_split": {"fetch": GEMM_TRAFFIC_FETCH, "write": GEMM_TRAFFIC_WRITE,

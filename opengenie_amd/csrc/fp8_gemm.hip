@@ -11,20 +11,27 @@
 // 256 (N) output tile; wave (wm, wn) owns 128 (M) x 128 (N) of it as 4 x 4
 // blocks of v_mfma_f32_32x32x64_f8f6f4, whose 256 float32 accumulators per
 // lane live in the accumulation registers. One MFMA step covers 64 bytes of
-// K; the operands move through LDS in slabs of 128 bytes of K (two steps)
-// and two slab buffers (2 x (256x128 A + 256x128 W) = 128 KiB), filled by
-// LDS-DMA (global_load_lds_dwordx4) so tiles never pass through VGPRs. Each
-// DMA instruction fetches eight whole 128-byte rows: full-line requests
-// halve the address and tag work of the load path compared with 64-byte
-// half lines.
+// K; the operands move through LDS in slabs of 128 bytes of K (two steps),
+// three A and two W slab buffers (5 x 32 KiB = 160 KiB), filled by LDS-DMA
+// (global_load_lds / buffer_load ... lds, 16 bytes per lane) so tiles never
+// pass through VGPRs. Each DMA instruction fetches eight whole 128-byte
+// rows: full-line requests halve the address and tag work of the load path
+// compared with 64-byte half lines.
 //
 // Step pair (2d, 2d+1) consumes slab d. Fragments are read one step ahead
 // (double-buffered in VGPRs) between the step's first eight MFMAs. At the
 // odd step 2d+1 every wave waits for its DMA of slab d+1 and joins one
 // barrier, which publishes slab d+1 and tells that every wave has finished
-// reading slab d (its last fragments were read during step 2d); the DMA of
-// slab d+2 then goes into slab d's buffer, spread one instruction per MFMA
-// over that step.
+// reading slab d (its last fragments were read during step 2d). The DMA of
+// A slab d+2 (into the A buffer of slab d-1) is spread over the last eight
+// MFMAs of step 2d, that of W slab d+2 (into slab d's W buffer) over the
+// last eight of step 2d+1: A is sent two and a half steps, W one and a half
+// steps before it is needed.
+//
+// Two kernels share this loop: k_fp8_gemm_ring (K >= 256, N % 128 == 0, bf16
+// or no bias) is persistent, one workgroup per CU looping over tiles with
+// the slab ring running on across tile boundaries; k_fp8_gemm (every other
+// supported shape) runs one workgroup per tile.
 //
 // LDS layout of an operand slab (256 rows x 128 bytes): two rows share one
 // 256-byte line of the 64 LDS banks; row r's 16-byte chunk c (c = 0..7)
@@ -32,9 +39,9 @@
 //   (r / 2) * 256 + ((8 * (r % 2) + c) ^ ((r / 2) % 8)) * 16,
 // which keeps the 128-bit fragment reads (32 rows x 2 chunks per
 // instruction) free of bank conflicts and lets each 1 KiB DMA write fill
-// four whole lines. The two A slabs fill LDS bytes [0, 64 KiB) and the two W
-// slabs [64 KiB, 128 KiB), so every fragment read is a per-lane base plus an
-// immediate offset.
+// four whole lines. The A slabs fill LDS bytes [0, 96 KiB) and the W slabs
+// [96 KiB, 160 KiB); every fragment read is a per-lane base plus the slab
+// buffer's offset plus an immediate offset.
 //
 // The weight tile is the MFMA's A operand and the activation tile its B
 // operand, so each lane's accumulators hold 4 consecutive output columns of
@@ -461,6 +468,354 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Persistent form (K >= 256, N a multiple of 128). One workgroup per CU runs
+// tiles v, v + G, v + 2G, ... (G = grid size; with the XCD remap every tile
+// of a workgroup lies in its XCD's range, and at any moment the XCD's
+// workgroups work on consecutive tiles of that range) and keeps the slab
+// ring running across tile boundaries: the DMA of a tile's last two slabs
+// fetches slabs 0 and 1 of its next tile, so when the epilogue ends the next
+// tile's first operands are in LDS and its first fragments in VGPRs. The
+// epilogue stages each wave's output, 32 rows at a time, in its own quarter
+// of the A buffer of the tile's last slab: no wave reads that buffer any
+// more (the last odd step's barrier), no DMA targets it until the next
+// tile's first even step, and the first DMA into that quarter is the same
+// wave's own, issued after its staging reads completed. The stores are not
+// waited for here; the next tile's first odd step waits for them with the
+// DMA sent before them.
+constexpr int kStagePitch = 136;  // bytes per staged row of 64 bf16 columns
+static_assert(32 * kStagePitch <= kSlabBytes / kWaves, "a staging pass fits the wave's quarter of an A buffer");
+// Staged row r, 16-byte chunk c (of 8) sits at byte r * kStagePitch + 16c.
+// Writes: lane (fr, fh) stores 8 bytes of row fr at chunk c, half fh; each
+// 32-lane half of a ds_write_b64 must touch 64 distinct banks. Reads: lane l
+// loads row 4u + l/16 + 16*((l/8)%2), chunk l%8; each 16-lane group of a
+// ds_read_b128 must touch 64 distinct banks.
+constexpr bool stage_writes_conflict_free() {
+  for (int c = 0; c < 8; ++c)
+    for (int half = 0; half < 2; ++half) {
+      unsigned long long banks = 0;
+      for (int l = 32 * half; l < 32 * half + 32; ++l) {
+        const int b = (((l & 31) * kStagePitch + (l >> 5) * 8 + 16 * c) >> 2) & 63;
+        if ((banks >> b) & 3ull) return false;
+        banks |= 3ull << b;  // b is even: no wrap
+      }
+    }
+  return true;
+}
+constexpr bool stage_reads_conflict_free() {
+  for (int u = 0; u < 4; ++u)
+    for (int grp = 0; grp < 4; ++grp) {
+      unsigned long long banks = 0;
+      for (int l = 16 * grp; l < 16 * grp + 16; ++l) {
+        const int row = 4 * u + (l >> 4) + 16 * ((l >> 3) & 1);
+        const int b = ((row * kStagePitch + (l & 7) * 16) >> 2) & 63;
+        for (int k = 0; k < 4; ++k) {
+          if ((banks >> ((b + k) & 63)) & 1ull) return false;
+          banks |= 1ull << ((b + k) & 63);
+        }
+      }
+    }
+  return true;
+}
+static_assert(stage_writes_conflict_free(), "staging writes would conflict");
+static_assert(stage_reads_conflict_free(), "staging reads would conflict");
+// Word 3 of a buffer resource on gfx9: 32-bit data format, no swizzle.
+constexpr int kBufferWord3 = 0x00020000;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(1))) uint16_t gu16;
+typedef const __attribute__((address_space(1))) u32x4 gu32x4;
+// buffer_load_dwordx4 ... lds: LDS-DMA through a buffer resource; lanes out
+// of the resource's range read nothing.
+__device__ void buffer_load_lds(i32x4 rsrc, lds_void* lds, int size, int voffset, int soffset, int offset,
+                                int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
+// 128 bf16 -0.0 values: the bias row of a linear without bias.
+__device__ const uint16_t kNegZeroRow[128] = {
+#define OGA_NZ8 0x8000, 0x8000, 0x8000, 0x8000, 0x8000, 0x8000, 0x8000, 0x8000
+    OGA_NZ8, OGA_NZ8, OGA_NZ8, OGA_NZ8, OGA_NZ8, OGA_NZ8, OGA_NZ8, OGA_NZ8,
+    OGA_NZ8, OGA_NZ8, OGA_NZ8, OGA_NZ8, OGA_NZ8, OGA_NZ8, OGA_NZ8, OGA_NZ8,
+#undef OGA_NZ8
+};
+
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1))) void k_fp8_gemm_ring(
+    GemmArgs g) {
+  __shared__ uint4 smem[(kABufs + kWBufs) * kSlabBytes / 16];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  const int wm = wv >> 1, wn = wv & 1;
+  const int fr = lane & 31, fh = lane >> 5;
+  const int nt = g.tiles_m * g.tiles_n;
+  const int per_group = kGroupM * g.tiles_n;
+  const int nslab = g.k / GKS;  // >= 2
+  uint8_t* lds_bytes = (uint8_t*)smem;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
+  const float sc = g.sa[0] * g.sb[0];
+
+  // Tile v in launch order -> origin (the same XCD-contiguous, M-grouped
+  // order as k_fp8_gemm).
+  auto tile_origin = [&](int v, int& m0, int& n0) {
+    int t = v;
+    if (g.xcd_remap) t = (t & 7) * (nt >> 3) + (t >> 3);
+    const int grp = t / per_group;
+    const int first_m = grp * kGroupM;
+    const int gsize = min(g.tiles_m - first_m, kGroupM);
+    m0 = (first_m + (t % per_group) % gsize) * GM;
+    n0 = ((t % per_group) / gsize) * GN;
+  };
+  // The operands are read through buffer resources based at the tile's first
+  // row and sized to its rows inside the matrix: a DMA lane past the edge is
+  // out of range and reads no memory, so the per-lane offsets are the same
+  // for every tile. Lane offsets as in k_fp8_gemm; the slab offset is the
+  // scalar offset.
+  auto rsrc = [&](const uint8_t* base, int r0, int rows, int64_t ld) {
+    const uint64_t addr = (uint64_t)(base + (int64_t)r0 * ld);
+    const uint32_t bytes = (uint32_t)(min(rows - r0, GM) * ld);  // < 2^32: 256 * ld + K fits (host check)
+    const i32x4 r = {__builtin_amdgcn_readfirstlane((int)(uint32_t)addr),
+                     __builtin_amdgcn_readfirstlane((int)((uint32_t)(addr >> 32) & 0xFFFFu)),
+                     __builtin_amdgcn_readfirstlane((int)bytes), kBufferWord3};
+    return r;
+  };
+  // DMA instructions i and i + 2 of a wave cover rows 16 apart at the same
+  // chunk (their line indices differ by 8), so two per-lane offsets per
+  // operand serve all eight: instruction i reads row row_(i%2) + 16*(i/2).
+  uint32_t a_off[2], w_off[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int line = (wv * kDmaPerOp + i) * 4 + (lane >> 4);
+    const int c16 = (lane & 15) ^ (line & 7);
+    const int row = 2 * line + (c16 >> 3);
+    a_off[i] = (uint32_t)(row * g.lda + (c16 & 7) * 16);
+    w_off[i] = (uint32_t)(row * g.ldw + (c16 & 7) * 16);
+  }
+  const uint32_t a_row16 = (uint32_t)(16 * g.lda), w_row16 = (uint32_t)(16 * g.ldw);
+  // DMA instruction I of operand A or W for k-slab dk through resource rs
+  // into byte offset `buf` of LDS. The row lies in the lane offset, which
+  // the range check sees; the slab offset is the scalar offset.
+  auto dma = [&](auto i_c, auto w_c, const i32x4& rs, uint32_t buf, int dk) {
+    constexpr int I = decltype(i_c)::value;
+    constexpr bool W = decltype(w_c)::value;
+    const int blk = wv * kDmaPerOp + I;
+    const uint32_t voff = W ? w_off[I & 1] + (I >> 1) * w_row16 : a_off[I & 1] + (I >> 1) * a_row16;
+    buffer_load_lds(rs, (lds_void*)(lds_bytes + buf + blk * 1024), 16, (int)voff, dk * GKS, 0, 0);
+  };
+  auto issue_all = [&](auto w_c, const i32x4& rs, uint32_t buf, int dk) {
+    dma(IC<0>{}, w_c, rs, buf, dk); dma(IC<1>{}, w_c, rs, buf, dk); dma(IC<2>{}, w_c, rs, buf, dk);
+    dma(IC<3>{}, w_c, rs, buf, dk); dma(IC<4>{}, w_c, rs, buf, dk); dma(IC<5>{}, w_c, rs, buf, dk);
+    dma(IC<6>{}, w_c, rs, buf, dk); dma(IC<7>{}, w_c, rs, buf, dk);
+  };
+  // Ring position s (counted across tiles): A slab in A buffer s % 3, W slab
+  // in W buffer s % 2.
+  auto abuf = [&](int s) { return (uint32_t)((s % kABufs) * kSlabBytes); };
+  auto wbuf = [&](int s) { return (uint32_t)(kWBase + (s % kWBufs) * kSlabBytes); };
+
+  // Fragment bases (as in k_fp8_gemm); the A bases are the W bases plus the
+  // uniform (wm - wn) * 16 KiB, added with the slab buffer offset.
+  uint32_t lw[2][2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t in_line = (fr >> 1) * 256 + (8 * (fr & 1) + ((4 * p + 2 * fh + q) ^ ((fr >> 1) & 7))) * 16;
+      lw[p][q] = lds0 + wn * 16384 + in_line;
+    }
+  const uint32_t a_minus_w = (uint32_t)((wm - wn) * 16384);
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+#define OGA_FRAG_W(P, i) frag<(i) * 4096>(lw[P][0] + wb, lw[P][1] + wb)
+#define OGA_FRAG_A(P, j) frag<(j) * 4096>(lw[P][0] + ab, lw[P][1] + ab)
+#define OGA_MF(i, j) acc[i][j] = mfma(cw[i], ca[j], acc[i][j])
+  // Even step of ring slab s: as in k_fp8_gemm, with the A DMA of k-slab dk
+  // through resource rs into ring slot s + 2.
+  auto even_step = [&](int s, int dk, const i32x4& rs, i32x8(&cw)[4], i32x8(&ca)[4], i32x8(&nw)[4],
+                       i32x8(&na)[4]) {
+    const uint32_t ab = abuf(s) + a_minus_w, wb = wbuf(s), an = abuf(s + 2);
+    OGA_MF(0, 0); nw[0] = OGA_FRAG_W(1, 0); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(0, 1); nw[1] = OGA_FRAG_W(1, 1); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(0, 2); nw[2] = OGA_FRAG_W(1, 2); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(0, 3); nw[3] = OGA_FRAG_W(1, 3); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 0); na[0] = OGA_FRAG_A(1, 0); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 1); na[1] = OGA_FRAG_A(1, 1); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 2); na[2] = OGA_FRAG_A(1, 2); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 3); na[3] = OGA_FRAG_A(1, 3); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(2, 0); dma(IC<0>{}, IC<0>{}, rs, an, dk); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(2, 1); dma(IC<1>{}, IC<0>{}, rs, an, dk); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(2, 2); dma(IC<2>{}, IC<0>{}, rs, an, dk); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(2, 3); dma(IC<3>{}, IC<0>{}, rs, an, dk); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(3, 0); dma(IC<4>{}, IC<0>{}, rs, an, dk); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(3, 1); dma(IC<5>{}, IC<0>{}, rs, an, dk); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(3, 2); dma(IC<6>{}, IC<0>{}, rs, an, dk); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(3, 3); dma(IC<7>{}, IC<0>{}, rs, an, dk); __builtin_amdgcn_sched_barrier(0);
+    OGA_LGKM_WAIT(0, "+v"(nw[0]), "+v"(nw[1]), "+v"(nw[2]), "+v"(nw[3]), "+v"(na[0]), "+v"(na[1]), "+v"(na[2]),
+                  "+v"(na[3]));
+  };
+  // Odd step of ring slab s: wait for slab s + 1 (only the A DMA of the even
+  // step may stay in flight; every older DMA, bias load and output store is
+  // waited for), barrier, MFMAs with the fragments of slab s + 1 read between
+  // the first eight, and the W DMA of k-slab dk through resource rs into
+  // ring slot s + 2.
+  auto odd_step = [&](int s, int dk, const i32x4& rs, i32x8(&cw)[4], i32x8(&ca)[4], i32x8(&nw)[4],
+                      i32x8(&na)[4]) {
+    const uint32_t ab = abuf(s + 1) + a_minus_w, wb = wbuf(s + 1), wn2 = wbuf(s + 2);
+    OGA_WAIT_VM(kDmaPerOp);
+    OGA_BARRIER();
+    __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(0, 0); nw[0] = OGA_FRAG_W(0, 0); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(0, 1); nw[1] = OGA_FRAG_W(0, 1); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(0, 2); nw[2] = OGA_FRAG_W(0, 2); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(0, 3); nw[3] = OGA_FRAG_W(0, 3); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 0); na[0] = OGA_FRAG_A(0, 0); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 1); na[1] = OGA_FRAG_A(0, 1); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 2); na[2] = OGA_FRAG_A(0, 2); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(1, 3); na[3] = OGA_FRAG_A(0, 3); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(2, 0); dma(IC<0>{}, IC<1>{}, rs, wn2, dk); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(2, 1); dma(IC<1>{}, IC<1>{}, rs, wn2, dk); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(2, 2); dma(IC<2>{}, IC<1>{}, rs, wn2, dk); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(2, 3); dma(IC<3>{}, IC<1>{}, rs, wn2, dk); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(3, 0); dma(IC<4>{}, IC<1>{}, rs, wn2, dk); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(3, 1); dma(IC<5>{}, IC<1>{}, rs, wn2, dk); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(3, 2); dma(IC<6>{}, IC<1>{}, rs, wn2, dk); __builtin_amdgcn_sched_barrier(0);
+    OGA_MF(3, 3); dma(IC<7>{}, IC<1>{}, rs, wn2, dk); __builtin_amdgcn_sched_barrier(0);
+    OGA_LGKM_WAIT(0, "+v"(nw[0]), "+v"(nw[1]), "+v"(nw[2]), "+v"(nw[3]), "+v"(na[0]), "+v"(na[1]), "+v"(na[2]),
+                  "+v"(na[3]));
+  };
+#undef OGA_MF
+
+  // Staging: a pass holds 32 rows x 64 columns of the wave's block (block
+  // row j, column half h) inside the wave's 8 KiB quarter. Lane (fr, fh)
+  // writes at sw + 64*(i - 2h) + 16q; lane l reads its row (srow, plus 4u)
+  // at sr + 4u * kStagePitch.
+  const int srow = (lane >> 4) + 16 * ((lane >> 3) & 1);
+  const uint32_t sw = (uint32_t)(fr * kStagePitch + fh * 8);
+  const uint32_t sr = (uint32_t)(srow * kStagePitch + (lane & 7) * 16);
+
+  int v = blockIdx.x;
+  int s = 0;
+  int m0, n0;
+  tile_origin(v, m0, n0);
+  i32x4 ra = rsrc(g.a, m0, g.m, g.lda), rw = rsrc(g.w, n0, g.n, g.ldw);
+  issue_all(IC<0>{}, ra, abuf(0), 0);
+  issue_all(IC<1>{}, rw, wbuf(0), 0);
+  issue_all(IC<0>{}, ra, abuf(1), 1);
+  issue_all(IC<1>{}, rw, wbuf(1), 1);
+  OGA_WAIT_VM(2 * kDmaPerOp);
+  OGA_BARRIER();
+  i32x8 xw[4], xa[4], yw[4], ya[4];
+  {
+    const uint32_t ab = abuf(0) + a_minus_w, wb = wbuf(0);
+    xw[0] = OGA_FRAG_W(0, 0);
+    xw[1] = OGA_FRAG_W(0, 1);
+    xw[2] = OGA_FRAG_W(0, 2);
+    xw[3] = OGA_FRAG_W(0, 3);
+    xa[0] = OGA_FRAG_A(0, 0);
+    xa[1] = OGA_FRAG_A(0, 1);
+    xa[2] = OGA_FRAG_A(0, 2);
+    xa[3] = OGA_FRAG_A(0, 3);
+  }
+#undef OGA_FRAG_W
+#undef OGA_FRAG_A
+  OGA_LGKM_WAIT(0, "+v"(xw[0]), "+v"(xw[1]), "+v"(xw[2]), "+v"(xw[3]), "+v"(xa[0]), "+v"(xa[1]), "+v"(xa[2]),
+                "+v"(xa[3]));
+
+  for (;;) {
+    // The next tile (after the last one: this tile again, whose first
+    // slabs are then re-read and never consumed).
+    const int vn = v + (int)gridDim.x;
+    const bool more = vn < nt;
+    int nm0, nn0;
+    tile_origin(more ? vn : v, nm0, nn0);
+    const i32x4 nra = rsrc(g.a, nm0, g.m, g.lda), nrw = rsrc(g.w, nn0, g.n, g.ldw);
+    // Bias of the 16 columns this lane stores, (lane % 8) * 8 + 0..7 of each
+    // 64-column half of the wave's block, as bf16 (R(bias)). Loaded at the
+    // tile's start, so the first odd step's wait covers them. A block wholly
+    // past N reads the last 128 columns instead (its results are not
+    // stored); without a bias the values are -0.0, which an add leaves every
+    // value (signed zeros included) as it is.
+    u32x4 bq[2];
+    {
+      gu16* const bsrc = g.bias ? (gu16*)g.bias + min(n0 + wn * 128, g.n - 128) : (gu16*)kNegZeroRow;
+      bq[0] = *(gu32x4*)(bsrc + (lane & 7) * 8);
+      bq[1] = *(gu32x4*)(bsrc + 64 + (lane & 7) * 8);
+    }
+    // All slabs of the tile; the DMA of its last two fetches the first two
+    // slabs of the next tile.
+    for (int d = 0; d < nslab; ++d, ++s) {
+      const bool here = d + 2 < nslab;
+      const int dk = here ? d + 2 : d + 2 - nslab;
+      even_step(s, dk, here ? ra : nra, xw, xa, yw, ya);
+      odd_step(s, dk, here ? rw : nrw, yw, ya, xw, xa);
+    }
+
+    // Epilogue of tile (m0, n0): out = R(R(acc * sc) + R(bias)). Eight
+    // passes (block row j, column half h) through the wave's staging quarter
+    // of A buffer s - 1 (the tile's last slab): R(acc * sc) is staged as
+    // bf16, read back as 16-byte row pieces, the bias added, and stored.
+    const uint32_t stg = lds0 + abuf(s - 1) + wv * (kSlabBytes / kWaves);
+    const bool col_ok = n0 + wn * 128 < g.n;
+    // Row j*32 + u*4 + srow, columns h*64 + (lane%8)*8 of the wave's block:
+    // a uniform row pointer plus the lane's byte offset.
+    const int rlane = m0 + wm * 128 + srow;
+    const uint32_t olane = (uint32_t)(srow * g.ldo + (lane & 7) * 8) * 2;
+    uint16_t* const oblk = g.out + (int64_t)(m0 + wm * 128) * g.ldo + n0 + wn * 128;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 2 * h; i < 2 * h + 2; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            uint2 pk;
+            pk.x = pack_bf16(acc[i][j][q * 4 + 0] * sc, acc[i][j][q * 4 + 1] * sc);
+            pk.y = pack_bf16(acc[i][j][q * 4 + 2] * sc, acc[i][j][q * 4 + 3] * sc);
+            asm volatile("ds_write_b64 %0, %1 offset:%2" ::"v"(stg + sw), "v"(pk), "i"((i - 2 * h) * 64 + q * 16)
+                         : "memory");
+          }
+        u32x4 ov[4];
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(ov[u]) : "v"(stg + sr), "i"(u * 4 * kStagePitch));
+        OGA_LGKM_WAIT(0, "+v"(ov[0]), "+v"(ov[1]), "+v"(ov[2]), "+v"(ov[3]));
+        const u32x4 bw = bq[h];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          u32x4 y;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            y[e] = pack_bf16(__uint_as_float(ov[u][e] << 16) + __uint_as_float(bw[e] << 16),
+                             __uint_as_float(ov[u][e] & 0xFFFF0000u) + __uint_as_float(bw[e] & 0xFFFF0000u));
+          const int r = j * 32 + u * 4;  // block row, less srow
+          uint8_t* const rowp = (uint8_t*)(oblk + (int64_t)r * g.ldo + h * 64);
+          if (col_ok && rlane + r < g.m) *(u32x4*)(rowp + olane) = y;
+        }
+      }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    if (!more) break;
+    v = vn;
+    m0 = nm0;
+    n0 = nn0;
+    ra = nra;
+    rw = nrw;
+  }
+  OGA_WAIT_VM(0);  // the re-reads sent during the last tile
+}
+
 }  // namespace oga
 
 using namespace oga;
@@ -498,7 +853,18 @@ extern "C" int oga_fp8_linear(const void* a, int64_t lda, const void* w, int64_t
   g.tiles_n = (int)((n + GN - 1) / GN);
   const int64_t nt = (int64_t)g.tiles_m * g.tiles_n;
   if (nt > INT32_MAX) return unsupported("too many tiles");
-  g.xcd_remap = (nt % 8) == 0;
-  hipLaunchKernelGGL(k_fp8_gemm, dim3((unsigned)nt), dim3(64 * kWaves), 0, (hipStream_t)stream, g);
+  // The persistent kernel needs two slabs per tile, whole 128-column wave
+  // blocks and no bias or a 16-byte aligned bf16 bias; other shapes take one
+  // workgroup per tile.
+  const bool bias_vec = !bias || (bias_dtype == OGA_DT_BF16 && aligned(bias, 16));
+  if (k >= 2 * GKS && n % 128 == 0 && bias_vec) {
+    const int64_t cus = cu_count();
+    const int64_t grid = nt < cus ? nt : cus;
+    g.xcd_remap = (nt % 8) == 0 && (grid % 8) == 0;
+    hipLaunchKernelGGL(k_fp8_gemm_ring, dim3((unsigned)grid), dim3(64 * kWaves), 0, (hipStream_t)stream, g);
+  } else {
+    g.xcd_remap = (nt % 8) == 0;
+    hipLaunchKernelGGL(k_fp8_gemm, dim3((unsigned)nt), dim3(64 * kWaves), 0, (hipStream_t)stream, g);
+  }
   return launch_status();
 }

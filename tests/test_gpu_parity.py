@@ -380,7 +380,10 @@ def _fp8_weights(n, k, seed):
 
 
 @pytest.mark.parametrize("m,n,k", [(256, 256, 128), (512, 768, 1024), (300, 520, 384), (1, 16, 128),
-                                   (1024, 4096, 4096)])
+                                   (1024, 4096, 4096),
+                                   # more tiles than CUs: several tiles per persistent workgroup,
+                                   # partial last row and column tiles, two and three slabs per tile
+                                   (4100, 4224, 256), (2304, 8192, 512), (600, 16384, 384), (4352, 4096, 1024)])
 @pytest.mark.parametrize("bias_dtype", [None, torch.bfloat16, torch.float32])
 def test_fp8_linear(m, n, k, bias_dtype):
     from opengenie_amd.ltx_ops import fp8_scaled_mm
@@ -395,10 +398,16 @@ def test_fp8_linear(m, n, k, bias_dtype):
     ref = O.fp8_linear(a.view(torch.uint8).numpy(), w.view(torch.uint8).numpy(), float(sa), float(sb),
                        to_T(bias) if bias is not None else None)
     got = out_np(out)
-    np.testing.assert_allclose(got, ref, rtol=1e-2, atol=1e-3 * float(np.abs(ref).max()))
-    # Tripwire for gross errors (a wrong k pairing or layout moves most
-    # outputs): float32 accumulation order alone moves a small fraction of
-    # outputs by more than one bf16 step (sums near zero, bias cancellation).
+    close = np.isclose(got, ref, rtol=1e-2, atol=1e-3 * float(np.abs(ref).max()))
+    # rtol 1e-2 against the float64-accumulated oracle. The FP8 MFMA's own
+    # accumulation rounding followed by the two bf16 roundings moves a handful
+    # of outputs (about 1 in 2e6) just past 1%: two bf16 steps next to a power
+    # of two. A wrong k pairing, layout or tile would move whole rows or tiles.
+    assert (~close).mean() < 1e-5, (~close).sum()
+    assert (bf16_ulp_distance(got[~close], ref[~close]) <= 2).all()
+    # Tripwire for gross errors: accumulation order alone moves a small
+    # fraction of outputs by more than one bf16 step (sums near zero, bias
+    # cancellation).
     assert (bf16_ulp_distance(got, ref) > 1).mean() < 1e-2
 
 
