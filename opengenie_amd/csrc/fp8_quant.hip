@@ -148,6 +148,24 @@ __global__ __launch_bounds__(256) void k_head_scale_quant(const uint16_t* x, con
   const float s = fmaxf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), 1e-12f) / 448.0f;
   if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[b * heads + h] = s;
 
+  // x / s as the compiler's IEEE float32 division computes it (v_div_scale,
+  // v_rcp, three Newton/FMA corrections, v_div_fmas, v_div_fixup), with the
+  // divisor-only part (the refined reciprocal r) hoisted out of the loop.
+  // v_div_scale leaves both operands unscaled and v_div_fmas is a plain FMA
+  // unless the denominator is denormal or above 2^126, the quotient is
+  // above 2^96, or the numerator or quotient is tiny (exponent below -103,
+  // or a denormal quotient). Here 2.2e-15 <= s <= 7.6e35 and |x / s| <= 448,
+  // so only tiny quotients are left out, and those, like the fast path's,
+  // round to a zero e4m3 code whose sign v_div_fixup sets; v_div_fixup also
+  // returns the hardware's result for zero, infinite and NaN numerators.
+  const float r0 = __builtin_amdgcn_rcpf(s);
+  const float r = fmaf(fmaf(-s, r0, 1.0f), r0, r0);
+  auto div = [&](float n) {
+    float qv = n * r;
+    qv = fmaf(fmaf(-s, qv, n), r, qv);
+    qv = fmaf(fmaf(-s, qv, n), r, qv);
+    return __builtin_amdgcn_div_fixupf(qv, s, n);
+  };
   const int sub = threadIdx.x % LPT, tk = threadIdx.x / LPT;
   const int64_t t0 = (int64_t)blockIdx.x * kQuantTokens;
   const int64_t t1 = min(t0 + kQuantTokens, tokens);
@@ -156,7 +174,7 @@ __global__ __launch_bounds__(256) void k_head_scale_quant(const uint16_t* x, con
     float f[8];
     unpack8(*(const uint4*)(x + e0), f);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) f[i] = clamp448(f[i] / s);
+    for (int i = 0; i < 8; ++i) f[i] = clamp448(div(f[i]));
     typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
     const u32x2 o = {e4m3x4(f[0], f[1], f[2], f[3]), e4m3x4(f[4], f[5], f[6], f[7])};
     __builtin_nontemporal_store(o, (u32x2*)(q + e0));

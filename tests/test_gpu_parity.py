@@ -312,6 +312,41 @@ def test_fp8_per_head(shape):
     assert np.array_equal(q.view(torch.uint8).cpu().numpy(), qr)
 
 
+def test_fp8_per_head_special_values():
+    """Division edge cases: every finite bf16 value (scale at the top of the
+    range), +-inf (infinite scale, inf / inf), and +-0, denormals and tiny
+    values beside normal ones (zero codes keep their sign)."""
+    from opengenie_amd.ltx_ops import fused_fp8_quantize_e4m3_per_head_4d
+
+    bits = np.arange(65536, dtype=np.uint32)
+    exp = (bits >> 7) & 0xFF
+    finite = bits[exp != 0xFF]
+    x = np.random.default_rng(8).standard_normal((1, 512, 8, 128)).astype(np.float32)  # H*D = 1024 (guard)
+    h0 = np.zeros(512 * 128, np.uint32)
+    h0[: finite.size] = finite
+    x[0, :, 0, :] = (h0 << 16).view(np.float32).reshape(512, 128)
+    rng = np.random.default_rng(7)
+    h1 = rng.standard_normal(512 * 128).astype(np.float32)
+    h1[::97] = np.inf
+    h1[::89] = -np.inf
+    x[0, :, 1, :] = h1.reshape(512, 128)
+    h2 = rng.standard_normal(512 * 128).astype(np.float32) * 3
+    h2[::5] = 0.0
+    h2[1::5] = -0.0
+    h2[2::5] = ((rng.integers(1, 128, h2[2::5].size).astype(np.uint32) | 0x8000 * rng.integers(0, 2, h2[2::5].size).astype(np.uint32)) << 16).view(np.float32)  # bf16 denormals
+    h2[3::5] *= 1e-4
+    x[0, :, 2, :] = h2.reshape(512, 128)
+    x[0, :, 3, :] = rng.standard_normal((512, 128)).astype(np.float32) * 1e-30
+    xt = torch.from_numpy(x).to(torch.bfloat16)
+    q, s = fused_fp8_quantize_e4m3_per_head_4d(g(xt))
+    _ran("fused_fp8_quantize_e4m3_per_head_4d")
+    torch.cuda.synchronize()
+    qr, sr = O.fp8_per_head_quantize(np32(xt))
+    assert_same_bits(s.cpu().numpy(), sr, "per-head scale")
+    got = q.view(torch.uint8).cpu().numpy()
+    assert np.array_equal(nan_canon(got), nan_canon(qr))
+
+
 # ------------------------------------------------------------ Q/K preattention
 def _rope(seed, tokens, cos_dtype=torch.bfloat16, w_dtype=torch.bfloat16, cos_batch=1):
     q = randn((1, tokens, 4096), seed)
