@@ -16,14 +16,25 @@
 
 namespace oga {
 
+// GELU-tanh, torch gelu(approximate='tanh'): 0.5 x (1 + tanh(u)) with
+// u = sqrt(2/pi) (x + 0.044715 x^3), evaluated as the same function
+// x / (1 + exp(-2u)) = x / (1 + 2^a), a = x (c0 + c1 x^2): one v_exp_f32 and a
+// Newton-refined v_rcp_f32 instead of a library tanh, and no cancellation in
+// 1 + tanh(u) for negative x. Rounded once to bf16. Where 2^a would pass 2^64
+// (x below about -7.7) the result is x * 0: -0 as torch's saturated tanh
+// gives, and NaN for -inf as torch does.
+constexpr double kLog2e = 1.4426950408889634;
+constexpr float kGeluC0 = (float)(-2.0 * 0.7978845608028654 * kLog2e);
+constexpr float kGeluC1 = (float)(-2.0 * 0.7978845608028654 * 0.044715 * kLog2e);
 template <bool GELU>
 OGA_DEVICE float pre(float x) {
   if (!GELU) return x;
-  // torch gelu(approximate='tanh') in float32, rounded to the bf16 result.
-  const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
-  const float k1 = 0.044715f;
-  const float inner = k0 * (x + k1 * x * x * x);
-  return rbf(0.5f * x * (1.0f + tanhf(inner)));
+  const float a = x * fmaf(kGeluC1, x * x, kGeluC0);
+  const bool big = a > 64.0f;
+  const float d = 1.0f + __builtin_amdgcn_exp2f(big ? 64.0f : a);
+  float rc = __builtin_amdgcn_rcpf(d);
+  rc = fmaf(fmaf(-d, rc, 1.0f), rc, rc);
+  return rbf(x * (big ? 0.0f : rc));
 }
 
 template <bool GELU>

@@ -297,6 +297,24 @@ def test_gelu_tanh_fp8_quantize():
     assert np.nanmax(d / np.maximum(np.abs(e4m3_decode(ref)), 2 ** -9)) <= 0.126
 
 
+def test_gelu_tanh_fp8_quantize_special_values():
+    """Signed zeros, infinities, NaN, saturated tails (tanh(u) = -1 in float32,
+    GELU -0) and huge values give torch's codes exactly."""
+    from opengenie_amd.ltx_ops import fused_gelu_tanh_fp8_quantize_e4m3
+
+    vals = [0.0, -0.0, float("inf"), float("-inf"), float("nan"), 10.0, -10.0, 100.0, -100.0, 3e38, -3e38,
+            -7.0, -8.0, 1e-30, -1e-30, 0.5, -0.5]
+    x = torch.tensor(vals * 16, dtype=torch.bfloat16).reshape(16, len(vals))
+    s = torch.tensor(0.02)
+    q = fused_gelu_tanh_fp8_quantize_e4m3(g(x), g(s))
+    _ran("fused_gelu_tanh_fp8_quantize_e4m3")
+    torch.cuda.synchronize()
+    ref = tr.gelu_tanh_fp8_quantize_e4m3(x, s).view(torch.uint8).numpy()
+    got = q.view(torch.uint8).cpu().numpy()
+    special = np.array([not (0.1 < abs(v) < 5) for v in vals] * 16).reshape(got.shape)
+    assert np.array_equal(nan_canon(got[special]), nan_canon(ref[special]))
+
+
 @pytest.mark.parametrize("shape", [(1, 33, 32, 128), (2, 17, 16, 128), (1, 40, 32, 64), (1, 9216 // 16, 32, 128)])
 def test_fp8_per_head(shape):
     from opengenie_amd.ltx_ops import fused_fp8_quantize_e4m3_per_head_4d
