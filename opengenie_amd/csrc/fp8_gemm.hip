@@ -84,6 +84,11 @@ struct GemmArgs {
   int tiles_m, tiles_n;
   int bias_dt;
   int xcd_remap;
+  // Persistent kernel: `units` work units, either whole tiles (the first
+  // nfull tiles) or K-chunks of the remaining tiles, each cut into `split`
+  // chunks of kchunk slabs, whose float32 partial sums go to ws.
+  int nfull, split, kchunk, units;
+  float* ws;
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -537,6 +542,7 @@ __device__ const uint16_t kNegZeroRow[128] = {
 #undef OGA_NZ8
 };
 
+template <bool PARTIAL>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1))) void k_fp8_gemm_ring(
     GemmArgs g) {
   __shared__ uint4 smem[(kABufs + kWBufs) * kSlabBytes / 16];
@@ -546,18 +552,31 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int wm = wv >> 1, wn = wv & 1;
   const int fr = lane & 31, fh = lane >> 5;
-  const int nt = g.tiles_m * g.tiles_n;
   const int per_group = kGroupM * g.tiles_n;
   const int nslab = g.k / GKS;  // >= 2
   uint8_t* lds_bytes = (uint8_t*)smem;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
   const float sc = g.sa[0] * g.sb[0];
 
-  // Tile v in launch order -> origin (the same XCD-contiguous, M-grouped
-  // order as k_fp8_gemm).
-  auto tile_origin = [&](int v, int& m0, int& n0) {
-    int t = v;
-    if (g.xcd_remap) t = (t & 7) * (nt >> 3) + (t >> 3);
+  // Work unit u in launch order -> tile origin, first k-slab, slab count and
+  // (PARTIAL) split index. Whole tiles: units 0 .. nfull-1 are tiles
+  // 0 .. nfull-1; PARTIAL: unit sp is K-chunk sp % split of tile
+  // nfull + sp / split. The XCD remap makes each XCD's units a contiguous
+  // range; tiles follow the M-grouped order of k_fp8_gemm.
+  auto unit = [&](int u, int& m0, int& n0, int& kb, int& kn, int& sp) {
+    int t;
+    const int x = g.xcd_remap ? (u & 7) * (g.units >> 3) + (u >> 3) : u;
+    if constexpr (!PARTIAL) {
+      t = x;
+      kb = 0;
+      kn = nslab;
+      sp = -1;
+    } else {
+      sp = x;
+      t = g.nfull + sp / g.split;
+      kb = (sp % g.split) * g.kchunk;
+      kn = g.kchunk;
+    }
     const int grp = t / per_group;
     const int first_m = grp * kGroupM;
     const int gsize = min(g.tiles_m - first_m, kGroupM);
@@ -699,13 +718,13 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
 
   int v = blockIdx.x;
   int s = 0;
-  int m0, n0;
-  tile_origin(v, m0, n0);
+  int m0, n0, kb, kn, sp;
+  unit(v, m0, n0, kb, kn, sp);
   i32x4 ra = rsrc(g.a, m0, g.m, g.lda), rw = rsrc(g.w, n0, g.n, g.ldw);
-  issue_all(IC<0>{}, ra, abuf(0), 0);
-  issue_all(IC<1>{}, rw, wbuf(0), 0);
-  issue_all(IC<0>{}, ra, abuf(1), 1);
-  issue_all(IC<1>{}, rw, wbuf(1), 1);
+  issue_all(IC<0>{}, ra, abuf(0), kb);
+  issue_all(IC<1>{}, rw, wbuf(0), kb);
+  issue_all(IC<0>{}, ra, abuf(1), kb + 1);
+  issue_all(IC<1>{}, rw, wbuf(1), kb + 1);
   OGA_WAIT_VM(2 * kDmaPerOp);
   OGA_BARRIER();
   i32x8 xw[4], xa[4], yw[4], ya[4];
@@ -726,12 +745,12 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
                 "+v"(xa[3]));
 
   for (;;) {
-    // The next tile (after the last one: this tile again, whose first
-    // slabs are then re-read and never consumed).
+    // The next unit (after the last one: this unit again, whose first slabs
+    // are then re-read and never consumed).
     const int vn = v + (int)gridDim.x;
-    const bool more = vn < nt;
-    int nm0, nn0;
-    tile_origin(more ? vn : v, nm0, nn0);
+    const bool more = vn < g.units;
+    int nm0, nn0, nkb, nkn, nsp;
+    unit(more ? vn : v, nm0, nn0, nkb, nkn, nsp);
     const i32x4 nra = rsrc(g.a, nm0, g.m, g.lda), nrw = rsrc(g.w, nn0, g.n, g.ldw);
     // Bias of the 16 columns this lane stores, (lane % 8) * 8 + 0..7 of each
     // 64-column half of the wave's block, as bf16 (R(bias)). Loaded at the
@@ -745,15 +764,30 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
       bq[0] = *(gu32x4*)(bsrc + (lane & 7) * 8);
       bq[1] = *(gu32x4*)(bsrc + 64 + (lane & 7) * 8);
     }
-    // All slabs of the tile; the DMA of its last two fetches the first two
-    // slabs of the next tile.
-    for (int d = 0; d < nslab; ++d, ++s) {
-      const bool here = d + 2 < nslab;
-      const int dk = here ? d + 2 : d + 2 - nslab;
+    // All slabs of the unit; the DMA of its last two fetches the first two
+    // slabs of the next unit.
+    for (int d = 0; d < kn; ++d, ++s) {
+      const bool here = d + 2 < kn;
+      const int dk = here ? kb + d + 2 : nkb + d + 2 - kn;
       even_step(s, dk, here ? ra : nra, xw, xa, yw, ya);
       odd_step(s, dk, here ? rw : nrw, yw, ya, xw, xa);
     }
 
+    if constexpr (PARTIAL) {
+      // A K-chunk of a split tile: its float32 partial sums, as each lane
+      // holds them, for k_fp8_splitk_reduce: [sp][wave][i][j][q] x 64 lanes
+      // x 4 floats.
+      f32x4* const pw = (f32x4*)g.ws + (int64_t)(sp * kWaves + wv) * 64 * 64 + lane;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f32x4 p4 = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+            pw[((i * 4 + j) * 4 + q) * 64] = p4;
+          }
+    } else {
     // Epilogue of tile (m0, n0): out = R(R(acc * sc) + R(bias)). Eight
     // passes (block row j, column half h) through the wave's staging quarter
     // of A buffer s - 1 (the tile's last slab): R(acc * sc) is staged as
@@ -799,6 +833,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
           if (col_ok && rlane + r < g.m) *(u32x4*)(rowp + olane) = y;
         }
       }
+    }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -810,21 +845,103 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
     v = vn;
     m0 = nm0;
     n0 = nn0;
+    kb = nkb;
+    kn = nkn;
+    sp = nsp;
     ra = nra;
     rw = nrw;
   }
   OGA_WAIT_VM(0);  // the re-reads sent during the last tile
 }
 
+
+// Sum of the K-chunk partials of the split tiles, in chunk order, then the
+// epilogue of k_fp8_gemm_ring: out = R(R(sum * sa * sb) + R(bias)). One
+// thread per 4 accumulators of the GEMM: float4 index f of a tile's chunk is
+// (wave, (i * 4 + j) * 4 + q, lane), output row wm*128 + 32j + lane%32,
+// columns wn*128 + 32i + 8q + 4(lane/32) + 0..3; consecutive threads read
+// consecutive float4s of every chunk.
+__global__ __launch_bounds__(256) void k_fp8_splitk_reduce(GemmArgs g) {
+  constexpr int kPerTile = kWaves * 64 * 64;  // float4s per tile chunk
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int x = (int)(gid / kPerTile), f = (int)(gid % kPerTile);
+  const int wv = f >> 12, b = (f >> 6) & 63, lane = f & 63;
+  const int wm = wv >> 1, wn = wv & 1, fr = lane & 31, fh = lane >> 5;
+  const int i = b >> 4, j = (b >> 2) & 3, q = b & 3;
+  const int t = g.nfull + x;
+  const int per_group = kGroupM * g.tiles_n;
+  const int grp = t / per_group;
+  const int first_m = grp * kGroupM;
+  const int gsize = min(g.tiles_m - first_m, kGroupM);
+  const int row = (first_m + (t % per_group) % gsize) * GM + wm * 128 + 32 * j + fr;
+  const int col = ((t % per_group) / gsize) * GN + wn * 128 + 32 * i + 8 * q + 4 * fh;
+  const f32x4* const p = (const f32x4*)g.ws + (int64_t)x * g.split * kPerTile + f;
+  f32x4 sum = p[0];
+  for (int c = 1; c < g.split; ++c) sum += p[(int64_t)c * kPerTile];
+  if (row >= g.m || col >= g.n) return;
+  const float sc = g.sa[0] * g.sb[0];
+  float o[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float bb = g.bias ? __uint_as_float(((uint32_t)((const uint16_t*)g.bias)[col + e]) << 16) : -0.0f;
+    o[e] = rbf(sum[e] * sc) + bb;
+  }
+  uint2 pk;
+  pk.x = pack_bf16(o[0], o[1]);
+  pk.y = pack_bf16(o[2], o[3]);
+  *(uint2*)(g.out + (int64_t)row * g.ldo + col) = pk;
+}
+
 }  // namespace oga
 
 using namespace oga;
 
-extern "C" int oga_fp8_linear(const void* a, int64_t lda, const void* w, int64_t ldw, const float* scale_a,
-                              const float* scale_b, const void* bias, int bias_dtype, void* out, int64_t ldo,
-                              int64_t m, int64_t n, int64_t k, void* stream) {
+namespace {
+
+// Split-K plan of the persistent kernel for tiles that do not fill a last
+// round: with R whole rounds over the CUs and r < CUs tiles left, each of the
+// r tiles is cut into S K-chunks (the largest power of two with r * S <= CUs
+// and at least two slabs per chunk), so every workgroup ends with about the
+// same work. S = 1: no split.
+struct SplitPlan {
+  int nfull, split, kchunk, units;
+  int64_t ws_bytes;
+};
+SplitPlan split_plan(int64_t m, int64_t n, int64_t k, int64_t cus) {
+  const int64_t nt = ((m + GM - 1) / GM) * ((n + GN - 1) / GN);
+  const int64_t nslab = k / GKS;
+  SplitPlan p{(int)nt, 1, (int)nslab, (int)nt, 0};
+  const int64_t rounds = nt / cus, rest = nt % cus;
+  if (rounds < 1 || rest == 0) return p;
+  int sp = 1;
+  while (rest * sp * 2 <= cus && nslab % (sp * 2) == 0 && nslab / (sp * 2) >= 2) sp *= 2;
+  if (sp == 1) return p;
+  p.nfull = (int)(rounds * cus);
+  p.split = sp;
+  p.kchunk = (int)(nslab / sp);
+  p.units = (int)(p.nfull + rest * sp);
+  p.ws_bytes = rest * sp * (int64_t)GM * GN * 4;
+  return p;
+}
+
+bool ring_ok(int64_t n, int64_t k, const void* bias, int bias_dtype) {
+  const bool bias_vec = !bias || (bias_dtype == OGA_DT_BF16 && aligned(bias, 16));
+  return k >= 2 * GKS && n % 128 == 0 && bias_vec;
+}
+
+}  // namespace
+
+extern "C" int64_t oga_fp8_linear_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || k <= 0 || k % GKS || n % 128 || k < 2 * GKS) return 0;
+  return split_plan(m, n, k, cu_count()).ws_bytes;
+}
+
+extern "C" int oga_fp8_linear_ws(const void* a, int64_t lda, const void* w, int64_t ldw, const float* scale_a,
+                                 const float* scale_b, const void* bias, int bias_dtype, void* out, int64_t ldo,
+                                 int64_t m, int64_t n, int64_t k, void* workspace, int64_t workspace_bytes,
+                                 void* stream) {
   if (!a || !w || !scale_a || !scale_b || !out) return fail("null pointer");
-  if (m < 0 || n < 0 || k < 0) return fail("bad shape");
+  if (m < 0 || n < 0 || k < 0 || workspace_bytes < 0) return fail("bad shape");
   if (m == 0 || n == 0) return OGA_OK;
   if (k == 0 || k % GKS) return unsupported("K must be a positive multiple of %d (got %lld)", GKS, (long long)k);
   if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX) return unsupported("dimension too large");
@@ -835,6 +952,7 @@ extern "C" int oga_fp8_linear(const void* a, int64_t lda, const void* w, int64_t
   if (256 * lda + k > (int64_t)UINT32_MAX || 256 * ldw + k > (int64_t)UINT32_MAX)
     return unsupported("row stride too large");
   if (bias && !dt_ok(bias_dtype)) return fail("bias dtype must be bf16 or f32");
+  if (workspace && !aligned(workspace, 16)) return fail("workspace must be 16-byte aligned");
   GemmArgs g{};
   g.a = (const uint8_t*)a;
   g.w = (const uint8_t*)w;
@@ -852,19 +970,40 @@ extern "C" int oga_fp8_linear(const void* a, int64_t lda, const void* w, int64_t
   g.tiles_m = (int)((m + GM - 1) / GM);
   g.tiles_n = (int)((n + GN - 1) / GN);
   const int64_t nt = (int64_t)g.tiles_m * g.tiles_n;
-  if (nt > INT32_MAX) return unsupported("too many tiles");
+  if (nt > INT32_MAX / 16) return unsupported("too many tiles");
   // The persistent kernel needs two slabs per tile, whole 128-column wave
   // blocks and no bias or a 16-byte aligned bf16 bias; other shapes take one
   // workgroup per tile.
-  const bool bias_vec = !bias || (bias_dtype == OGA_DT_BF16 && aligned(bias, 16));
-  if (k >= 2 * GKS && n % 128 == 0 && bias_vec) {
+  if (ring_ok(n, k, bias, bias_dtype)) {
     const int64_t cus = cu_count();
-    const int64_t grid = nt < cus ? nt : cus;
-    g.xcd_remap = (nt % 8) == 0 && (grid % 8) == 0;
-    hipLaunchKernelGGL(k_fp8_gemm_ring, dim3((unsigned)grid), dim3(64 * kWaves), 0, (hipStream_t)stream, g);
+    SplitPlan p = split_plan(m, n, k, cus);
+    if (p.split > 1 && (!workspace || workspace_bytes < p.ws_bytes)) p = SplitPlan{(int)nt, 1, (int)(k / GKS), (int)nt, 0};
+    // Whole tiles, then (split) the K-chunks of the rest and their sums.
+    g.nfull = p.nfull;
+    g.split = p.split;
+    g.kchunk = p.kchunk;
+    g.ws = (float*)workspace;
+    g.units = p.nfull;
+    int64_t grid = g.units < cus ? g.units : cus;
+    g.xcd_remap = (g.units % 8) == 0 && (grid % 8) == 0;
+    hipLaunchKernelGGL(k_fp8_gemm_ring<false>, dim3((unsigned)grid), dim3(64 * kWaves), 0, (hipStream_t)stream, g);
+    if (p.split > 1) {
+      g.units = p.units - p.nfull;
+      grid = g.units < cus ? g.units : cus;
+      g.xcd_remap = (g.units % 8) == 0 && (grid % 8) == 0;
+      hipLaunchKernelGGL(k_fp8_gemm_ring<true>, dim3((unsigned)grid), dim3(64 * kWaves), 0, (hipStream_t)stream, g);
+      hipLaunchKernelGGL(k_fp8_splitk_reduce, dim3((unsigned)((nt - p.nfull) * kWaves * 64 * 64 / 256)), dim3(256), 0,
+                         (hipStream_t)stream, g);
+    }
   } else {
     g.xcd_remap = (nt % 8) == 0;
     hipLaunchKernelGGL(k_fp8_gemm, dim3((unsigned)nt), dim3(64 * kWaves), 0, (hipStream_t)stream, g);
   }
   return launch_status();
+}
+
+extern "C" int oga_fp8_linear(const void* a, int64_t lda, const void* w, int64_t ldw, const float* scale_a,
+                              const float* scale_b, const void* bias, int bias_dtype, void* out, int64_t ldo,
+                              int64_t m, int64_t n, int64_t k, void* stream) {
+  return oga_fp8_linear_ws(a, lda, w, ldw, scale_a, scale_b, bias, bias_dtype, out, ldo, m, n, k, nullptr, 0, stream);
 }

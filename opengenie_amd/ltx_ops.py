@@ -809,9 +809,13 @@ def fp8_scaled_mm(
     out = torch.empty((m, n), device=qinput.device, dtype=out_dtype)
     bias_c = bias.contiguous() if bias is not None else None
     _hip("fp8_scaled_mm")
-    _lib.call("oga_fp8_linear", _ptr(qinput), qinput.stride(0), _ptr(weight), weight.stride(0), _ptr(scale_a),
+    # Split-K workspace for a last round of tiles that would not fill the
+    # CUs (torch's caching allocator makes the per-call tensor cheap).
+    ws_bytes = int(_lib.load().oga_fp8_linear_workspace_bytes(m, n, k))
+    ws = torch.empty((ws_bytes // 4,), device=qinput.device, dtype=torch.float32) if ws_bytes else None
+    _lib.call("oga_fp8_linear_ws", _ptr(qinput), qinput.stride(0), _ptr(weight), weight.stride(0), _ptr(scale_a),
               _ptr(scale_b), _ptr(bias_c), _dt(bias_c) if bias_c is not None else 0, _ptr(out), out.stride(0), m, n,
-              k, _stream(qinput))
+              k, _ptr(ws), ws_bytes, _stream(qinput))
     return out
 
 
