@@ -464,6 +464,40 @@ def test_fp8_linear(m, n, k, bias_dtype):
     assert (bf16_ulp_distance(got, ref) > 1).mean() < 1e-2
 
 
+@pytest.mark.parametrize("m,n,k", [(2304, 8192, 512), (4352, 4096, 1024)])
+def test_fp8_linear_split_k_through_c_abi(m, n, k):
+    """The split-K schedule (workspace given) and the whole-tile schedule
+    (no workspace) through the C ABI, both against the oracle."""
+    from opengenie_amd import _lib
+
+    lib = _lib.load()
+    ws_bytes = int(lib.oga_fp8_linear_workspace_bytes(m, n, k))
+    assert ws_bytes > 0  # these shapes leave a partial last round of tiles
+    x = randn((m, k), 80 + m, std=1.0)
+    sa = (x.float().abs().amax() / 448.0).reshape(())
+    a = torch.clamp(x.float() / sa, -448, 448).to(torch.float8_e4m3fn)
+    w, sb = _fp8_weights(n, k, 81 + n)
+    bias = randn((n,), 82, std=0.01)
+    ga, gw, gsa, gsb, gb = g(a), g(w), g(sa).float(), g(sb).float(), g(bias)
+    ref = O.fp8_linear(a.view(torch.uint8).numpy(), w.view(torch.uint8).numpy(), float(sa), float(sb), to_T(bias))
+    stream = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for use_ws in (False, True):
+        out = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
+        ws = torch.empty((ws_bytes // 4,), device="cuda", dtype=torch.float32) if use_ws else None
+        _lib.call("oga_fp8_linear_ws", ga.data_ptr(), k, gw.data_ptr(), k, gsa.data_ptr(), gsb.data_ptr(),
+                  gb.data_ptr(), _lib.DT_BF16, out.data_ptr(), n, m, n, k, ws.data_ptr() if use_ws else None,
+                  ws_bytes if use_ws else 0, stream)
+        torch.cuda.synchronize()
+        got = out_np(out)
+        close = np.isclose(got, ref, rtol=1e-2, atol=1e-3 * float(np.abs(ref).max()))
+        assert (~close).mean() < 1e-5 and (bf16_ulp_distance(got[~close], ref[~close]) <= 2).all()
+        assert (bf16_ulp_distance(got, ref) > 1).mean() < 1e-2
+        outs.append(got)
+    # the two schedules differ only in the order of the float32 sums
+    assert (bf16_ulp_distance(outs[0], outs[1]) > 1).mean() < 1e-3
+
+
 def test_fp8_linear_forward_module():
     """The patched FP8Linear.forward on a duck-typed module, 3-D input."""
     from opengenie_amd.ltx_ops import fp8_linear_forward
