@@ -10,6 +10,8 @@ resident in HBM. The JSON line also carries:
                 HBM GB/s (algorithmic bytes / kernel time) and fraction of peak
   attention     dense video self-attention q, k, v [1, 9216, 32, 128]: TFLOP/s
                 and fraction of the bf16 MFMA peak, plus the per-head FP8 path
+  fp8_linears   the FFN down-projection (16384 -> 4096) and the 4096 -> 4096
+                projections at 9216 tokens, next to torch._scaled_mm + bias
   cpu_baseline  the numpy oracle of the same step on a bounded row sample,
                 on this host's cores
 
@@ -232,6 +234,46 @@ def attention_rows(seed: int, reps: int = 10) -> dict:
     return rows
 
 
+def linear_rows(seed: int, reps: int = 10) -> dict:
+    """The other LTX-2.3 FP8 linear shapes at 9216 tokens, with their exact
+    bf16 bias: the FFN down-projection 16384 -> 4096 and the 4096 -> 4096
+    attention projections (576 tiles: the split-K tail schedule), timed with
+    HIP events on the current stream next to torch._scaled_mm (hipBLASLt)
+    plus the bias add on the same inputs."""
+    import torch
+
+    from opengenie_amd import ltx_ops as L
+
+    rows = {}
+    st = torch.cuda.current_stream()
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for _ in range(reps):
+            fn()
+        e1.record(st)
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1000.0 / reps
+
+    for name, (k, n) in (("ffn_down_16384_to_4096", (16384, 4096)), ("proj_4096_to_4096", (4096, 4096))):
+        x, s_in, w, s_w, bias = make_fp8_linear_inputs(seed + n + k, "cuda", M, k, n)
+        q = L.fused_fp8_quantize_e4m3(x, s_in)
+        del x
+        wt = w.t()
+        us = timed(lambda: L.fp8_scaled_mm(q, w, s_in, s_w, bias))
+        us_t = timed(lambda: torch._scaled_mm(q, wt, scale_a=s_in, scale_b=s_w, out_dtype=torch.bfloat16,
+                                              use_fast_accum=True) + bias)
+        fl = 2.0 * M * n * k
+        rows[name] = {"shape": f"{M}x{k}->{n}", "us": round(us, 1), "TFLOP/s": round(fl / us / 1e6, 1),
+                      "frac": round(fl / us / 1e6 / FP8_PEAK_TFLOPS, 4),
+                      "torch_scaled_mm_plus_bias_us": round(us_t, 1)}
+        del q, w, wt
+    return rows
+
+
 COPY_ELEMS = 64 * 1024 * 1024  # bf16 elements per calibration copy: 128 MiB read + 128 MiB written
 
 
@@ -402,6 +444,7 @@ def main() -> None:
     if fused:
         fused["copy_reference"] = copy_reference()
     attention = {} if args.no_fused else attention_rows(args.seed)
+    linears = {} if args.no_fused else linear_rows(args.seed)
     cpu = None if args.no_cpu else cpu_baseline(x, s_in, w, s_w, bias)
 
     line = {
@@ -428,6 +471,7 @@ def main() -> None:
                      "us_per_launch": round(gemm_us, 2)},
         "fused_ops": fused,
         "attention": attention,
+        "fp8_linears": linears,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
