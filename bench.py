@@ -10,8 +10,9 @@ resident in HBM. The JSON line also carries:
                 HBM GB/s (algorithmic bytes / kernel time) and fraction of peak
   attention     dense video self-attention q, k, v [1, 9216, 32, 128]: TFLOP/s
                 and fraction of the bf16 MFMA peak, plus the per-head FP8 path
-  fp8_linears   the FFN down-projection (16384 -> 4096) and the 4096 -> 4096
-                projections at 9216 tokens, next to torch._scaled_mm + bias
+  fp8_linears   the FFN down-projection (16384 -> 4096), the 4096 -> 4096
+                projections and the grouped Q/K/V projection at 9216 tokens,
+                next to torch._scaled_mm + bias
   cpu_baseline  the numpy oracle of the same step on a bounded row sample,
                 on this host's cores
 
@@ -271,6 +272,30 @@ def linear_rows(seed: int, reps: int = 10) -> dict:
                       "frac": round(fl / us / 1e6 / FP8_PEAK_TFLOPS, 4),
                       "torch_scaled_mm_plus_bias_us": round(us_t, 1)}
         del q, w, wt
+
+    # Q/K/V of video self-attention from one quantized input: the grouped
+    # GEMM (one launch, per-linear weight scale and bias) against three
+    # separate FP8 linears and torch's per-linear _scaled_mm + bias.
+    x, s_in, _, _, _ = make_fp8_linear_inputs(seed + 3, "cuda", M, 4096, 256)
+    q = L.fused_fp8_quantize_e4m3(x, s_in)
+    del x
+    lins = []
+    for i in range(3):
+        _, _, w, s_w, bias = make_fp8_linear_inputs(seed + 10 + i, "cuda", 256, 4096, 4096)
+        lin = torch.nn.Module()
+        lin.weight, lin.weight_scale, lin.input_scale, lin.bias = w, s_w.float(), s_in, bias
+        lins.append(lin)
+    us_g = timed(lambda: L._fp8_grouped_linear(lins, q, torch.bfloat16))
+    us_s = timed(lambda: [L.fp8_linear_from_quantized_e4m3(lin, q, out_dtype=torch.bfloat16) for lin in lins])
+    us_t = timed(lambda: [torch._scaled_mm(q, lin.weight.t(), scale_a=s_in, scale_b=lin.weight_scale,
+                                           out_dtype=torch.bfloat16, use_fast_accum=True) + lin.bias
+                          for lin in lins])
+    fl = 2.0 * M * 4096 * 4096 * 3
+    rows["qkv_grouped_3x4096_to_4096"] = {"shape": f"{M}x4096->3x4096", "us": round(us_g, 1),
+                                         "TFLOP/s": round(fl / us_g / 1e6, 1),
+                                         "frac": round(fl / us_g / 1e6 / FP8_PEAK_TFLOPS, 4),
+                                         "three_separate_linears_us": round(us_s, 1),
+                                         "torch_scaled_mm_plus_bias_us": round(us_t, 1)}
     return rows
 
 

@@ -192,6 +192,24 @@ int oga_fp8_linear(const void* a, int64_t lda, const void* w, int64_t ldw, const
  * runs oga_fp8_linear's schedule.
  */
 int64_t oga_fp8_linear_workspace_bytes(int64_t m, int64_t n, int64_t k);
+
+/*
+ * Grouped FP8 linear: `groups` (1..4) linears of n_group output columns each
+ * on one quantized input a [M, K], in one persistent launch — the exact
+ * grouped Q/K/V (Q/K) projection of `fp8_qkv_from_grouped_mm` /
+ * `fp8_qk_from_grouped_mm` (triton_ltx_ops.py:890-955: torch._scaled_grouped_mm
+ * with one weight scale per linear, then + bias). w, scale_b, bias and out are
+ * host arrays of `groups` device pointers: w[i] [n_group, K] e4m3 (row stride
+ * ldw), scale_b[i] a float32 scalar, bias[i] (n_group,) bf16 16-byte aligned or
+ * null, out[i] [M, n_group] bf16 (row stride ldo). out[i] = R(R(acc_i *
+ * scale_a * scale_b[i]) + R(bias[i])) as oga_fp8_linear gives per group.
+ * K >= 256 and a multiple of 128; n_group a multiple of 128, and of 256 when
+ * groups > 1. Workspace: oga_fp8_linear_workspace_bytes(M, groups * n_group, K).
+ */
+int oga_fp8_linear_grouped_ws(const void* a, int64_t lda, const void* const* w, int64_t ldw, const float* scale_a,
+                              const float* const* scale_b, const void* const* bias, int bias_dtype,
+                              void* const* out, int64_t ldo, int64_t m, int64_t n_group, int64_t groups, int64_t k,
+                              void* workspace, int64_t workspace_bytes, void* stream);
 int oga_fp8_linear_ws(const void* a, int64_t lda, const void* w, int64_t ldw, const float* scale_a,
                       const float* scale_b, const void* bias, int bias_dtype, void* out, int64_t ldo,
                       int64_t m, int64_t n, int64_t k, void* workspace, int64_t workspace_bytes, void* stream);

@@ -72,6 +72,8 @@ constexpr int kDmaPerOp = GM * GKS / 1024 / kWaves;  // 1 KiB DMA instructions p
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 static_assert(3 * 4096 < 65536, "fragment offsets must fit the 16-bit immediate");
 
+constexpr int kMaxGroups = 4;
+
 struct GemmArgs {
   const uint8_t* a;
   const uint8_t* w;
@@ -89,7 +91,23 @@ struct GemmArgs {
   // chunks of kchunk slabs, whose float32 partial sums go to ws.
   int nfull, split, kchunk, units;
   float* ws;
+  // Persistent kernel: the N columns are `groups` linears of group_n columns
+  // sharing the activation (1 group: the plain linear). Group i has its own
+  // weight, weight scale, bias and output; a tile never straddles two.
+  const uint8_t* wg[kMaxGroups];
+  const float* sbg[kMaxGroups];
+  const void* biasg[kMaxGroups];
+  uint16_t* outg[kMaxGroups];
+  int group_n;
 };
+
+// Group i's entry of a kernel-argument array, by a uniform select chain (no
+// dynamic indexing, which would copy the arguments to scratch).
+template <typename T>
+OGA_DEVICE T pick(T const (&arr)[kMaxGroups], int i) {
+  static_assert(kMaxGroups == 4, "select chain covers four groups");
+  return i == 0 ? arr[0] : i == 1 ? arr[1] : i == 2 ? arr[2] : arr[3];
+}
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -556,7 +574,6 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
   const int nslab = g.k / GKS;  // >= 2
   uint8_t* lds_bytes = (uint8_t*)smem;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
-  const float sc = g.sa[0] * g.sb[0];
 
   // Work unit u in launch order -> tile origin, first k-slab, slab count and
   // (PARTIAL) split index. Whole tiles: units 0 .. nfull-1 are tiles
@@ -720,7 +737,12 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
   int s = 0;
   int m0, n0, kb, kn, sp;
   unit(v, m0, n0, kb, kn, sp);
-  i32x4 ra = rsrc(g.a, m0, g.m, g.lda), rw = rsrc(g.w, n0, g.n, g.ldw);
+  // W of the group holding columns n0 .. n0 + 255, from its first row.
+  auto wrsrc = [&](int n0) {
+    const int gi = n0 / g.group_n, r0 = n0 - gi * g.group_n;
+    return rsrc(pick(g.wg, gi), r0, g.group_n, g.ldw);
+  };
+  i32x4 ra = rsrc(g.a, m0, g.m, g.lda), rw = wrsrc(n0);
   issue_all(IC<0>{}, ra, abuf(0), kb);
   issue_all(IC<1>{}, rw, wbuf(0), kb);
   issue_all(IC<0>{}, ra, abuf(1), kb + 1);
@@ -751,7 +773,10 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
     const bool more = vn < g.units;
     int nm0, nn0, nkb, nkn, nsp;
     unit(more ? vn : v, nm0, nn0, nkb, nkn, nsp);
-    const i32x4 nra = rsrc(g.a, nm0, g.m, g.lda), nrw = rsrc(g.w, nn0, g.n, g.ldw);
+    const i32x4 nra = rsrc(g.a, nm0, g.m, g.lda), nrw = wrsrc(nn0);
+    // The group of this tile: its bias, output, scale and first column.
+    const int gi = n0 / g.group_n, nc0 = n0 - gi * g.group_n;
+    const void* const gbias = pick(g.biasg, gi);
     // Bias of the 16 columns this lane stores, (lane % 8) * 8 + 0..7 of each
     // 64-column half of the wave's block, as bf16 (R(bias)). Loaded at the
     // tile's start, so the first odd step's wait covers them. A block wholly
@@ -760,7 +785,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
     // value (signed zeros included) as it is.
     u32x4 bq[2];
     {
-      gu16* const bsrc = g.bias ? (gu16*)g.bias + min(n0 + wn * 128, g.n - 128) : (gu16*)kNegZeroRow;
+      gu16* const bsrc = gbias ? (gu16*)gbias + min(nc0 + wn * 128, g.group_n - 128) : (gu16*)kNegZeroRow;
       bq[0] = *(gu32x4*)(bsrc + (lane & 7) * 8);
       bq[1] = *(gu32x4*)(bsrc + 64 + (lane & 7) * 8);
     }
@@ -793,12 +818,13 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
     // of A buffer s - 1 (the tile's last slab): R(acc * sc) is staged as
     // bf16, read back as 16-byte row pieces, the bias added, and stored.
     const uint32_t stg = lds0 + abuf(s - 1) + wv * (kSlabBytes / kWaves);
-    const bool col_ok = n0 + wn * 128 < g.n;
+    const bool col_ok = nc0 + wn * 128 < g.group_n;
+    const float sc = g.sa[0] * pick(g.sbg, gi)[0];
     // Row j*32 + u*4 + srow, columns h*64 + (lane%8)*8 of the wave's block:
     // a uniform row pointer plus the lane's byte offset.
     const int rlane = m0 + wm * 128 + srow;
     const uint32_t olane = (uint32_t)(srow * g.ldo + (lane & 7) * 8) * 2;
-    uint16_t* const oblk = g.out + (int64_t)(m0 + wm * 128) * g.ldo + n0 + wn * 128;
+    uint16_t* const oblk = pick(g.outg, gi) + (int64_t)(m0 + wm * 128) * g.ldo + nc0 + wn * 128;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -873,23 +899,26 @@ __global__ __launch_bounds__(256) void k_fp8_splitk_reduce(GemmArgs g) {
   const int grp = t / per_group;
   const int first_m = grp * kGroupM;
   const int gsize = min(g.tiles_m - first_m, kGroupM);
+  const int n0 = ((t % per_group) / gsize) * GN;
+  const int gi = n0 / g.group_n;  // the tile's group (uniform per workgroup)
   const int row = (first_m + (t % per_group) % gsize) * GM + wm * 128 + 32 * j + fr;
-  const int col = ((t % per_group) / gsize) * GN + wn * 128 + 32 * i + 8 * q + 4 * fh;
+  const int col = n0 - gi * g.group_n + wn * 128 + 32 * i + 8 * q + 4 * fh;  // inside the group
   const f32x4* const p = (const f32x4*)g.ws + (int64_t)x * g.split * kPerTile + f;
   f32x4 sum = p[0];
   for (int c = 1; c < g.split; ++c) sum += p[(int64_t)c * kPerTile];
-  if (row >= g.m || col >= g.n) return;
-  const float sc = g.sa[0] * g.sb[0];
+  if (row >= g.m || col >= g.group_n) return;
+  const float sc = g.sa[0] * pick(g.sbg, gi)[0];
+  const uint16_t* const bias = (const uint16_t*)pick(g.biasg, gi);
   float o[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const float bb = g.bias ? __uint_as_float(((uint32_t)((const uint16_t*)g.bias)[col + e]) << 16) : -0.0f;
+    const float bb = bias ? __uint_as_float(((uint32_t)bias[col + e]) << 16) : -0.0f;
     o[e] = rbf(sum[e] * sc) + bb;
   }
   uint2 pk;
   pk.x = pack_bf16(o[0], o[1]);
   pk.y = pack_bf16(o[2], o[3]);
-  *(uint2*)(g.out + (int64_t)row * g.ldo + col) = pk;
+  *(uint2*)(pick(g.outg, gi) + (int64_t)row * g.ldo + col) = pk;
 }
 
 }  // namespace oga
@@ -924,9 +953,67 @@ SplitPlan split_plan(int64_t m, int64_t n, int64_t k, int64_t cus) {
   return p;
 }
 
-bool ring_ok(int64_t n, int64_t k, const void* bias, int bias_dtype) {
-  const bool bias_vec = !bias || (bias_dtype == OGA_DT_BF16 && aligned(bias, 16));
-  return k >= 2 * GKS && n % 128 == 0 && bias_vec;
+bool bias_ok(const void* bias, int bias_dtype) {
+  return !bias || (bias_dtype == OGA_DT_BF16 && aligned(bias, 16));
+}
+
+// Common argument checks of the FP8 linear entry points (n: all columns).
+int check_args(const void* a, int64_t lda, int64_t ldw, const float* scale_a, int64_t ldo, int64_t m, int64_t n,
+               int64_t k, const void* workspace, int64_t workspace_bytes) {
+  if (!a || !scale_a) return fail("null pointer");
+  if (m < 0 || n < 0 || k < 0 || workspace_bytes < 0) return fail("bad shape");
+  if (k == 0 || k % GKS) return unsupported("K must be a positive multiple of %d (got %lld)", GKS, (long long)k);
+  if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX) return unsupported("dimension too large");
+  if (lda < k || ldw < k) return fail("leading dimension smaller than the row");
+  if (!aligned(a, 16) || lda % 16 || ldw % 16) return fail("a/w rows must be 16-byte aligned");
+  if (ldo % 8) return fail("out rows must be 16-byte aligned");
+  // Per-lane byte offsets inside one 256-row tile (plus K) are 32-bit.
+  if (256 * lda + k > (int64_t)UINT32_MAX || 256 * ldw + k > (int64_t)UINT32_MAX)
+    return unsupported("row stride too large");
+  if (workspace && !aligned(workspace, 16)) return fail("workspace must be 16-byte aligned");
+  const int64_t nt = ((m + GM - 1) / GM) * ((n + GN - 1) / GN);
+  if (nt > INT32_MAX / 16) return unsupported("too many tiles");
+  return OGA_OK;
+}
+
+// The persistent schedule: whole tiles, then (split, workspace given) the
+// K-chunks of the rest and their sums. g has its shape, operands and groups.
+int launch_ring(GemmArgs& g, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  const int64_t nt = (int64_t)g.tiles_m * g.tiles_n;
+  const int64_t cus = cu_count();
+  SplitPlan p = split_plan(g.m, (int64_t)g.tiles_n * GN, g.k, cus);
+  if (p.split > 1 && (!workspace || workspace_bytes < p.ws_bytes)) p = SplitPlan{(int)nt, 1, g.k / GKS, (int)nt, 0};
+  g.nfull = p.nfull;
+  g.split = p.split;
+  g.kchunk = p.kchunk;
+  g.ws = (float*)workspace;
+  g.units = p.nfull;
+  int64_t grid = g.units < cus ? g.units : cus;
+  g.xcd_remap = (g.units % 8) == 0 && (grid % 8) == 0;
+  hipLaunchKernelGGL(k_fp8_gemm_ring<false>, dim3((unsigned)grid), dim3(64 * kWaves), 0, stream, g);
+  if (p.split > 1) {
+    g.units = p.units - p.nfull;
+    grid = g.units < cus ? g.units : cus;
+    g.xcd_remap = (g.units % 8) == 0 && (grid % 8) == 0;
+    hipLaunchKernelGGL(k_fp8_gemm_ring<true>, dim3((unsigned)grid), dim3(64 * kWaves), 0, stream, g);
+    hipLaunchKernelGGL(k_fp8_splitk_reduce, dim3((unsigned)((nt - p.nfull) * kWaves * 64 * 64 / 256)), dim3(256), 0,
+                       stream, g);
+  }
+  return launch_status();
+}
+
+void set_shape(GemmArgs& g, const void* a, int64_t lda, int64_t ldw, const float* scale_a, int64_t ldo, int64_t m,
+               int64_t n, int64_t k) {
+  g.a = (const uint8_t*)a;
+  g.sa = scale_a;
+  g.lda = lda;
+  g.ldw = ldw;
+  g.ldo = ldo;
+  g.m = (int)m;
+  g.n = (int)n;
+  g.k = (int)k;
+  g.tiles_m = (int)((m + GM - 1) / GM);
+  g.tiles_n = (int)((n + GN - 1) / GN);
 }
 
 }  // namespace
@@ -940,65 +1027,34 @@ extern "C" int oga_fp8_linear_ws(const void* a, int64_t lda, const void* w, int6
                                  const float* scale_b, const void* bias, int bias_dtype, void* out, int64_t ldo,
                                  int64_t m, int64_t n, int64_t k, void* workspace, int64_t workspace_bytes,
                                  void* stream) {
-  if (!a || !w || !scale_a || !scale_b || !out) return fail("null pointer");
-  if (m < 0 || n < 0 || k < 0 || workspace_bytes < 0) return fail("bad shape");
+  if (!w || !scale_b || !out) return fail("null pointer");
+  if (const int rc = check_args(a, lda, ldw, scale_a, ldo, m, n, k, workspace, workspace_bytes)) return rc;
   if (m == 0 || n == 0) return OGA_OK;
-  if (k == 0 || k % GKS) return unsupported("K must be a positive multiple of %d (got %lld)", GKS, (long long)k);
-  if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX) return unsupported("dimension too large");
-  if (lda < k || ldw < k || ldo < n) return fail("leading dimension smaller than the row");
-  if (!aligned(a, 16) || !aligned(w, 16) || lda % 16 || ldw % 16) return fail("a/w rows must be 16-byte aligned");
-  if (!aligned(out, 16) || ldo % 8) return fail("out rows must be 16-byte aligned");
-  // Per-lane byte offsets inside one 256-row tile (plus K) are 32-bit.
-  if (256 * lda + k > (int64_t)UINT32_MAX || 256 * ldw + k > (int64_t)UINT32_MAX)
-    return unsupported("row stride too large");
+  if (ldo < n) return fail("leading dimension smaller than the row");
+  if (!aligned(w, 16)) return fail("a/w rows must be 16-byte aligned");
+  if (!aligned(out, 16)) return fail("out rows must be 16-byte aligned");
   if (bias && !dt_ok(bias_dtype)) return fail("bias dtype must be bf16 or f32");
-  if (workspace && !aligned(workspace, 16)) return fail("workspace must be 16-byte aligned");
   GemmArgs g{};
-  g.a = (const uint8_t*)a;
+  set_shape(g, a, lda, ldw, scale_a, ldo, m, n, k);
   g.w = (const uint8_t*)w;
-  g.sa = scale_a;
   g.sb = scale_b;
   g.bias = bias;
   g.bias_dt = bias_dtype;
   g.out = (uint16_t*)out;
-  g.lda = lda;
-  g.ldw = ldw;
-  g.ldo = ldo;
-  g.m = (int)m;
-  g.n = (int)n;
-  g.k = (int)k;
-  g.tiles_m = (int)((m + GM - 1) / GM);
-  g.tiles_n = (int)((n + GN - 1) / GN);
-  const int64_t nt = (int64_t)g.tiles_m * g.tiles_n;
-  if (nt > INT32_MAX / 16) return unsupported("too many tiles");
   // The persistent kernel needs two slabs per tile, whole 128-column wave
   // blocks and no bias or a 16-byte aligned bf16 bias; other shapes take one
   // workgroup per tile.
-  if (ring_ok(n, k, bias, bias_dtype)) {
-    const int64_t cus = cu_count();
-    SplitPlan p = split_plan(m, n, k, cus);
-    if (p.split > 1 && (!workspace || workspace_bytes < p.ws_bytes)) p = SplitPlan{(int)nt, 1, (int)(k / GKS), (int)nt, 0};
-    // Whole tiles, then (split) the K-chunks of the rest and their sums.
-    g.nfull = p.nfull;
-    g.split = p.split;
-    g.kchunk = p.kchunk;
-    g.ws = (float*)workspace;
-    g.units = p.nfull;
-    int64_t grid = g.units < cus ? g.units : cus;
-    g.xcd_remap = (g.units % 8) == 0 && (grid % 8) == 0;
-    hipLaunchKernelGGL(k_fp8_gemm_ring<false>, dim3((unsigned)grid), dim3(64 * kWaves), 0, (hipStream_t)stream, g);
-    if (p.split > 1) {
-      g.units = p.units - p.nfull;
-      grid = g.units < cus ? g.units : cus;
-      g.xcd_remap = (g.units % 8) == 0 && (grid % 8) == 0;
-      hipLaunchKernelGGL(k_fp8_gemm_ring<true>, dim3((unsigned)grid), dim3(64 * kWaves), 0, (hipStream_t)stream, g);
-      hipLaunchKernelGGL(k_fp8_splitk_reduce, dim3((unsigned)((nt - p.nfull) * kWaves * 64 * 64 / 256)), dim3(256), 0,
-                         (hipStream_t)stream, g);
-    }
-  } else {
-    g.xcd_remap = (nt % 8) == 0;
-    hipLaunchKernelGGL(k_fp8_gemm, dim3((unsigned)nt), dim3(64 * kWaves), 0, (hipStream_t)stream, g);
+  if (k >= 2 * GKS && n % 128 == 0 && bias_ok(bias, bias_dtype)) {
+    g.wg[0] = g.w;
+    g.sbg[0] = g.sb;
+    g.biasg[0] = g.bias;
+    g.outg[0] = g.out;
+    g.group_n = g.n;
+    return launch_ring(g, workspace, workspace_bytes, (hipStream_t)stream);
   }
+  const int64_t nt = (int64_t)g.tiles_m * g.tiles_n;
+  g.xcd_remap = (nt % 8) == 0;
+  hipLaunchKernelGGL(k_fp8_gemm, dim3((unsigned)nt), dim3(64 * kWaves), 0, (hipStream_t)stream, g);
   return launch_status();
 }
 
@@ -1006,4 +1062,38 @@ extern "C" int oga_fp8_linear(const void* a, int64_t lda, const void* w, int64_t
                               const float* scale_b, const void* bias, int bias_dtype, void* out, int64_t ldo,
                               int64_t m, int64_t n, int64_t k, void* stream) {
   return oga_fp8_linear_ws(a, lda, w, ldw, scale_a, scale_b, bias, bias_dtype, out, ldo, m, n, k, nullptr, 0, stream);
+}
+
+extern "C" int oga_fp8_linear_grouped_ws(const void* a, int64_t lda, const void* const* w, int64_t ldw,
+                                         const float* scale_a, const float* const* scale_b,
+                                         const void* const* bias, int bias_dtype, void* const* out, int64_t ldo,
+                                         int64_t m, int64_t n_group, int64_t groups, int64_t k, void* workspace,
+                                         int64_t workspace_bytes, void* stream) {
+  if (!w || !scale_b || !bias || !out) return fail("null pointer");
+  if (groups < 1 || groups > kMaxGroups) return unsupported("1 to %d groups (got %lld)", kMaxGroups, (long long)groups);
+  if (n_group <= 0 || (groups > 1 && n_group % GN)) return unsupported("group width must be a multiple of %d", GN);
+  if (const int rc = check_args(a, lda, ldw, scale_a, ldo, m, n_group * groups, k, workspace, workspace_bytes))
+    return rc;
+  if (m == 0) return OGA_OK;
+  if (ldo < n_group) return fail("leading dimension smaller than the row");
+  if (k < 2 * GKS || n_group % 128) return unsupported("grouped FP8 linear needs K >= %d and N %% 128 == 0", 2 * GKS);
+  GemmArgs g{};
+  set_shape(g, a, lda, ldw, scale_a, ldo, m, n_group * groups, k);
+  g.group_n = (int)n_group;
+  for (int i = 0; i < kMaxGroups; ++i) {
+    const int j = i < groups ? i : 0;  // unused entries repeat group 0
+    if (!w[j] || !scale_b[j] || !out[j]) return fail("null pointer");
+    if (!aligned(w[j], 16) || !aligned(out[j], 16)) return fail("a/w rows and out must be 16-byte aligned");
+    if (!bias_ok(bias[j], bias_dtype)) return unsupported("grouped FP8 linear takes no bias or a 16-byte aligned bf16 bias");
+    g.wg[i] = (const uint8_t*)w[j];
+    g.sbg[i] = scale_b[j];
+    g.biasg[i] = bias[j];
+    g.outg[i] = (uint16_t*)out[j];
+  }
+  g.w = g.wg[0];
+  g.sb = g.sbg[0];
+  g.bias = g.biasg[0];
+  g.bias_dt = bias_dtype;
+  g.out = g.outg[0];
+  return launch_ring(g, workspace, workspace_bytes, (hipStream_t)stream);
 }

@@ -46,6 +46,9 @@ __all__ = [
     "fp8_linear_without_bias",
     "fp8_linear_forward",
     "fp8_scaled_mm",
+    "fp8_qkv_from_shared_quantized_input",
+    "fp8_qkv_from_grouped_mm",
+    "fp8_qk_from_grouped_mm",
 ]
 
 _FP8 = torch.float8_e4m3fn
@@ -875,3 +878,123 @@ def fp8_linear_forward(linear: torch.nn.Module, x: torch.Tensor) -> torch.Tensor
     output = fp8_scaled_mm(qflat, linear.weight, linear.input_scale, linear.weight_scale,
                            getattr(linear, "bias", None), out_dtype=x.dtype)
     return _restore_shape(output, origin_shape)
+
+
+# --------------------------------------------------------------------------
+# Q/K/V projections of video self-attention
+# --------------------------------------------------------------------------
+def _is_fp8_linear(linear) -> bool:
+    """FP8Linear recognised by its attributes (ltx_core is not a dependency)."""
+    w = getattr(linear, "weight", None)
+    return (isinstance(w, torch.Tensor) and w.dtype == _FP8 and getattr(linear, "input_scale", None) is not None
+            and getattr(linear, "weight_scale", None) is not None)
+
+
+def _scale_fits(scale: torch.Tensor, length: int) -> bool:
+    """`_scale_row` (:1281-1287) accepts a scalar or `length` values."""
+    return scale.numel() in (1, length)
+
+
+def _can_use_video_qkv_shared(attn: torch.nn.Module, x: torch.Tensor, names: tuple[str, ...],
+                              grouped: bool) -> bool:
+    """:1070-1096 (shared quantized input) and, with `grouped`, :1187-1233 /
+    :1236-1278 (grouped scaled-mm): x (1, N, 4096) contiguous bf16/fp16; the
+    linears are FP8 with a bias and one input scale; grouped also needs
+    square 4096 linears and weight scales `_scale_row` accepts."""
+    if not x.is_cuda or not x.is_contiguous() or x.dtype not in (torch.bfloat16, torch.float16):
+        return False
+    if x.ndim != 3 or x.shape[0] != 1 or x.shape[1] < 1 or x.shape[-1] != 4096:
+        return False
+    linears = [getattr(attn, n, None) for n in names]
+    if not all(_is_fp8_linear(lin) for lin in linears):
+        return False
+    if not all(getattr(lin, "bias", None) is not None for lin in linears):
+        return False
+    s0 = linears[0].input_scale
+    if not all(torch.equal(s0, lin.input_scale) for lin in linears[1:]):
+        return False
+    if not grouped:
+        return True
+    if not all(tuple(lin.weight.shape) == (x.shape[-1], x.shape[-1]) for lin in linears):
+        return False
+    rows = x.shape[0] * x.shape[1]
+    return _scale_fits(s0, rows) and all(_scale_fits(lin.weight_scale, lin.weight.shape[0]) for lin in linears)
+
+
+def _grouped_hip_ok(linears, qflat: torch.Tensor, out_dtype: torch.dtype) -> bool:
+    """The HIP grouped GEMM: bf16 outputs, scalar float32 scales, e4m3 weights
+    with 16-byte rows, 16-byte aligned bf16 biases."""
+    if out_dtype != torch.bfloat16 or not qflat.is_cuda or qflat.stride(1) != 1 or qflat.data_ptr() % 16:
+        return False
+    s0 = linears[0].input_scale
+    if s0.numel() != 1 or s0.dtype != torch.float32 or not s0.is_cuda:
+        return False
+    for lin in linears:
+        w, ws, b = lin.weight, lin.weight_scale, lin.bias
+        if not w.is_cuda or w.stride(1) != 1 or w.stride(0) != qflat.shape[1] or w.data_ptr() % 16:
+            return False
+        if ws.numel() != 1 or ws.dtype != torch.float32 or not ws.is_cuda:
+            return False
+        if b.dtype != torch.bfloat16 or not b.is_cuda or not b.is_contiguous() or b.data_ptr() % 16:
+            return False
+    return True
+
+
+def _fp8_grouped_linear(linears, qinput: torch.Tensor, out_dtype: torch.dtype) -> tuple[torch.Tensor, ...]:
+    """One quantized input through several FP8 linears with their own weight
+    scales and biases: R(R(acc * sa * sb_i) + R(bias_i)) per linear, one HIP
+    launch for all; otherwise each as `fp8_linear_from_quantized_e4m3`."""
+    import ctypes
+
+    qflat = qinput.reshape(-1, qinput.shape[-1]) if qinput.dim() == 3 else qinput
+    if not _grouped_hip_ok(linears, qflat, out_dtype):
+        _fallback("fp8_grouped_linear", qinput)
+        return tuple(fp8_linear_from_quantized_e4m3(lin, qinput, out_dtype=out_dtype) for lin in linears)
+    m, k = qflat.shape
+    n = linears[0].weight.shape[0]
+    outs = [torch.empty((m, n), device=qflat.device, dtype=out_dtype) for _ in linears]
+    lib = _lib.load()
+    ws_bytes = int(lib.oga_fp8_linear_workspace_bytes(m, n * len(linears), k))
+    ws = torch.empty((ws_bytes // 4,), device=qflat.device, dtype=torch.float32) if ws_bytes else None
+    arr = ctypes.c_void_p * len(linears)
+    w_p = arr(*[lin.weight.data_ptr() for lin in linears])
+    s_p = arr(*[lin.weight_scale.data_ptr() for lin in linears])
+    b_p = arr(*[lin.bias.data_ptr() for lin in linears])
+    o_p = arr(*[o.data_ptr() for o in outs])
+    _hip("fp8_grouped_linear")
+    _lib.call("oga_fp8_linear_grouped_ws", qflat.data_ptr(), qflat.stride(0), ctypes.addressof(w_p), k,
+              linears[0].input_scale.data_ptr(), ctypes.addressof(s_p), ctypes.addressof(b_p), _lib.DT_BF16,
+              ctypes.addressof(o_p), n, m, n, len(linears), k, _ptr(ws), ws_bytes, _stream(qflat))
+    if qinput.dim() == 3:
+        outs = [o.reshape(qinput.shape[0], qinput.shape[1], n) for o in outs]
+    return tuple(outs)
+
+
+def fp8_qkv_from_shared_quantized_input(attn: torch.nn.Module, x: torch.Tensor):
+    """:805-820 — Q/K/V FP8 linears from one quantized input (to_q's input
+    scale, equal for all three); None when the guard fails."""
+    if not _can_use_video_qkv_shared(attn, x, ("to_q", "to_k", "to_v"), grouped=False):
+        return None
+    qinput = fused_fp8_quantize_e4m3(x.contiguous(), attn.to_q.input_scale)
+    return (fp8_linear_from_quantized_e4m3(attn.to_q, qinput, out_dtype=x.dtype),
+            fp8_linear_from_quantized_e4m3(attn.to_k, qinput, out_dtype=x.dtype),
+            fp8_linear_from_quantized_e4m3(attn.to_v, qinput, out_dtype=x.dtype))
+
+
+def fp8_qkv_from_grouped_mm(attn: torch.nn.Module, x: torch.Tensor):
+    """:890-925 — exact Q/K/V projections as one grouped FP8 GEMM with each
+    linear's own weight scale and bias (one launch over the three linears'
+    tiles); None when the guard fails."""
+    if not _can_use_video_qkv_shared(attn, x, ("to_q", "to_k", "to_v"), grouped=True):
+        return None
+    qinput = fused_fp8_quantize_e4m3(x.contiguous(), attn.to_q.input_scale)
+    return _fp8_grouped_linear((attn.to_q, attn.to_k, attn.to_v), qinput, x.dtype)
+
+
+def fp8_qk_from_grouped_mm(attn: torch.nn.Module, x: torch.Tensor):
+    """:927-955 — exact Q/K projections as one grouped FP8 GEMM; None when the
+    guard fails."""
+    if not _can_use_video_qkv_shared(attn, x, ("to_q", "to_k"), grouped=True):
+        return None
+    qinput = fused_fp8_quantize_e4m3(x.contiguous(), attn.to_q.input_scale)
+    return _fp8_grouped_linear((attn.to_q, attn.to_k), qinput, x.dtype)

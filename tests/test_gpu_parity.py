@@ -498,6 +498,70 @@ def test_fp8_linear_split_k_through_c_abi(m, n, k):
     assert (bf16_ulp_distance(outs[0], outs[1]) > 1).mean() < 1e-3
 
 
+class _FP8Lin(torch.nn.Module):
+    """Duck-typed FP8Linear: e4m3 weight, input/weight scales, bias."""
+
+    def __init__(self, n, k, seed, input_scale):
+        super().__init__()
+        w, sb = _fp8_weights(n, k, seed)
+        self.weight = g(w)
+        self.weight_scale = g(sb).float()
+        self.input_scale = input_scale
+        self.bias = g(randn((n,), seed + 1, std=0.01))
+
+
+@pytest.mark.parametrize("tokens", [300, 1536])
+@pytest.mark.parametrize("names", [("to_q", "to_k", "to_v"), ("to_q", "to_k")])
+def test_fp8_qkv_grouped_mm(tokens, names):
+    """fp8_qkv_from_grouped_mm / fp8_qk_from_grouped_mm: one launch, each
+    linear with its own weight scale and bias, against the oracle per linear
+    (1536 tokens: more tiles than CUs, split-K tail)."""
+    from opengenie_amd import ltx_ops as L
+
+    attn = torch.nn.Module()
+    s_in = g(torch.tensor(0.0123))
+    for i, nm in enumerate(names):
+        setattr(attn, nm, _FP8Lin(4096, 4096, 100 + 7 * i, s_in))
+    x = randn((1, tokens, 4096), 99)
+    fn = L.fp8_qkv_from_grouped_mm if len(names) == 3 else L.fp8_qk_from_grouped_mm
+    outs = fn(attn, g(x))
+    _ran("fp8_grouped_linear")
+    torch.cuda.synchronize()
+    assert len(outs) == len(names)
+    q = O.fp8_quantize_e4m3(to_T(x), 0.0123, True, device="cuda").reshape(tokens, 4096)
+    for nm, out in zip(names, outs):
+        lin = getattr(attn, nm)
+        assert out.shape == (1, tokens, 4096) and out.dtype == torch.bfloat16
+        ref = O.fp8_linear(q, lin.weight.view(torch.uint8).cpu().numpy(), 0.0123, float(lin.weight_scale),
+                           to_T(lin.bias.cpu()))
+        got = out_np(out).reshape(tokens, 4096)
+        close = np.isclose(got, ref, rtol=1e-2, atol=1e-3 * float(np.abs(ref).max()))
+        assert (~close).mean() < 1e-5 and (bf16_ulp_distance(got[~close], ref[~close]) <= 2).all(), nm
+        assert (bf16_ulp_distance(got, ref) > 1).mean() < 1e-2, nm
+
+
+def test_fp8_qkv_shared_quantized_input_and_guard():
+    from opengenie_amd import ltx_ops as L
+
+    attn = torch.nn.Module()
+    s_in = g(torch.tensor(0.0123))
+    for i, nm in enumerate(("to_q", "to_k", "to_v")):
+        setattr(attn, nm, _FP8Lin(4096, 4096, 120 + 7 * i, s_in))
+    x = g(randn((1, 64, 4096), 98))
+    shared = L.fp8_qkv_from_shared_quantized_input(attn, x)
+    grouped = L.fp8_qkv_from_grouped_mm(attn, x)
+    torch.cuda.synchronize()
+    for a, b in zip(shared, grouped):
+        assert (bf16_ulp_distance(out_np(a), out_np(b)) > 1).mean() < 1e-3
+    # a different input scale on to_v: the reference guards return None
+    attn.to_v.input_scale = g(torch.tensor(0.02))
+    assert L.fp8_qkv_from_grouped_mm(attn, x) is None
+    assert L.fp8_qkv_from_shared_quantized_input(attn, x) is None
+    assert L.fp8_qk_from_grouped_mm(attn, x) is not None
+    # batch 2 is outside the guard
+    assert L.fp8_qk_from_grouped_mm(attn, g(randn((2, 8, 4096), 97))) is None
+
+
 def test_fp8_linear_forward_module():
     """The patched FP8Linear.forward on a duck-typed module, 3-D input."""
     from opengenie_amd.ltx_ops import fp8_linear_forward
