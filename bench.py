@@ -17,7 +17,7 @@ resident in HBM. The JSON line also carries:
                 on this host's cores
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-fused]
-       python bench.py --only {gemm,quant,fused,copy,attention}   (one part, for profiling)
+       python bench.py --only {gemm,quant,fused,copy,attention,linears}   (one part, for profiling)
 """
 
 from __future__ import annotations
@@ -56,7 +56,7 @@ def _parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fused", action="store_true")
     ap.add_argument("--seed", type=int, default=20260100)
-    ap.add_argument("--only", choices=["gemm", "quant", "fused", "copy", "attention"], default=None,
+    ap.add_argument("--only", choices=["gemm", "quant", "fused", "copy", "attention", "linears"], default=None,
                     help="run one workload --steps times and print its mean time (for profiler runs)")
     return ap.parse_args()
 
@@ -409,6 +409,9 @@ def main() -> None:
         return
     if args.only == "attention":
         print(json.dumps(attention_rows(args.seed)))
+        return
+    if args.only == "linears":
+        print(json.dumps(linear_rows(args.seed)))
         return
     x, s_in, w, s_w, bias = make_fp8_linear_inputs(args.seed, dev)
     if args.only in ("gemm", "quant"):

@@ -273,7 +273,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     constexpr int PAR = decltype(par_c)::value;
     constexpr int KB = PAR * kParBytes + kKBuf;
     constexpr int VB = PAR * kParBytes;  // vaddr already includes kVBuf
-    __syncthreads();  // this wave's DMA of step st landed (vmcnt(0)), and every wave's; other pair free
+    // This wave's DMA of step st has landed, then every wave's: the other
+    // pair is free. The wait is explicit because the barrier's workgroup
+    // fence does not wait for loads, and the LDS reads below are inline
+    // assembly the compiler does not order after the DMA.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
     if (st + 1 < nsteps) dma_step(st + 1, smem + (2 - 2 * PAR) * kATileU4, smem + (3 - 2 * PAR) * kATileU4);
 
     // S^T blocks: key block j (keys 32j .. 32j+31) x the wave's 32 queries.

@@ -1,0 +1,83 @@
+"""Properties of the compiled gfx950 code that GPU runs cannot pin down
+reliably (CPU only: hipcc cross-compiles, nothing is launched).
+
+The attention kernel fills LDS with global_load_lds (DMA counted by vmcnt)
+and reads it with inline-assembly ds_read instructions after a workgroup
+barrier. The barrier's workgroup-scope fence does not wait for loads, so
+each barrier must be preceded, in its own basic block, by an explicit
+s_waitcnt vmcnt(0) with no LDS DMA issued between that wait and the
+barrier; otherwise a wave may read a tile before its DMA has landed, a
+timing-dependent error in the attention output.
+"""
+
+from __future__ import annotations
+
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+from opengenie_amd import build
+
+CSRC = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "opengenie_amd", "csrc")
+
+
+def _device_asm(src: str) -> str:
+    flags = [f for f in build.HIPCC_FLAGS if f not in ("-fPIC", "-Wall", "-Wno-unused-function")]
+    with tempfile.TemporaryDirectory() as td:
+        out = os.path.join(td, "k.s")
+        subprocess.run([build.hipcc(), *flags, "--cuda-device-only", "-S", "-o", out, src], check=True,
+                       capture_output=True)
+        return open(out).read()
+
+
+def _kernel_body(asm: str, kernel_substr: str) -> list[str]:
+    lines = asm.splitlines()
+    start = next(i for i, l in enumerate(lines) if re.match(r"^_Z\w*" + kernel_substr + r"\w*:", l))
+    end = next(i for i in range(start, len(lines)) if lines[i].strip().startswith(".Lfunc_end"))
+    return [l.split(";")[0].strip() for l in lines[start + 1:end]]
+
+
+def barrier_violations(body: list[str]) -> list[int]:
+    """Indexes of s_barrier instructions not preceded, within their basic
+    block, by s_waitcnt vmcnt(0) with no LDS DMA after it."""
+    bad = []
+    for i, ins in enumerate(body):
+        if ins != "s_barrier":
+            continue
+        ok = False
+        for j in range(i - 1, -1, -1):
+            prev = body[j]
+            if prev.endswith(":") or prev.startswith("s_cbranch") or prev.startswith("s_branch"):
+                break  # start of the basic block
+            if "load_lds" in prev:
+                break
+            if prev.startswith("s_waitcnt") and re.search(r"\bvmcnt\(0\)", prev):
+                ok = True
+                break
+        if not ok:
+            bad.append(i)
+    return bad
+
+
+def test_barrier_check_sees_a_missing_wait():
+    body = ["global_load_lds_dwordx4 v1, s[2:3]", "s_waitcnt lgkmcnt(0)", "s_barrier"]
+    assert barrier_violations(body) == [2]
+    body = [".LBB0_1:", "s_waitcnt vmcnt(0)", ".LBB0_2:", "s_barrier"]
+    assert barrier_violations(body) == [3]
+    body = ["s_waitcnt vmcnt(0)", "global_load_lds_dwordx4 v1, s[2:3]", "s_barrier"]
+    assert barrier_violations(body) == [2]
+    body = ["global_load_lds_dwordx4 v1, s[2:3]", "s_waitcnt vmcnt(0)", "v_mov_b32 v0, 0", "s_barrier"]
+    assert barrier_violations(body) == []
+
+
+@pytest.mark.skipif(not os.path.exists("/opt/rocm/bin/hipcc") and not os.environ.get("HIPCC"),
+                    reason="hipcc not present")
+def test_attention_barriers_wait_for_lds_dma():
+    body = _kernel_body(_device_asm(os.path.join(CSRC, "attention.hip")), "k_attention")
+    n_barriers = sum(1 for ins in body if ins == "s_barrier")
+    assert n_barriers >= 2
+    assert any("load_lds" in ins for ins in body)
+    assert barrier_violations(body) == []
