@@ -552,6 +552,29 @@ typedef const __attribute__((address_space(1))) u32x4 gu32x4;
 // of the resource's range read nothing.
 __device__ void buffer_load_lds(i32x4 rsrc, lds_void* lds, int size, int voffset, int soffset, int offset,
                                 int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
+// buffer_store_dwordx4 through a buffer resource; lanes out of its range
+// write nothing.
+__device__ void buffer_store_x4(u32x4 data, i32x4 rsrc, int voffset, int soffset, int aux) __asm(
+    "llvm.amdgcn.raw.buffer.store.v4i32");
+// Cache policy of the output stores: non-temporal (written once, not read
+// back by this kernel; keeps L2 for the operand slabs).
+constexpr int kStoreNT = 2;
+// An accumulator as the MFMA left it in an AGPR, read into a VGPR where the
+// epilogue needs it (so that only the values of one staging pass are live
+// in VGPRs, not all of them from the end of the K loop on).
+OGA_DEVICE float acc_read(float x) {
+  float r;
+  asm("v_accvgpr_read_b32 %0, %1" : "=v"(r) : "a"(x));
+  return r;
+}
+// A 16-byte global load the compiler does not wait for by itself: the
+// caller's own vmcnt waits cover it before the value is used, so the
+// compiler adds no wait that would also drain the DMA sent after it.
+OGA_DEVICE u32x4 load_x4_unwaited(gu32x4* p) {
+  u32x4 r;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p));
+  return r;
+}
 // 128 bf16 -0.0 values: the bias row of a linear without bias.
 __device__ const uint16_t kNegZeroRow[128] = {
 #define OGA_NZ8 0x8000, 0x8000, 0x8000, 0x8000, 0x8000, 0x8000, 0x8000, 0x8000
@@ -605,13 +628,16 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
   // out of range and reads no memory, so the per-lane offsets are the same
   // for every tile. Lane offsets as in k_fp8_gemm; the slab offset is the
   // scalar offset.
-  auto rsrc = [&](const uint8_t* base, int r0, int rows, int64_t ld) {
-    const uint64_t addr = (uint64_t)(base + (int64_t)r0 * ld);
-    const uint32_t bytes = (uint32_t)(min(rows - r0, GM) * ld);  // < 2^32: 256 * ld + K fits (host check)
+  auto resource = [&](const void* base, uint32_t bytes) {
+    const uint64_t addr = (uint64_t)base;
     const i32x4 r = {__builtin_amdgcn_readfirstlane((int)(uint32_t)addr),
                      __builtin_amdgcn_readfirstlane((int)((uint32_t)(addr >> 32) & 0xFFFFu)),
                      __builtin_amdgcn_readfirstlane((int)bytes), kBufferWord3};
     return r;
+  };
+  auto rsrc = [&](const uint8_t* base, int r0, int rows, int64_t ld) {
+    // < 2^32 bytes: 256 * ld + K fits (host check)
+    return resource(base + (int64_t)r0 * ld, (uint32_t)(min(rows - r0, GM) * ld));
   };
   // DMA instructions i and i + 2 of a wave cover rows 16 apart at the same
   // chunk (their line indices differ by 8), so two per-lane offsets per
@@ -733,6 +759,13 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
   const uint32_t sw = (uint32_t)(fr * kStagePitch + fh * 8);
   const uint32_t sr = (uint32_t)(srow * kStagePitch + (lane & 7) * 16);
 
+  // sa * sb of each group, read before any DMA is in flight (read in the
+  // epilogue, they would make it wait for every outstanding DMA).
+  float scg[kMaxGroups];
+#pragma unroll
+  for (int i = 0; i < kMaxGroups; ++i)
+    scg[i] = PARTIAL ? 0.0f : __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(g.sa[0] * g.sbg[i][0])));
+
   int v = blockIdx.x;
   int s = 0;
   int m0, n0, kb, kn, sp;
@@ -778,16 +811,16 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
     const int gi = n0 / g.group_n, nc0 = n0 - gi * g.group_n;
     const void* const gbias = pick(g.biasg, gi);
     // Bias of the 16 columns this lane stores, (lane % 8) * 8 + 0..7 of each
-    // 64-column half of the wave's block, as bf16 (R(bias)). Loaded at the
-    // tile's start, so the first odd step's wait covers them. A block wholly
+    // 64-column half of the wave's block, as bf16 (R(bias)). A block wholly
     // past N reads the last 128 columns instead (its results are not
     // stored); without a bias the values are -0.0, which an add leaves every
-    // value (signed zeros included) as it is.
+    // value (signed zeros included) as it is. Loaded at the tile's start;
+    // the wait of the first odd step covers them.
     u32x4 bq[2];
-    {
+    if constexpr (!PARTIAL) {
       gu16* const bsrc = gbias ? (gu16*)gbias + min(nc0 + wn * 128, g.group_n - 128) : (gu16*)kNegZeroRow;
-      bq[0] = *(gu32x4*)(bsrc + (lane & 7) * 8);
-      bq[1] = *(gu32x4*)(bsrc + 64 + (lane & 7) * 8);
+      bq[0] = load_x4_unwaited((gu32x4*)(bsrc + (lane & 7) * 8));
+      bq[1] = load_x4_unwaited((gu32x4*)(bsrc + 64 + (lane & 7) * 8));
     }
     // All slabs of the unit; the DMA of its last two fetches the first two
     // slabs of the next unit.
@@ -814,51 +847,90 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
           }
     } else {
     // Epilogue of tile (m0, n0): out = R(R(acc * sc) + R(bias)). Eight
-    // passes (block row j, column half h) through the wave's staging quarter
-    // of A buffer s - 1 (the tile's last slab): R(acc * sc) is staged as
-    // bf16, read back as 16-byte row pieces, the bias added, and stored.
+    // passes p = 2j + h (block row j, column half h) through the wave's
+    // staging quarter of A buffer s - 1 (the tile's last slab): R(acc * sc)
+    // is staged as bf16, read back as 16-byte row pieces, the bias added,
+    // and stored. The passes overlap: pass p packs its values while the
+    // reads of pass p - 1 are in flight, and finishes pass p - 1 (bias and
+    // stores) while its own writes are.
     const uint32_t stg = lds0 + abuf(s - 1) + wv * (kSlabBytes / kWaves);
+    const float sc = pick(scg, gi);
+    // The stores of block row j go through a buffer resource over its 32
+    // rows inside the matrix (none for a block past N), which drops rows
+    // past M. Lane l stores row 4u + srow, columns h*64 + (lane%8)*8: the
+    // row in the lane offset, h*128 bytes as the scalar offset (a lane's 16
+    // bytes end inside its row, so the range check sees the row whether or
+    // not it counts the scalar offset).
     const bool col_ok = nc0 + wn * 128 < g.group_n;
-    const float sc = g.sa[0] * pick(g.sbg, gi)[0];
-    // Row j*32 + u*4 + srow, columns h*64 + (lane%8)*8 of the wave's block:
-    // a uniform row pointer plus the lane's byte offset.
-    const int rlane = m0 + wm * 128 + srow;
-    const uint32_t olane = (uint32_t)(srow * g.ldo + (lane & 7) * 8) * 2;
+    const int rows_left = g.m - (m0 + wm * 128);
     uint16_t* const oblk = pick(g.outg, gi) + (int64_t)(m0 + wm * 128) * g.ldo + nc0 + wn * 128;
+    const int olane = (srow * (int)g.ldo + (lane & 7) * 8) * 2;
+    const int orow4 = 8 * (int)g.ldo;  // bytes of 4 rows
+    uint2 pk[2][4];
+    u32x4 ov[4];
+    auto pack = [&](auto p_c) {
+      constexpr int J = decltype(p_c)::value / 2, H = decltype(p_c)::value % 2;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+      for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 2 * h; i < 2 * h + 2; ++i)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            uint2 pk;
-            pk.x = pack_bf16(acc[i][j][q * 4 + 0] * sc, acc[i][j][q * 4 + 1] * sc);
-            pk.y = pack_bf16(acc[i][j][q * 4 + 2] * sc, acc[i][j][q * 4 + 3] * sc);
-            asm volatile("ds_write_b64 %0, %1 offset:%2" ::"v"(stg + sw), "v"(pk), "i"((i - 2 * h) * 64 + q * 16)
-                         : "memory");
-          }
-        u32x4 ov[4];
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-          asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(ov[u]) : "v"(stg + sr), "i"(u * 4 * kStagePitch));
-        OGA_LGKM_WAIT(0, "+v"(ov[0]), "+v"(ov[1]), "+v"(ov[2]), "+v"(ov[3]));
-        const u32x4 bw = bq[h];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          u32x4 y;
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            y[e] = pack_bf16(__uint_as_float(ov[u][e] << 16) + __uint_as_float(bw[e] << 16),
-                             __uint_as_float(ov[u][e] & 0xFFFF0000u) + __uint_as_float(bw[e] & 0xFFFF0000u));
-          const int r = j * 32 + u * 4;  // block row, less srow
-          uint8_t* const rowp = (uint8_t*)(oblk + (int64_t)r * g.ldo + h * 64);
-          if (col_ok && rlane + r < g.m) *(u32x4*)(rowp + olane) = y;
+        for (int q = 0; q < 4; ++q) {
+          const f32x16& a = acc[2 * H + ii][J];
+          pk[ii][q].x = pack_bf16(acc_read(a[q * 4 + 0]) * sc, acc_read(a[q * 4 + 1]) * sc);
+          pk[ii][q].y = pack_bf16(acc_read(a[q * 4 + 2]) * sc, acc_read(a[q * 4 + 3]) * sc);
         }
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    auto write = [&]() {
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          asm volatile("ds_write_b64 %0, %1 offset:%2" ::"v"(stg + sw), "v"(pk[ii][q]), "i"(ii * 64 + q * 16)
+                       : "memory");
+    };
+    auto read = [&]() {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(ov[u]) : "v"(stg + sr), "i"(u * 4 * kStagePitch));
+    };
+    auto finish = [&](auto p_c) {
+      constexpr int J = decltype(p_c)::value / 2, H = decltype(p_c)::value % 2;
+      const int rows_j = col_ok ? min(max(rows_left - 32 * J, 0), 32) : 0;
+      const i32x4 ro = resource(oblk + (int64_t)32 * J * g.ldo, (uint32_t)(rows_j * 2 * g.ldo));
+      const u32x4 bw = bq[H];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        u32x4 y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          y[e] = pack_bf16(__uint_as_float(ov[u][e] << 16) + __uint_as_float(bw[e] << 16),
+                           __uint_as_float(ov[u][e] & 0xFFFF0000u) + __uint_as_float(bw[e] & 0xFFFF0000u));
+        buffer_store_x4(y, ro, olane + u * orow4, H * 128, kStoreNT);
       }
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    auto next = [&](auto p_c) {  // pass p >= 1
+      constexpr int P = decltype(p_c)::value;
+      pack(IC<P>{});
+      OGA_LGKM_WAIT(0, "+v"(ov[0]), "+v"(ov[1]), "+v"(ov[2]), "+v"(ov[3]));  // reads of p - 1
+      write();
+      finish(IC<P - 1>{});
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // writes of p
+      read();
+    };
+    pack(IC<0>{});
+    write();
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    read();
+    next(IC<1>{});
+    next(IC<2>{});
+    next(IC<3>{});
+    next(IC<4>{});
+    next(IC<5>{});
+    next(IC<6>{});
+    next(IC<7>{});
+    OGA_LGKM_WAIT(0, "+v"(ov[0]), "+v"(ov[1]), "+v"(ov[2]), "+v"(ov[3]));
+    finish(IC<7>{});
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -1045,10 +1117,12 @@ extern "C" int oga_fp8_linear_ws(const void* a, int64_t lda, const void* w, int6
   // blocks and no bias or a 16-byte aligned bf16 bias; other shapes take one
   // workgroup per tile.
   if (k >= 2 * GKS && n % 128 == 0 && bias_ok(bias, bias_dtype)) {
-    g.wg[0] = g.w;
-    g.sbg[0] = g.sb;
-    g.biasg[0] = g.bias;
-    g.outg[0] = g.out;
+    for (int i = 0; i < kMaxGroups; ++i) {  // one group; the others repeat it
+      g.wg[i] = g.w;
+      g.sbg[i] = g.sb;
+      g.biasg[i] = g.bias;
+      g.outg[i] = g.out;
+    }
     g.group_n = g.n;
     return launch_ring(g, workspace, workspace_bytes, (hipStream_t)stream);
   }
