@@ -694,11 +694,15 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
 
 #define OGA_FRAG_W(P, i) frag<(i) * 4096>(lw[P][0] + wb, lw[P][1] + wb)
 #define OGA_FRAG_A(P, j) frag<(j) * 4096>(lw[P][0] + ab, lw[P][1] + ab)
-#define OGA_MF(i, j) acc[i][j] = mfma(cw[i], ca[j], acc[i][j])
+// MFMA of block (i, j); the first step of a tile (Z) starts from zero.
+#define OGA_MF(i, j) acc[i][j] = mfma(cw[i], ca[j], Z ? kZero16 : acc[i][j])
   // Even step of ring slab s: as in k_fp8_gemm, with the A DMA of k-slab dk
-  // through resource rs into ring slot s + 2.
-  auto even_step = [&](int s, int dk, const i32x4& rs, i32x8(&cw)[4], i32x8(&ca)[4], i32x8(&nw)[4],
+  // through resource rs into ring slot s + 2; on a tile's first slab (z_c)
+  // the MFMAs take zero accumulators.
+  const f32x16 kZero16 = {};
+  auto even_step = [&](auto z_c, int s, int dk, const i32x4& rs, i32x8(&cw)[4], i32x8(&ca)[4], i32x8(&nw)[4],
                        i32x8(&na)[4]) {
+    constexpr bool Z = decltype(z_c)::value;
     const uint32_t ab = abuf(s) + a_minus_w, wb = wbuf(s), an = abuf(s + 2);
     OGA_MF(0, 0); nw[0] = OGA_FRAG_W(1, 0); __builtin_amdgcn_sched_barrier(0);
     OGA_MF(0, 1); nw[1] = OGA_FRAG_W(1, 1); __builtin_amdgcn_sched_barrier(0);
@@ -726,6 +730,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
   // ring slot s + 2.
   auto odd_step = [&](int s, int dk, const i32x4& rs, i32x8(&cw)[4], i32x8(&ca)[4], i32x8(&nw)[4],
                       i32x8(&na)[4]) {
+    constexpr bool Z = false;
     const uint32_t ab = abuf(s + 1) + a_minus_w, wb = wbuf(s + 1), wn2 = wbuf(s + 2);
     OGA_WAIT_VM(kDmaPerOp);
     OGA_BARRIER();
@@ -824,12 +829,16 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
     }
     // All slabs of the unit; the DMA of its last two fetches the first two
     // slabs of the next unit.
-    for (int d = 0; d < kn; ++d, ++s) {
+    // The first slab's MFMAs start from zero accumulators.
+    auto slab = [&](auto z_c, int d) {
       const bool here = d + 2 < kn;
       const int dk = here ? kb + d + 2 : nkb + d + 2 - kn;
-      even_step(s, dk, here ? ra : nra, xw, xa, yw, ya);
+      even_step(z_c, s, dk, here ? ra : nra, xw, xa, yw, ya);
       odd_step(s, dk, here ? rw : nrw, yw, ya, xw, xa);
-    }
+      ++s;
+    };
+    slab(IC<1>{}, 0);
+    for (int d = 1; d < kn; ++d) slab(IC<0>{}, d);
 
     if constexpr (PARTIAL) {
       // A K-chunk of a split tile: its float32 partial sums, as each lane
@@ -933,12 +942,6 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
     finish(IC<7>{});
     }
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
     if (!more) break;
     v = vn;
     m0 = nm0;
