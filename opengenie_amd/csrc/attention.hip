@@ -183,10 +183,6 @@ OGA_DEVICE float sum_halves(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-template <int N>
-struct IC {
-  static constexpr int value = N;
-};
 
 // LDS: [K0 | V0 | K1 | V1], 16 KiB each; step st uses buffer pair st % 2.
 constexpr int kKBuf = 0, kVBuf = 16384, kParBytes = 32768;

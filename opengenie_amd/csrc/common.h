@@ -21,6 +21,13 @@ namespace oga {
 
 constexpr int kWave = 64;
 
+// A compile-time integer as a value (unrolled steps pass their index this
+// way so that register arrays are indexed by constants).
+template <int N>
+struct IC {
+  static constexpr int value = N;
+};
+
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));

@@ -144,10 +144,6 @@ OGA_DEVICE f32x16 mfma(const i32x8& w, const i32x8& a, const f32x16& c) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w, a, c, 0, 0, 0, 0, 0, 0);
 }
 
-template <int N>
-struct IC {
-  static constexpr int value = N;
-};
 
 // Fragment read addresses folded into per-lane bases (checked for every lane,
 // block, step parity and chunk pair): block b (rows 32b .. 32b+31), step

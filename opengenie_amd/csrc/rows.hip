@@ -233,25 +233,60 @@ __global__ __launch_bounds__(256) void k_elem(RowArgs a, int64_t rows_per_group)
 
 // ------------------------------------------------------------ AdaZero
 // y = R(R?(R(x * inv_rms) * R?(1 + scale)) + shift). A workgroup of CH waves
-// owns a block of up to RMAX consecutive token rows; wave w owns columns
-// w*512 + 8l .. +7 of every row of the block. Each wave computes its Ada
-// constants once, issues the loads of all its rows together, and adds up
-// the squares of its chunk per row (float64: squares of bf16 values are
-// exact); one barrier later every wave combines the CH partial sums of a
-// row into that row's normaliser and writes its chunk.
-constexpr int kAdaRows = 8;
+// streams a run of consecutive token rows; wave w owns columns w*512 + 8l ..
+// +7 of every row. Each wave keeps the loads of the next kAdaAhead rows in
+// flight while it finishes the current one (the first ones go out before
+// the Ada constants are computed), so a workgroup's reads of later rows
+// overlap its writes of earlier ones. Per row a wave adds up the squares
+// of its chunk (float64: squares of bf16 values are exact), and after one
+// barrier every wave combines the CH partial sums of the row (double-
+// buffered in LDS: a wave writes the partials of row u + 2 only after the
+// barrier of row u + 1, which every wave reaches after reading those of row
+// u) into the row's normaliser and writes its chunk.
+#ifndef OGA_ADA_AHEAD
+#define OGA_ADA_AHEAD 2
+#endif
+constexpr int kAdaAhead = OGA_ADA_AHEAD;
+static_assert(kAdaAhead >= 1 && kAdaAhead <= 4, "prefetch depth");
 template <int CH, bool UNIFORM, int D0, int D1, bool VEC>
 __global__ __launch_bounds__(512) void k_adazero(RowArgs a, int rows_per_wg) {
   constexpr int C = CH * 512;
   constexpr bool B1 = D1 == OGA_DT_BF16;
   constexpr bool B0 = D0 == OGA_DT_BF16;
-  __shared__ double part[kAdaRows][CH];
+  __shared__ double part[2][CH];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int64_t b = blockIdx.y;
   const int col0 = wv * 512 + lane * 8;
   const int64_t t0 = (int64_t)blockIdx.x * rows_per_wg;
   const int nr = (int)min((int64_t)rows_per_wg, a.tokens - t0);  // >= 1 by the grid
+  const int64_t tsc0 = a.s0.ts_off + b * a.s0.ts_sb + (int64_t)col0 * a.s0.ts_sc;
+  const int64_t tsc1 = a.s1.ts_off + b * a.s1.ts_sb + (int64_t)col0 * a.s1.ts_sc;
+  constexpr bool kPre = !UNIFORM && VEC;
+  const uint16_t* const xrow = a.x + (b * a.tokens + t0) * C + col0;
+  uint16_t* const orow = a.out + (b * a.tokens + t0) * C + col0;
+
+  // Row u of the run lives in slot u % kAdaAhead. (nr and every branch on
+  // it are uniform over the workgroup, so every wave reaches each barrier.)
+  uint4 xv[kAdaAhead];
+  Raw8<D0> p0[kPre ? kAdaAhead : 1];
+  Raw8<D1> p1[kPre ? kAdaAhead : 1];
+  auto issue = [&](int u, auto k_c) {
+    constexpr int K = decltype(k_c)::value;
+    xv[K] = *(const uint4*)(xrow + (int64_t)u * C);
+    if constexpr (kPre) {
+      const int64_t t = t0 + u;
+      p0[K] = raw8_load<D0>(a.s0.ts, tsc0 + t * a.s0.ts_st);
+      p1[K] = raw8_load<D1>(a.s1.ts, tsc1 + t * a.s1.ts_st);
+    }
+  };
+  auto prologue = [&](auto k_c) {
+    if (decltype(k_c)::value < nr) issue(decltype(k_c)::value, k_c);
+  };
+  prologue(IC<0>{});
+  if constexpr (kAdaAhead > 1) prologue(IC<1>{});
+  if constexpr (kAdaAhead > 2) prologue(IC<2>{});
+  if constexpr (kAdaAhead > 3) prologue(IC<3>{});
 
   const bool tab0 = a.s0.tab != nullptr;
   const bool tab1 = a.s1.tab != nullptr;
@@ -270,98 +305,86 @@ __global__ __launch_bounds__(512) void k_adazero(RowArgs a, int rows_per_wg) {
       c1[i] = B1 ? rbf(f) : f;
     }
   }
-  const int64_t tsc0 = a.s0.ts_off + b * a.s0.ts_sb + (int64_t)col0 * a.s0.ts_sc;
-  const int64_t tsc1 = a.s1.ts_off + b * a.s1.ts_sb + (int64_t)col0 * a.s1.ts_sc;
-  constexpr bool kPre = !UNIFORM && VEC;
 
-  uint4 xv[kAdaRows];
-  Raw8<D0> p0[kPre ? kAdaRows : 1];
-  Raw8<D1> p1[kPre ? kAdaRows : 1];
+  auto row = [&](int u, auto k_c) {
+    constexpr int K = decltype(k_c)::value;
+    const int64_t t = t0 + u;
+    float xf[8];
+    unpack8(xv[K], xf);
+    double ss[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-  for (int u = 0; u < kAdaRows; ++u) {
-    if (u < nr) {
-      const int64_t t = t0 + u;
-      xv[u] = *(const uint4*)(a.x + (b * a.tokens + t) * C + col0);
-      if (kPre) {
-        p0[kPre ? u : 0] = raw8_load<D0>(a.s0.ts, tsc0 + t * a.s0.ts_st);
-        p1[kPre ? u : 0] = raw8_load<D1>(a.s1.ts, tsc1 + t * a.s1.ts_st);
-      }
+    for (int i = 0; i < 8; ++i) {
+      const double d = (double)xf[i];
+      ss[i & 3] = fma(d, d, ss[i & 3]);
     }
-  }
+    const double w = wave_sum_d((ss[0] + ss[1]) + (ss[2] + ss[3]));
+    if (lane == 0) part[u & 1][wv] = w;
+    __syncthreads();
+    double tot = 0.0;
 #pragma unroll
-  for (int u = 0; u < kAdaRows; ++u) {
-    if (u < nr) {
-      float f[8];
-      unpack8(xv[u], f);
-      double ss[4] = {0.0, 0.0, 0.0, 0.0};
+    for (int c = 0; c < CH; ++c) tot += part[u & 1][c];
+    const float mean = (float)(tot / (double)C);
+    const float inv = 1.0f / sqrtf(mean + a.eps);
+    float v0[8], v1[8], o[8];
+    if (UNIFORM) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const double d = (double)f[i];
-        ss[i & 3] = fma(d, d, ss[i & 3]);
+        v0[i] = c0[i];
+        v1[i] = c1[i];
       }
-      const double w = wave_sum_d((ss[0] + ss[1]) + (ss[2] + ss[3]));
-      if (lane == 0) part[u][wv] = w;
-    }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int u = 0; u < kAdaRows; ++u) {
-    if (u < nr) {
-      const int64_t t = t0 + u;
-      double tot = 0.0;
-#pragma unroll
-      for (int c = 0; c < CH; ++c) tot += part[u][c];
-      const float mean = (float)(tot / (double)C);
-      const float inv = 1.0f / sqrtf(mean + a.eps);
-      float v0[8], v1[8], xf[8], o[8];
-      if (UNIFORM) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          v0[i] = c0[i];
-          v1[i] = c1[i];
-        }
-      } else {
-        float tsv[8];
-        if (kPre) raw8_get<D0>(p0[kPre ? u : 0], tsv);
-        else load8_t<D0, false>(a.s0.ts, tsc0 + t * a.s0.ts_st, a.s0.ts_sc, tsv);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float sum = tab0 ? c0[i] + tsv[i] : tsv[i];
-          v0[i] = (tab0 && B0) ? rbf(sum) : sum;
-        }
-        if (kPre) raw8_get<D1>(p1[kPre ? u : 0], tsv);
-        else load8_t<D1, false>(a.s1.ts, tsc1 + t * a.s1.ts_st, a.s1.ts_sc, tsv);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          float sum = tab1 ? c1[i] + tsv[i] : tsv[i];
-          if (tab1 && B1) sum = rbf(sum);
-          const float f = 1.0f + sum;
-          v1[i] = B1 ? rbf(f) : f;
-        }
-      }
-      unpack8(xv[u], xf);
+    } else {
+      float tsv[8];
+      if constexpr (kPre) raw8_get<D0>(p0[K], tsv);
+      else load8_t<D0, false>(a.s0.ts, tsc0 + t * a.s0.ts_st, a.s0.ts_sc, tsv);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        float p = rbf(xf[i] * inv) * v1[i];
-        if (B1) p = rbf(p);
-        o[i] = p + v0[i];
+        const float sum = tab0 ? c0[i] + tsv[i] : tsv[i];
+        v0[i] = (tab0 && B0) ? rbf(sum) : sum;
       }
-      st_nt16(a.out + (b * a.tokens + t) * C + col0, pack8(o));
+      if constexpr (kPre) raw8_get<D1>(p1[K], tsv);
+      else load8_t<D1, false>(a.s1.ts, tsc1 + t * a.s1.ts_st, a.s1.ts_sc, tsv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float sum = tab1 ? c1[i] + tsv[i] : tsv[i];
+        if (tab1 && B1) sum = rbf(sum);
+        const float f = 1.0f + sum;
+        v1[i] = B1 ? rbf(f) : f;
+      }
     }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float p = rbf(xf[i] * inv) * v1[i];
+      if (B1) p = rbf(p);
+      o[i] = p + v0[i];
+    }
+    st_nt16(orow + (int64_t)u * C, pack8(o));
+  };
+  auto step = [&](int base, auto k_c) {
+    const int u = base + decltype(k_c)::value;
+    if (u < nr) {
+      row(u, k_c);
+      if (u + kAdaAhead < nr) issue(u + kAdaAhead, k_c);
+    }
+  };
+  for (int base = 0; base < nr; base += kAdaAhead) {
+    step(base, IC<0>{});
+    if constexpr (kAdaAhead > 1) step(base, IC<1>{});
+    if constexpr (kAdaAhead > 2) step(base, IC<2>{});
+    if constexpr (kAdaAhead > 3) step(base, IC<3>{});
   }
 }
 
-// Grid of k_adazero: about OGA_ADA_WAVES_PER_CU waves per CU, blocks of
-// equal row counts.
-#ifndef OGA_ADA_WAVES_PER_CU
-#define OGA_ADA_WAVES_PER_CU 16
+// Grid of k_adazero: about OGA_ADA_WGS_PER_CU workgroups per CU, each
+// streaming an equal run of rows.
+#ifndef OGA_ADA_WGS_PER_CU
+#define OGA_ADA_WGS_PER_CU 4
 #endif
-static void adazero_grid(int64_t batch, int64_t tokens, int ch, dim3& grid, int& rows_per_wg) {
-  const int64_t target_wgs = (int64_t)cu_count() * OGA_ADA_WAVES_PER_CU / ch;
+static void adazero_grid(int64_t batch, int64_t tokens, dim3& grid, int& rows_per_wg) {
+  const int64_t target_wgs = (int64_t)cu_count() * OGA_ADA_WGS_PER_CU;
   int64_t per_batch = target_wgs / batch;
   if (per_batch < 1) per_batch = 1;
   int64_t rows = (tokens + per_batch - 1) / per_batch;
-  if (rows > kAdaRows) rows = kAdaRows;
+  if (rows > INT32_MAX) rows = INT32_MAX;
   rows_per_wg = (int)rows;
   grid = dim3((unsigned)((tokens + rows - 1) / rows), (unsigned)batch);
 }
@@ -483,7 +506,7 @@ static void launch_row_v(RowArgs& a, int64_t batch, bool vec, hipStream_t st) {
   } else {
     dim3 grid;
     int rpw = 0;
-    adazero_grid(batch, a.tokens, CH, grid, rpw);
+    adazero_grid(batch, a.tokens, grid, rpw);
     if (vec)
       hipLaunchKernelGGL((k_adazero<CH, UNIFORM, D0, D1, true>), grid, dim3(64 * CH), 0, st, a, rpw);
     else
