@@ -17,13 +17,14 @@ resident in HBM. The JSON line also carries:
                 on this host's cores
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-fused]
-       python bench.py --only {gemm,quant,fused,copy,attention,linears}   (one part, for profiling)
+       python bench.py --only {gemm,quant,fused,copy,attention,linears,block}   (one part, for profiling)
 """
 
 from __future__ import annotations
 
 import argparse
 import json
+import statistics
 import os
 import sys
 import time
@@ -56,7 +57,7 @@ def _parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fused", action="store_true")
     ap.add_argument("--seed", type=int, default=20260100)
-    ap.add_argument("--only", choices=["gemm", "quant", "fused", "copy", "attention", "linears"], default=None,
+    ap.add_argument("--only", choices=["gemm", "quant", "fused", "copy", "attention", "linears", "block"], default=None,
                     help="run one workload --steps times and print its mean time (for profiler runs)")
     return ap.parse_args()
 
@@ -186,6 +187,49 @@ def fused_op_rows(seed: int) -> dict:
 
 
 ATT_N, ATT_H, ATT_D = 9216, 32, 128
+
+
+def block_rows(seed: int, reps: int = 5, ctx_tokens: int = 256) -> dict:
+    """One video transformer-block slice at 9216 tokens (self-attention, text
+    cross-attention over ctx_tokens text tokens, feed-forward; the production
+    op order of opengenie_amd.block), random-init synthetic parameters of the
+    LTX-2.3 shapes; HIP events on the current stream around the whole slice
+    and between its three branches."""
+    import torch
+
+    from opengenie_amd import block as B
+
+    blk = B.random_video_block(4096, 32, seed=seed + 40)
+    g = _gen(seed + 41, "cuda")
+    vx = torch.randn((1, M, 4096), generator=g, device="cuda").to(torch.bfloat16)
+    ctx = torch.randn((1, ctx_tokens, 4096), generator=g, device="cuda").to(torch.bfloat16)
+    ts = (torch.randn((1, 1, 9 * 4096), generator=g, device="cuda") * 0.5).to(torch.bfloat16).expand(1, M, 9 * 4096)
+    pts = (torch.randn((1, ctx_tokens, 2 * 4096), generator=g, device="cuda") * 0.5).to(torch.bfloat16)
+    cos = torch.randn((1, 32, M, 64), generator=g, device="cuda").clamp(-1, 1).to(torch.bfloat16)
+    sin = torch.randn((1, 32, M, 64), generator=g, device="cuda").clamp(-1, 1).to(torch.bfloat16)
+    st = torch.cuda.current_stream()
+    rows = {}
+    for fuse in (False, True):
+        parts = {"self_attention": [], "text_cross_attention": [], "feed_forward": [], "block": []}
+        for rep in range(reps + 2):
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+            ev[0].record(st)
+            x1 = B.video_self_attention(blk, vx, ts, cos, sin)
+            ev[1].record(st)
+            x2 = B.video_text_cross_attention(blk, x1, ctx, ts, pts)
+            ev[2].record(st)
+            B.video_feed_forward(blk, x2, ts, fuse_gelu_quant=fuse)
+            ev[3].record(st)
+            ev[3].synchronize()
+            if rep < 2:
+                continue
+            for i, k in enumerate(("self_attention", "text_cross_attention", "feed_forward")):
+                parts[k].append(ev[i].elapsed_time(ev[i + 1]) * 1000.0)
+            parts["block"].append(ev[0].elapsed_time(ev[3]) * 1000.0)
+        key = "gelu_fused_into_quantizer" if fuse else "production_flags"
+        rows[key] = {k: round(statistics.median(v), 1) for k, v in parts.items()}
+    rows["shape"] = f"vx (1,{M},4096), text context (1,{ctx_tokens},4096), 32 heads, FFN 16384; us per call"
+    return rows
 
 
 def attention_rows(seed: int, reps: int = 10) -> dict:
@@ -410,6 +454,9 @@ def main() -> None:
     if args.only == "attention":
         print(json.dumps(attention_rows(args.seed)))
         return
+    if args.only == "block":
+        print(json.dumps(block_rows(args.seed)))
+        return
     if args.only == "linears":
         print(json.dumps(linear_rows(args.seed)))
         return
@@ -473,6 +520,7 @@ def main() -> None:
         fused["copy_reference"] = copy_reference()
     attention = {} if args.no_fused else attention_rows(args.seed)
     linears = {} if args.no_fused else linear_rows(args.seed)
+    blk = {} if args.no_fused else block_rows(args.seed)
     cpu = None if args.no_cpu else cpu_baseline(x, s_in, w, s_w, bias)
 
     line = {
@@ -500,6 +548,7 @@ def main() -> None:
         "fused_ops": fused,
         "attention": attention,
         "fp8_linears": linears,
+        "video_block": blk,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

@@ -1,0 +1,223 @@
+"""One LTX-2.3 video transformer-block slice on this library's kernels, in the
+order the patched `BasicAVTransformerBlock.forward` runs its video branches
+with the production flags (ltx_serve/triton_ltx_ops.py:2989-3298):
+
+  self-attention   :3006-3083  AdaZero(shift 0, scale 1) -> to_q, to_k, to_v
+                               FP8 linears (:1671-1718) -> Q/K RMSNorm + RoPE
+                               (:1810-1875) -> attention (:2636) -> optional
+                               per-head gate (:2282-2302) -> to_out FP8 linear
+                               without bias (:762-781) -> residual gate + bias
+                               (gate 2, :3057-3064)
+  text cross-attn  :2810-2888  rms_norm -> AdaLN affine (6, 7); the context
+                               affine from the prompt table in torch (as in
+                               production, :2852-2856); the attention module's
+                               own forward: FP8 linears, q/k RMSNorm (torch),
+                               attention, to_out with bias -> residual gate
+                               (gate 8)
+  feed-forward     :3224-3258  AdaZero(3, 4) -> FP8 up-projection + bias ->
+                               GELU-tanh -> FP8 down-projection + bias ->
+                               residual gate (gate 5)
+
+`ltx_core` (the model library the reference patches) is not a dependency: the
+block's parameters are plain tensors and duck-typed FP8 linears carrying the
+attributes of the reference's FP8Linear (e4m3 `weight` [N, K], float32
+`weight_scale` and `input_scale`, bf16 `bias`). `random_video_block` draws
+synthetic parameters of the LTX-2.3 video block's shapes (no checkpoint).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from . import ltx_ops as L
+from .attention import attention_video
+
+_FP8 = torch.float8_e4m3fn
+
+
+class FP8Linear(torch.nn.Module):
+    """Per-tensor-scaled FP8 linear: weight codes e4m3 [out, in], weight and
+    input scales as float32 scalars, bf16 bias (or None)."""
+
+    def __init__(self, weight: torch.Tensor, weight_scale: torch.Tensor, input_scale: torch.Tensor,
+                 bias: torch.Tensor | None):
+        super().__init__()
+        self.weight = weight
+        self.weight_scale = weight_scale
+        self.input_scale = input_scale
+        self.bias = bias
+
+    @staticmethod
+    def quantized(w: torch.Tensor, input_scale: float, bias: torch.Tensor | None) -> "FP8Linear":
+        """From float weights: weight_scale = amax / 448, codes = e4m3(w / scale)."""
+        ws = (w.abs().amax().float() / 448.0).clamp_min(1e-12)
+        codes = (w.float() / ws).clamp(-448.0, 448.0).to(_FP8)
+        return FP8Linear(codes, ws.reshape(()), torch.tensor(float(input_scale), device=w.device), bias)
+
+
+@dataclass
+class VideoAttention:
+    to_q: FP8Linear
+    to_k: FP8Linear
+    to_v: FP8Linear
+    to_out: FP8Linear
+    q_norm_weight: torch.Tensor
+    k_norm_weight: torch.Tensor
+    heads: int
+    to_gate_logits: torch.nn.Linear | None = None
+
+
+@dataclass
+class VideoBlock:
+    table: torch.Tensor          # scale_shift_table (9, C)
+    prompt_table: torch.Tensor   # prompt_scale_shift_table (2, C)
+    attn1: VideoAttention        # video self-attention
+    attn2: VideoAttention        # video -> text cross-attention
+    ff_up: FP8Linear             # C -> 4C, GELU-tanh after it
+    ff_down: FP8Linear           # 4C -> C
+    eps: float = 1e-6
+
+
+def random_video_block(dim: int = 4096, heads: int = 32, context_dim: int = 4096, ff_mult: int = 4, *,
+                       gated: bool = False, seed: int = 0, device: str = "cuda") -> VideoBlock:
+    """Synthetic parameters of the LTX-2.3 video block's shapes: weights
+    ~N(0, 0.02), biases ~N(0, 0.01), norm weights ~1 + N(0, 0.05), tables
+    ~N(0, 0.02), input scales sized for unit-variance activations."""
+    gen = torch.Generator().manual_seed(seed)
+
+    def randn(*shape, std=1.0):
+        return (torch.randn(shape, generator=gen) * std).to(device)
+
+    def lin(n, k, input_scale):
+        return FP8Linear.quantized(randn(n, k, std=0.02), input_scale, randn(n, std=0.01).to(torch.bfloat16))
+
+    def attention(kv_dim):
+        return VideoAttention(
+            to_q=lin(dim, dim, 8.0 / 448), to_k=lin(dim, kv_dim, 8.0 / 448), to_v=lin(dim, kv_dim, 8.0 / 448),
+            to_out=lin(dim, dim, 2.0 / 448),
+            q_norm_weight=(1 + randn(dim, std=0.05)).to(torch.bfloat16),
+            k_norm_weight=(1 + randn(dim, std=0.05)).to(torch.bfloat16),
+            heads=heads,
+            to_gate_logits=None)
+
+    attn1 = attention(dim)
+    if gated:
+        gl = torch.nn.Linear(dim, heads, bias=True, device=device, dtype=torch.bfloat16)
+        with torch.no_grad():
+            gl.weight.copy_(randn(heads, dim, std=0.02))
+            gl.bias.copy_(randn(heads, std=0.1))
+        attn1.to_gate_logits = gl
+    return VideoBlock(
+        table=randn(9, dim, std=0.02).to(torch.bfloat16),
+        prompt_table=randn(2, context_dim, std=0.02).to(torch.bfloat16),
+        attn1=attn1,
+        attn2=attention(context_dim),
+        ff_up=lin(ff_mult * dim, dim, 8.0 / 448),
+        ff_down=lin(dim, ff_mult * dim, 4.0 / 448))
+
+
+@dataclass
+class Stages:
+    """Inputs and outputs of each step of a block slice, for per-step checks
+    (each tensor as the step saw or produced it)."""
+    t: dict = field(default_factory=dict)
+
+    def __setitem__(self, k, v):
+        self.t[k] = v
+
+    def __getitem__(self, k):
+        return self.t[k]
+
+
+def _rms_norm(x: torch.Tensor, eps: float, weight: torch.Tensor | None = None) -> torch.Tensor:
+    """ltx_core.utils.rms_norm / the attention module's q/k RMSNorm: torch's
+    rms_norm over the last dimension."""
+    return torch.nn.functional.rms_norm(x, (x.shape[-1],), weight=weight, eps=eps)
+
+
+def video_self_attention(block: VideoBlock, vx: torch.Tensor, timesteps: torch.Tensor, cos: torch.Tensor,
+                         sin: torch.Tensor, stages: Stages | None = None) -> torch.Tensor:
+    """:3006-3083 with `_attention_without_out_bias` (:2561-2648)."""
+    a = block.attn1
+    norm_vx = L.fused_adazero_from_ada(vx, block.eps, block.table, timesteps, shift_index=0, scale_index=1)
+    q = L.fp8_linear_forward(a.to_q, norm_vx)
+    k = L.fp8_linear_forward(a.to_k, norm_vx)
+    v = L.fp8_linear_forward(a.to_v, norm_vx)
+    qr, kr = L.fused_video_qk_rmsnorm_rope(q, k, a.q_norm_weight, a.k_norm_weight, block.eps, cos, sin)
+    o = attention_video(qr, kr, v, a.heads)
+    if a.to_gate_logits is not None:
+        gates = 2.0 * torch.sigmoid(a.to_gate_logits(norm_vx))
+        og = L.fused_head_gate_mul_bf16(o, gates, a.heads, o.shape[-1] // a.heads)
+    else:
+        gates, og = None, o
+    proj = L.fp8_linear_without_bias(a.to_out, og, out_dtype=og.dtype)
+    if proj is None:
+        raise RuntimeError("to_out is not an FP8 linear")
+    out = L.fused_residual_gate_bias_from_ada(vx, proj, a.to_out.bias, block.table, timesteps, gate_index=2)
+    if stages is not None:
+        for name, val in (("msa.x", vx), ("msa.norm", norm_vx), ("msa.q", q), ("msa.k", k), ("msa.v", v),
+                          ("msa.qr", qr), ("msa.kr", kr), ("msa.attn", o), ("msa.gates", gates),
+                          ("msa.gated", og), ("msa.proj", proj), ("msa.out", out)):
+            stages[name] = val
+    return out
+
+
+def video_text_cross_attention(block: VideoBlock, vx: torch.Tensor, context: torch.Tensor,
+                               timesteps: torch.Tensor, prompt_timestep: torch.Tensor,
+                               stages: Stages | None = None) -> torch.Tensor:
+    """:2810-2888 (cross_attention_adaln, production flags)."""
+    a = block.attn2
+    b = vx.shape[0]
+    shift_kv, scale_kv = (block.prompt_table[None, None].to(device=vx.device, dtype=vx.dtype)
+                          + prompt_timestep.reshape(b, prompt_timestep.shape[1], 2, -1)).unbind(dim=2)
+    enc = context * (1 + scale_kv) + shift_kv
+    normed = _rms_norm(vx, block.eps)
+    attn_in = L.fused_adaln_affine_from_ada(normed, block.table, timesteps, shift_index=6, scale_index=7)
+    q = _rms_norm(L.fp8_linear_forward(a.to_q, attn_in), block.eps, a.q_norm_weight)
+    k = _rms_norm(L.fp8_linear_forward(a.to_k, enc), block.eps, a.k_norm_weight)
+    v = L.fp8_linear_forward(a.to_v, enc)
+    o = attention_video(q, k, v, a.heads)
+    ca = L.fp8_linear_forward(a.to_out, o)
+    out = L.fused_residual_gate_from_ada(vx, ca, block.table, timesteps, gate_index=8)
+    if stages is not None:
+        for name, val in (("ca.x", vx), ("ca.enc", enc), ("ca.normed", normed), ("ca.in", attn_in), ("ca.q", q),
+                          ("ca.k", k), ("ca.v", v), ("ca.attn", o), ("ca.proj", ca), ("ca.out", out)):
+            stages[name] = val
+    return out
+
+
+def video_feed_forward(block: VideoBlock, vx: torch.Tensor, timesteps: torch.Tensor, *,
+                       fuse_gelu_quant: bool = False, stages: Stages | None = None) -> torch.Tensor:
+    """:3224-3258. With `fuse_gelu_quant` the GELU-tanh runs inside the
+    down-projection's input quantizer (`fused_gelu_tanh_fp8_quantize_e4m3`,
+    :164-182, off in the reference's production); otherwise torch's GELU
+    (tanh) in bf16, then the down-projection's own quantizer."""
+    y = L.fused_adazero_from_ada(vx, block.eps, block.table, timesteps, shift_index=3, scale_index=4)
+    h = L.fp8_linear_forward(block.ff_up, y)
+    if fuse_gelu_quant:
+        g = None
+        qg = L.fused_gelu_tanh_fp8_quantize_e4m3(h, block.ff_down.input_scale)
+        d = L.fp8_linear_from_quantized_e4m3(block.ff_down, qg, out_dtype=h.dtype)
+    else:
+        g = torch.nn.functional.gelu(h, approximate="tanh")
+        d = L.fp8_linear_forward(block.ff_down, g)
+    out = L.fused_residual_gate_from_ada(vx, d, block.table, timesteps, gate_index=5)
+    if stages is not None:
+        for name, val in (("ff.x", vx), ("ff.norm", y), ("ff.h", h), ("ff.gelu", g), ("ff.down", d),
+                          ("ff.out", out)):
+            stages[name] = val
+    return out
+
+
+def video_block_forward(block: VideoBlock, vx: torch.Tensor, context: torch.Tensor, timesteps: torch.Tensor,
+                        prompt_timestep: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, *,
+                        fuse_gelu_quant: bool = False, stages: Stages | None = None) -> torch.Tensor:
+    """The video branches of one block: self-attention, text cross-attention,
+    feed-forward (:2989-3298 without the audio and audio-video branches).
+    vx (B, N, C) bf16; context (B, T, C) bf16; timesteps (B, N, 9C) or a
+    stride-0 token axis; prompt_timestep (B, T, 2C); cos/sin [B or 1, H, N, 64]."""
+    vx = video_self_attention(block, vx, timesteps, cos, sin, stages)
+    vx = video_text_cross_attention(block, vx, context, timesteps, prompt_timestep, stages)
+    return video_feed_forward(block, vx, timesteps, fuse_gelu_quant=fuse_gelu_quant, stages=stages)
