@@ -138,13 +138,20 @@ def _rms_norm(x: torch.Tensor, eps: float, weight: torch.Tensor | None = None) -
 
 
 def video_self_attention(block: VideoBlock, vx: torch.Tensor, timesteps: torch.Tensor, cos: torch.Tensor,
-                         sin: torch.Tensor, stages: Stages | None = None) -> torch.Tensor:
-    """:3006-3083 with `_attention_without_out_bias` (:2561-2648)."""
+                         sin: torch.Tensor, stages: Stages | None = None, *, qkv_grouped: bool = False) -> torch.Tensor:
+    """:3006-3083 with `_attention_without_out_bias` (:2561-2648). With
+    `qkv_grouped` the three projections run as one grouped FP8 GEMM
+    (`fp8_qkv_from_grouped_mm`, :890-925; off in the reference's
+    production), otherwise as three FP8 linears."""
     a = block.attn1
     norm_vx = L.fused_adazero_from_ada(vx, block.eps, block.table, timesteps, shift_index=0, scale_index=1)
-    q = L.fp8_linear_forward(a.to_q, norm_vx)
-    k = L.fp8_linear_forward(a.to_k, norm_vx)
-    v = L.fp8_linear_forward(a.to_v, norm_vx)
+    qkv = L.fp8_qkv_from_grouped_mm(a, norm_vx) if qkv_grouped else None
+    if qkv is not None:
+        q, k, v = qkv
+    else:
+        q = L.fp8_linear_forward(a.to_q, norm_vx)
+        k = L.fp8_linear_forward(a.to_k, norm_vx)
+        v = L.fp8_linear_forward(a.to_v, norm_vx)
     qr, kr = L.fused_video_qk_rmsnorm_rope(q, k, a.q_norm_weight, a.k_norm_weight, block.eps, cos, sin)
     o = attention_video(qr, kr, v, a.heads)
     if a.to_gate_logits is not None:
@@ -213,11 +220,12 @@ def video_feed_forward(block: VideoBlock, vx: torch.Tensor, timesteps: torch.Ten
 
 def video_block_forward(block: VideoBlock, vx: torch.Tensor, context: torch.Tensor, timesteps: torch.Tensor,
                         prompt_timestep: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, *,
-                        fuse_gelu_quant: bool = False, stages: Stages | None = None) -> torch.Tensor:
+                        fuse_gelu_quant: bool = False, qkv_grouped: bool = False,
+                        stages: Stages | None = None) -> torch.Tensor:
     """The video branches of one block: self-attention, text cross-attention,
     feed-forward (:2989-3298 without the audio and audio-video branches).
     vx (B, N, C) bf16; context (B, T, C) bf16; timesteps (B, N, 9C) or a
     stride-0 token axis; prompt_timestep (B, T, 2C); cos/sin [B or 1, H, N, 64]."""
-    vx = video_self_attention(block, vx, timesteps, cos, sin, stages)
+    vx = video_self_attention(block, vx, timesteps, cos, sin, stages, qkv_grouped=qkv_grouped)
     vx = video_text_cross_attention(block, vx, context, timesteps, prompt_timestep, stages)
     return video_feed_forward(block, vx, timesteps, fuse_gelu_quant=fuse_gelu_quant, stages=stages)

@@ -86,20 +86,23 @@ def _check_attn(got, ref, v, what):
 
 @pytest.mark.parametrize("gated,fuse_gelu", [(False, False), (True, True)])
 def test_block_steps_match_oracle(gated, fuse_gelu):
-    """Every step of the slice against the oracle on that step's GPU inputs."""
+    """Every step of the slice against the oracle on that step's GPU inputs
+    (the second case also with the grouped Q/K/V projection)."""
     from opengenie_amd import ltx_ops as L
     from opengenie_amd.block import Stages, random_video_block, video_block_forward
 
     blk = random_video_block(C, HEADS, seed=11 + gated, gated=gated)
     vx, context, ts, pts, cos, sin = _g(*_inputs(300 + 7 * gated))
     st = Stages()
-    out = video_block_forward(blk, vx, context, ts, pts, cos, sin, fuse_gelu_quant=fuse_gelu, stages=st)
+    out = video_block_forward(blk, vx, context, ts, pts, cos, sin, fuse_gelu_quant=fuse_gelu, qkv_grouped=gated,
+                              stages=st)
     torch.cuda.synchronize()
     assert out.shape == vx.shape and out.dtype == torch.bfloat16
     calls = L.collect_hip_calls()
     for op in ("fused_adazero_from_ada", "fp8_scaled_mm", "fused_video_qk_rmsnorm_rope", "flash_attn_func",
                "fused_residual_gate_bias_from_ada", "fused_adaln_affine_from_ada", "fused_residual_gate_from_ada"):
         assert calls.get(op, 0) > 0, (op, calls)
+    assert (calls.get("fp8_grouped_linear", 0) > 0) == gated, calls
     tab, tsT = to_T(blk.table), to_T(ts)
     a1, a2 = blk.attn1, blk.attn2
 
