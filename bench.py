@@ -210,15 +210,16 @@ def block_rows(seed: int, reps: int = 5, ctx_tokens: int = 256) -> dict:
     st = torch.cuda.current_stream()
     rows = {}
     for fuse in (False, True):
-        # production flags; then the MI355X-side fusions (GELU inside the
-        # down-projection's quantizer, grouped Q/K/V projection)
+        # production flags; then the MI355X-side fusions (grouped Q/K/V,
+        # rms_norm + AdaLN as one AdaZero, GELU in the down-projection's
+        # quantizer)
         parts = {"self_attention": [], "text_cross_attention": [], "feed_forward": [], "block": []}
         for rep in range(reps + 2):
             ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
             ev[0].record(st)
             x1 = B.video_self_attention(blk, vx, ts, cos, sin, qkv_grouped=fuse)
             ev[1].record(st)
-            x2 = B.video_text_cross_attention(blk, x1, ctx, ts, pts)
+            x2 = B.video_text_cross_attention(blk, x1, ctx, ts, pts, fuse_norm=fuse)
             ev[2].record(st)
             B.video_feed_forward(blk, x2, ts, fuse_gelu_quant=fuse)
             ev[3].record(st)
@@ -228,7 +229,7 @@ def block_rows(seed: int, reps: int = 5, ctx_tokens: int = 256) -> dict:
             for i, k in enumerate(("self_attention", "text_cross_attention", "feed_forward")):
                 parts[k].append(ev[i].elapsed_time(ev[i + 1]) * 1000.0)
             parts["block"].append(ev[0].elapsed_time(ev[3]) * 1000.0)
-        key = "grouped_qkv_and_gelu_in_quantizer" if fuse else "production_flags"
+        key = "mi355x_fusions" if fuse else "production_flags"
         rows[key] = {k: round(statistics.median(v), 1) for k, v in parts.items()}
     rows["shape"] = f"vx (1,{M},4096), text context (1,{ctx_tokens},4096), 32 heads, FFN 16384; us per call"
     return rows

@@ -173,15 +173,22 @@ def video_self_attention(block: VideoBlock, vx: torch.Tensor, timesteps: torch.T
 
 def video_text_cross_attention(block: VideoBlock, vx: torch.Tensor, context: torch.Tensor,
                                timesteps: torch.Tensor, prompt_timestep: torch.Tensor,
-                               stages: Stages | None = None) -> torch.Tensor:
-    """:2810-2888 (cross_attention_adaln, production flags)."""
+                               stages: Stages | None = None, *, fuse_norm: bool = False) -> torch.Tensor:
+    """:2810-2888 (cross_attention_adaln, production flags). rms_norm
+    followed by the AdaLN affine of Ada rows 6/7 is AdaZero's composition
+    (R(R(R(rms_norm(x)) R(1 + scale)) + shift)); with `fuse_norm` it runs as
+    one AdaZero pass instead of torch's rms_norm and the affine kernel."""
     a = block.attn2
     b = vx.shape[0]
     shift_kv, scale_kv = (block.prompt_table[None, None].to(device=vx.device, dtype=vx.dtype)
                           + prompt_timestep.reshape(b, prompt_timestep.shape[1], 2, -1)).unbind(dim=2)
     enc = context * (1 + scale_kv) + shift_kv
-    normed = _rms_norm(vx, block.eps)
-    attn_in = L.fused_adaln_affine_from_ada(normed, block.table, timesteps, shift_index=6, scale_index=7)
+    if fuse_norm:
+        normed = None
+        attn_in = L.fused_adazero_from_ada(vx, block.eps, block.table, timesteps, shift_index=6, scale_index=7)
+    else:
+        normed = _rms_norm(vx, block.eps)
+        attn_in = L.fused_adaln_affine_from_ada(normed, block.table, timesteps, shift_index=6, scale_index=7)
     q = _rms_norm(L.fp8_linear_forward(a.to_q, attn_in), block.eps, a.q_norm_weight)
     k = _rms_norm(L.fp8_linear_forward(a.to_k, enc), block.eps, a.k_norm_weight)
     v = L.fp8_linear_forward(a.to_v, enc)
@@ -220,12 +227,12 @@ def video_feed_forward(block: VideoBlock, vx: torch.Tensor, timesteps: torch.Ten
 
 def video_block_forward(block: VideoBlock, vx: torch.Tensor, context: torch.Tensor, timesteps: torch.Tensor,
                         prompt_timestep: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, *,
-                        fuse_gelu_quant: bool = False, qkv_grouped: bool = False,
+                        fuse_gelu_quant: bool = False, qkv_grouped: bool = False, fuse_norm: bool = False,
                         stages: Stages | None = None) -> torch.Tensor:
     """The video branches of one block: self-attention, text cross-attention,
     feed-forward (:2989-3298 without the audio and audio-video branches).
     vx (B, N, C) bf16; context (B, T, C) bf16; timesteps (B, N, 9C) or a
     stride-0 token axis; prompt_timestep (B, T, 2C); cos/sin [B or 1, H, N, 64]."""
     vx = video_self_attention(block, vx, timesteps, cos, sin, stages, qkv_grouped=qkv_grouped)
-    vx = video_text_cross_attention(block, vx, context, timesteps, prompt_timestep, stages)
+    vx = video_text_cross_attention(block, vx, context, timesteps, prompt_timestep, stages, fuse_norm=fuse_norm)
     return video_feed_forward(block, vx, timesteps, fuse_gelu_quant=fuse_gelu_quant, stages=stages)

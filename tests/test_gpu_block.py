@@ -87,7 +87,9 @@ def _check_attn(got, ref, v, what):
 @pytest.mark.parametrize("gated,fuse_gelu", [(False, False), (True, True)])
 def test_block_steps_match_oracle(gated, fuse_gelu):
     """Every step of the slice against the oracle on that step's GPU inputs
-    (the second case also with the grouped Q/K/V projection)."""
+    (the second case with all the MI355X-side fusions: grouped Q/K/V, the
+    cross-attention's rms_norm + AdaLN as one AdaZero, GELU in the
+    down-projection's quantizer)."""
     from opengenie_amd import ltx_ops as L
     from opengenie_amd.block import Stages, random_video_block, video_block_forward
 
@@ -95,14 +97,16 @@ def test_block_steps_match_oracle(gated, fuse_gelu):
     vx, context, ts, pts, cos, sin = _g(*_inputs(300 + 7 * gated))
     st = Stages()
     out = video_block_forward(blk, vx, context, ts, pts, cos, sin, fuse_gelu_quant=fuse_gelu, qkv_grouped=gated,
-                              stages=st)
+                              fuse_norm=gated, stages=st)
     torch.cuda.synchronize()
     assert out.shape == vx.shape and out.dtype == torch.bfloat16
     calls = L.collect_hip_calls()
     for op in ("fused_adazero_from_ada", "fp8_scaled_mm", "fused_video_qk_rmsnorm_rope", "flash_attn_func",
-               "fused_residual_gate_bias_from_ada", "fused_adaln_affine_from_ada", "fused_residual_gate_from_ada"):
+               "fused_residual_gate_bias_from_ada", "fused_residual_gate_from_ada"):
         assert calls.get(op, 0) > 0, (op, calls)
     assert (calls.get("fp8_grouped_linear", 0) > 0) == gated, calls
+    assert (calls.get("fused_adaln_affine_from_ada", 0) > 0) == (not gated), calls
+    assert calls.get("fused_adazero_from_ada", 0) == (3 if gated else 2), calls
     tab, tsT = to_T(blk.table), to_T(ts)
     a1, a2 = blk.attn1, blk.attn2
 
@@ -123,9 +127,12 @@ def test_block_steps_match_oracle(gated, fuse_gelu):
     assert_same_bits(np32(st["msa.out"]), ref.v, "msa.out")
 
     # text cross-attention
-    nref = O.rms_norm(to_T(st["ca.x"]), EPS)
-    assert (bf16_ulp_distance(np32(st["ca.normed"]), nref.v) <= 1).all()
-    ref = O.adaln_affine_from_ada(to_T(st["ca.normed"]), tab, tsT, 6, 7)
+    if gated:  # rms_norm + AdaLN(6, 7) as one AdaZero pass
+        ref = O.adazero_from_ada(to_T(st["ca.x"]), EPS, tab, tsT, 6, 7)
+    else:
+        nref = O.rms_norm(to_T(st["ca.x"]), EPS)
+        assert (bf16_ulp_distance(np32(st["ca.normed"]), nref.v) <= 1).all()
+        ref = O.adaln_affine_from_ada(to_T(st["ca.normed"]), tab, tsT, 6, 7)
     assert_same_bits(np32(st["ca.in"]), ref.v, "ca.in")
     _check_attn(st["ca.attn"], _attn_ref(st["ca.q"], st["ca.k"], st["ca.v"]), st["ca.v"], "ca.attn")
     _check_linear(st["ca.proj"], _lin_ref(a2.to_out, to_T(st["ca.attn"])), "ca.proj")
