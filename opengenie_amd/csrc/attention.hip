@@ -39,9 +39,20 @@
 
 namespace oga {
 
-constexpr int kAD = 128;      // head dim
-constexpr int kAQ = 128;      // queries per workgroup
-constexpr int kAK = 64;       // keys per step
+#ifndef OGA_ATT_WAVES
+#define OGA_ATT_WAVES 8
+#endif
+#ifndef OGA_ATT_BUFS
+#define OGA_ATT_BUFS 3
+#endif
+constexpr int kAD = 128;                   // head dim
+constexpr int kAW = OGA_ATT_WAVES;         // waves per workgroup, 32 queries each
+constexpr int kAQ = 32 * kAW;              // queries per workgroup
+constexpr int kAK = 64;                    // keys per step
+constexpr int kABufs = OGA_ATT_BUFS;       // K/V tile pairs in the LDS ring
+constexpr int kADmaI = 16 / kAW;           // DMA instructions per wave per tile
+static_assert(kAW == 4 || kAW == 8, "4 or 8 waves");
+static_assert(kABufs == 2 || kABufs == 3, "2 or 3 tile pairs");
 constexpr int kATileU4 = kAK * kAD * 2 / 16;  // uint4 per K (or V) tile: 1024 (16 KiB)
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -127,19 +138,19 @@ static_assert(v_reads_conflict_free(), "transposing V reads would conflict");
 static_assert(folded_offsets_match(), "folded LDS offsets differ from tile_off");
 
 // DMA of one 64-key tile of K or V (bf16 rows of kAD elements) into LDS:
-// instruction i of wave w fills tile rows 4b .. 4b+3 (b = 4w + i); lane p
+// instruction i of wave w fills tile rows 4b .. 4b+3 (b = kADmaI w + i); lane p
 // writes the 16 bytes at row 4b + p/16, physical chunk p%16, i.e. logical
 // chunk (p%16) ^ swz(row%16). `off[i]` is that source's byte offset from the
 // tile's first key row; in the last, partial step rows past the last key
 // re-read the last key.
 struct TileSrc {
-  uint32_t off[4];
+  uint32_t off[kADmaI];
 };
 OGA_DEVICE TileSrc tile_src(int64_t row_stride, int64_t first_key, int64_t nk, int wv, int lane, bool clamp) {
   TileSrc t;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = (wv * 4 + i) * 4 + (lane >> 4);
+  for (int i = 0; i < kADmaI; ++i) {
+    const int row = (wv * kADmaI + i) * 4 + (lane >> 4);
     const int chunk = (lane & 15) ^ swz(row & 15);
     const int64_t r = clamp ? min((int64_t)row, nk - 1 - first_key) : (int64_t)row;
     t.off[i] = (uint32_t)(r * row_stride * 2 + chunk * 16);
@@ -148,9 +159,9 @@ OGA_DEVICE TileSrc tile_src(int64_t row_stride, int64_t first_key, int64_t nk, i
 }
 OGA_DEVICE void tile_dma(const char* tile_base, const TileSrc& t, uint4* dst, int wv) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    __builtin_amdgcn_global_load_lds((const void*)(tile_base + t.off[i]), (lds_void*)(dst + (wv * 4 + i) * 64), 16,
-                                     0, 0);
+  for (int i = 0; i < kADmaI; ++i)
+    __builtin_amdgcn_global_load_lds((const void*)(tile_base + t.off[i]),
+                                     (lds_void*)(dst + (wv * kADmaI + i) * 64), 16, 0, 0);
 }
 
 OGA_DEVICE uint32_t pack2(float a, float b) { return pack_bf16(a, b); }
@@ -184,11 +195,12 @@ OGA_DEVICE float sum_halves(float v) {
 }
 
 
-// LDS: [K0 | V0 | K1 | V1], 16 KiB each; step st uses buffer pair st % 2.
+// LDS: [K0 | V0 | K1 | V1 (| K2 | V2)], 16 KiB each; step st uses tile pair
+// st % kABufs, and the DMA of step st + kABufs - 1 goes out during step st.
 constexpr int kKBuf = 0, kVBuf = 16384, kParBytes = 32768;
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attention(AttnArgs a) {
-  __shared__ uint4 smem[4 * kATileU4];
+__global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attention(AttnArgs a) {
+  __shared__ uint4 smem[2 * kABufs * kATileU4];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   // Workgroups go to the 8 XCDs round-robin. With the remap, XCD x runs a
@@ -242,7 +254,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       tile_dma(vt, tile_src(a.v_sn, key0, a.nk, wv, lane, true), dV, wv);
     }
   };
+  // With three pairs the DMA runs two steps ahead; past the last step it
+  // re-reads the last tile (an index past it would put rows outside K/V)
+  // into a pair no later step reads, so that exactly one tile's DMA is sent
+  // after each step's own.
   dma_step(0, smem, smem + kATileU4);
+  if (kABufs == 3) dma_step(min((int64_t)1, nsteps - 1), smem + 2 * kATileU4, smem + 3 * kATileU4);
 
   // LDS read addresses (tile_off with the swizzle folded per lane):
   //  K fragment (key row 32j + ql, d = 16s + 8hl): kaddr[s] + 8192 j;
@@ -269,13 +286,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     constexpr int PAR = decltype(par_c)::value;
     constexpr int KB = PAR * kParBytes + kKBuf;
     constexpr int VB = PAR * kParBytes;  // vaddr already includes kVBuf
-    // This wave's DMA of step st has landed, then every wave's: the other
-    // pair is free. The wait is explicit because the barrier's workgroup
-    // fence does not wait for loads, and the LDS reads below are inline
-    // assembly the compiler does not order after the DMA.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (st + 1 < nsteps) dma_step(st + 1, smem + (2 - 2 * PAR) * kATileU4, smem + (3 - 2 * PAR) * kATileU4);
+    // This wave's DMA of step st has landed (with three pairs, the one DMA
+    // sent after it, of step st + 1, may stay in flight), then every wave's;
+    // every wave has also finished step st - 1, so its pair is free for the
+    // DMA of step st + kABufs - 1. The wait is explicit because the
+    // barrier's workgroup fence does not wait for loads, and the LDS reads
+    // below are inline assembly the compiler does not order after the DMA.
+    if (kABufs == 3)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"i"(2 * kADmaI) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // A bare barrier: __syncthreads()'s fence would add a vmcnt(0) (draining
+    // the DMA sent ahead); this wave's LDS reads of step st - 1 completed at
+    // that step's end (lgkmcnt(0)), and it writes LDS only by DMA.
+    asm volatile("s_barrier" ::: "memory");
+    {
+      constexpr int NP = (PAR + kABufs - 1) % kABufs;  // pair of step st + kABufs - 1
+      if (kABufs == 3)
+        dma_step(min(st + 2, nsteps - 1), smem + 2 * NP * kATileU4, smem + (2 * NP + 1) * kATileU4);
+      else if (st + 1 < nsteps)
+        dma_step(st + 1, smem + 2 * NP * kATileU4, smem + (2 * NP + 1) * kATileU4);
+    }
 
     // S^T blocks: key block j (keys 32j .. 32j+31) x the wave's 32 queries.
     f32x16 sacc[2];
@@ -392,10 +423,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     pv(IC<3>{}, vr1, vr0);
   };
 
-  for (int64_t st = 0; st < nsteps; st += 2) {
+  for (int64_t st = 0; st < nsteps; st += kABufs) {
     step(IC<0>{}, st);
     if (st + 1 < nsteps) step(IC<1>{}, st + 1);
+    if constexpr (kABufs == 3)
+      if (st + 2 < nsteps) step(IC<2 % kABufs>{}, st + 2);
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the re-reads past the last step
 
   // O = O^T / l: lane holds query q0 + ql, d = 32 dblk + 8 (e/4) + 4 hl + e%4.
   const float l_tot = sum_halves(l_run);
@@ -490,6 +524,6 @@ extern "C" int oga_attention(const void* q, const int64_t q_strides[3], const vo
   if (nqb > INT32_MAX || wgs > UINT32_MAX) return unsupported("too many query blocks");
   a.nqb = (int)nqb;
   a.xcd_remap = wgs % 8 == 0;
-  hipLaunchKernelGGL(k_attention, dim3((unsigned)wgs), dim3(256), 0, (hipStream_t)stream, a);
+  hipLaunchKernelGGL(k_attention, dim3((unsigned)wgs), dim3(64 * kAW), 0, (hipStream_t)stream, a);
   return launch_status();
 }
