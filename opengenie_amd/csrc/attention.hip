@@ -168,18 +168,28 @@ OGA_DEVICE uint32_t pack2(float a, float b) { return pack_bf16(a, b); }
 
 // LDS reads issued as inline assembly with immediate offsets, so that groups
 // of them stay in flight together and need no address arithmetic;
-// OGA_LGKM names the registers a wait makes valid.
+// OGA_LGKM names the registers a wait makes valid. The offset field holds
+// 16 bits: reads at 64 KiB and above (the third tile pair) move 64 KiB into
+// the address.
 template <int OFF>
 OGA_DEVICE bf16x8 lds_b128(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 2 * 65536, "LDS offset");
   uint4 v;
-  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  if constexpr (OFF >= 65536)
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr + 65536u), "i"(OFF - 65536));
+  else
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
   return __builtin_bit_cast(bf16x8, v);
 }
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 template <int OFF>
 OGA_DEVICE u32x2 lds_tr16(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 2 * 65536, "LDS offset");
   u32x2 v;
-  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  if constexpr (OFF >= 65536)
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr + 65536u), "i"(OFF - 65536));
+  else
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
   return v;
 }
 #define OGA_LGKM(N, ...) asm volatile("s_waitcnt lgkmcnt(" #N ")" : __VA_ARGS__)

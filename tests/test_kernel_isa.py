@@ -27,11 +27,15 @@ CSRC = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
 
 
 def _device_asm(src: str) -> str:
+    """The device assembly of src; the same source must also assemble (-S
+    alone does not check inline-assembly operands such as offset ranges)."""
     flags = [f for f in build.HIPCC_FLAGS if f not in ("-fPIC", "-Wall", "-Wno-unused-function")]
     with tempfile.TemporaryDirectory() as td:
         out = os.path.join(td, "k.s")
-        subprocess.run([build.hipcc(), *flags, "--cuda-device-only", "-S", "-o", out, src], check=True,
-                       capture_output=True)
+        for mode, path in (("-S", out), ("-c", os.path.join(td, "k.o"))):
+            res = subprocess.run([build.hipcc(), *flags, "--cuda-device-only", mode, "-o", path, src],
+                                 capture_output=True, text=True)
+            assert res.returncode == 0, res.stderr[-2000:]
         return open(out).read()
 
 
