@@ -442,20 +442,32 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the re-reads past the last step
 
   // O = O^T / l: lane holds query q0 + ql, d = 32 dblk + 8 (e/4) + 4 hl + e%4.
-  const float l_tot = sum_halves(l_run);
-  const int64_t qi = q0 + ql;
-  if (qi < a.nq) {
-    const float inv = 1.0f / l_tot;
-    uint16_t* orow = a.o + b * a.o_sb + qi * a.o_sn + (int64_t)h * a.o_sh;
+  // The wave's 32 x 128 tile goes through its own 8 KiB of LDS (free once
+  // every wave has finished its last step) so that each global store writes
+  // whole 256-byte query rows: stored straight from the registers, each row
+  // took 16 partial-line stores, and the partly written lines reached HBM
+  // more than once (up to 2.6x the output bytes at 8 waves per workgroup).
+  // 16-byte chunk c of row r sits at chunk c ^ (r % 16) of the row.
+  const float inv = 1.0f / sum_halves(l_run);
+  __syncthreads();
+  char* const otile = (char*)smem + wv * 8192;
 #pragma unroll
-    for (int dblk = 0; dblk < 4; ++dblk)
+  for (int dblk = 0; dblk < 4; ++dblk)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        uint2 w;
-        w.x = pack2(o[dblk][4 * g] * inv, o[dblk][4 * g + 1] * inv);
-        w.y = pack2(o[dblk][4 * g + 2] * inv, o[dblk][4 * g + 3] * inv);
-        *(uint2*)(orow + 32 * dblk + 8 * g + 4 * hl) = w;
-      }
+    for (int g = 0; g < 4; ++g) {
+      uint2 w;
+      w.x = pack2(o[dblk][4 * g] * inv, o[dblk][4 * g + 1] * inv);
+      w.y = pack2(o[dblk][4 * g + 2] * inv, o[dblk][4 * g + 3] * inv);
+      *(uint2*)(otile + ql * 256 + (((4 * dblk + g) ^ (ql & 15)) << 4) + 8 * hl) = w;
+    }
+  __syncthreads();
+  const int oc = lane & 15;
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int r = 4 * it + (lane >> 4);
+    const uint4 w = *(const uint4*)(otile + r * 256 + ((oc ^ (r & 15)) << 4));
+    const int64_t qr = q0 + r;
+    if (qr < a.nq) *(uint4*)(a.o + b * a.o_sb + qr * a.o_sn + (int64_t)h * a.o_sh + 8 * oc) = w;
   }
 }
 
