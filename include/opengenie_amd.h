@@ -228,6 +228,25 @@ int oga_attention(const void* q, const int64_t q_strides[3], const void* k, cons
                   int64_t nq, int64_t nk, int64_t heads, int64_t head_dim, float softmax_scale, void* stream);
 
 /*
+ * oga_attention with a caller-provided workspace of
+ * oga_attention_workspace_bytes(batch, nq, nk, heads, head_dim) bytes
+ * (16-byte aligned; 0 bytes and a null workspace run oga_attention). The
+ * kernel runs one workgroup per 256-query block per CU at a time; the blocks
+ * that would fill only part of a last round of the CUs (e.g. 1152 blocks on
+ * 256 CUs at 9216 tokens x 32 heads) are cut into 2..8 parts over their keys,
+ * whose float32 partial outputs, maxima and sums go to the workspace and are
+ * merged by a second kernel on the same stream. Results agree with
+ * oga_attention to float32 summation order. The size depends on the current
+ * device's CU count; a smaller workspace is an error.
+ * Same interface as oga_attention (benchmarks/official_ltx23_benchmark.py:3294-3369).
+ */
+int64_t oga_attention_workspace_bytes(int64_t batch, int64_t nq, int64_t nk, int64_t heads, int64_t head_dim);
+int oga_attention_ws(const void* q, const int64_t q_strides[3], const void* k, const int64_t k_strides[3],
+                     const void* v, const int64_t v_strides[3], void* o, const int64_t o_strides[3], int64_t batch,
+                     int64_t nq, int64_t nk, int64_t heads, int64_t head_dim, float softmax_scale, void* workspace,
+                     int64_t workspace_bytes, void* stream);
+
+/*
  * FP8 inputs of the attention (benchmarks/official_ltx23_benchmark.py
  * :3333-3340, descales from `fused_fp8_quantize_e4m3_per_head_4d`):
  * out[b, n, h, :] = R(e4m3(x8[b, n, h, :]) * descale[b, h]) as bf16;

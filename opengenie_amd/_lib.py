@@ -57,6 +57,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "oga_fp8_linear_grouped_ws": (_i32, [_p, _i64, _p, _i64, _p, _p, _p, _i32, _p, _i64, _i64, _i64, _i64, _i64, _p,
                                          _i64, _p]),
     "oga_attention": (_i32, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64, _f32, _p]),
+    "oga_attention_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64]),
+    "oga_attention_ws": (_i32, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64, _f32, _p,
+                                _i64, _p]),
     "oga_fp8_dequant_per_head": (_i32, [_p, _p, _p, _i64, _i64, _i64, _i64, _p]),
     "oga_selftest_convert": (_i32, [_p, _p, _p, _i64, _p]),
 }

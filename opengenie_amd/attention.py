@@ -105,8 +105,13 @@ def flash_attn_func(
     nk = k.shape[1]
     out = torch.empty((b, nq, h, d), device=q.device, dtype=torch.bfloat16)
     _hip("flash_attn_func")
-    _lib.call("oga_attention", q.data_ptr(), _strides3(q), k.data_ptr(), _strides3(k), v.data_ptr(), _strides3(v),
-              out.data_ptr(), _strides3(out), b, nq, nk, h, d, float(softmax_scale), _stream(q))
+    # Workspace for the key-split parts of a last partial round of blocks
+    # (torch's caching allocator makes the per-call tensor cheap).
+    ws_bytes = int(_lib.load().oga_attention_workspace_bytes(b, nq, nk, h, d))
+    ws = torch.empty((ws_bytes // 4,), device=q.device, dtype=torch.float32) if ws_bytes else None
+    _lib.call("oga_attention_ws", q.data_ptr(), _strides3(q), k.data_ptr(), _strides3(k), v.data_ptr(), _strides3(v),
+              out.data_ptr(), _strides3(out), b, nq, nk, h, d, float(softmax_scale),
+              ws.data_ptr() if ws is not None else None, ws_bytes, _stream(q))
     return out
 
 

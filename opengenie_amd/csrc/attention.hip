@@ -73,8 +73,18 @@ struct AttnArgs {
   int64_t nq, nk;
   int heads;
   int nqb;        // query blocks of kAQ per (batch, head)
-  int xcd_remap;  // workgroup count divisible by the 8 XCDs
+  int xcd_remap;  // nfull divisible by the 8 XCDs
   float scale_log2;  // softmax scale * log2(e)
+  // Workgroups 0 .. nfull-1 each own query block blockIdx.x (remapped) over
+  // all keys. The blocks nfull .. end, which would fill only part of a last
+  // round of the CUs, are cut into ksplit parts over their key steps: later
+  // workgroup nfull + u owns part u % ksplit of block nfull + u / ksplit and
+  // leaves its unnormalized O (part_o, [u][kAQ][kAD] float32) and its
+  // running max and sum (part_ml, [u][kAQ][2]) for k_attention_combine.
+  int64_t nfull;
+  int ksplit;
+  float* part_o;
+  float* part_ml;
 };
 
 OGA_DEVICE f32x16 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
@@ -218,7 +228,14 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
   // all query blocks of a head run together on one XCD and read that head's
   // K/V tiles through one L2.
   int64_t wg = blockIdx.x;
-  if (a.xcd_remap) wg = (wg & 7) * (int64_t)(gridDim.x >> 3) + (wg >> 3);
+  int part = -1;  // -1: all key steps
+  if (wg < a.nfull) {
+    if (a.xcd_remap) wg = (wg & 7) * (a.nfull >> 3) + (wg >> 3);
+  } else {
+    const int64_t u = wg - a.nfull;
+    wg = a.nfull + u / a.ksplit;
+    part = (int)(u % a.ksplit);
+  }
   const int qb = (int)(wg % a.nqb);
   const int64_t bh = wg / a.nqb;
   const int h = (int)(bh % a.heads);
@@ -239,7 +256,10 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
 
   const uint16_t* kbase = (const uint16_t*)a.k + b * a.k_sb + (int64_t)h * a.k_sh;
   const uint16_t* vbase = (const uint16_t*)a.v + b * a.v_sb + (int64_t)h * a.v_sh;
-  const int64_t nsteps = (a.nk + kAK - 1) / kAK;
+  // Key steps st_begin .. st_end - 1 (at least one: ksplit <= all steps).
+  const int64_t nsteps_all = (a.nk + kAK - 1) / kAK;
+  const int64_t st_begin = part < 0 ? 0 : nsteps_all * part / a.ksplit;
+  const int64_t st_end = part < 0 ? nsteps_all : nsteps_all * (part + 1) / a.ksplit;
 
   f32x16 o[4];
 #pragma unroll
@@ -268,8 +288,8 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
   // re-reads the last tile (an index past it would put rows outside K/V)
   // into a pair no later step reads, so that exactly one tile's DMA is sent
   // after each step's own.
-  dma_step(0, smem, smem + kATileU4);
-  if (kABufs == 3) dma_step(min((int64_t)1, nsteps - 1), smem + 2 * kATileU4, smem + 3 * kATileU4);
+  dma_step(st_begin, smem, smem + kATileU4);
+  if (kABufs == 3) dma_step(min(st_begin + 1, st_end - 1), smem + 2 * kATileU4, smem + 3 * kATileU4);
 
   // LDS read addresses (tile_off with the swizzle folded per lane):
   //  K fragment (key row 32j + ql, d = 16s + 8hl): kaddr[s] + 8192 j;
@@ -313,8 +333,8 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
     {
       constexpr int NP = (PAR + kABufs - 1) % kABufs;  // pair of step st + kABufs - 1
       if (kABufs == 3)
-        dma_step(min(st + 2, nsteps - 1), smem + 2 * NP * kATileU4, smem + (2 * NP + 1) * kATileU4);
-      else if (st + 1 < nsteps)
+        dma_step(min(st + 2, st_end - 1), smem + 2 * NP * kATileU4, smem + (2 * NP + 1) * kATileU4);
+      else if (st + 1 < st_end)
         dma_step(st + 1, smem + 2 * NP * kATileU4, smem + (2 * NP + 1) * kATileU4);
     }
 
@@ -433,11 +453,11 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
     pv(IC<3>{}, vr1, vr0);
   };
 
-  for (int64_t st = 0; st < nsteps; st += kABufs) {
+  for (int64_t st = st_begin; st < st_end; st += kABufs) {
     step(IC<0>{}, st);
-    if (st + 1 < nsteps) step(IC<1>{}, st + 1);
+    if (st + 1 < st_end) step(IC<1>{}, st + 1);
     if constexpr (kABufs == 3)
-      if (st + 2 < nsteps) step(IC<2 % kABufs>{}, st + 2);
+      if (st + 2 < st_end) step(IC<2 % kABufs>{}, st + 2);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the re-reads past the last step
 
@@ -448,6 +468,22 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
   // took 16 partial-line stores, and the partly written lines reached HBM
   // more than once (up to 2.6x the output bytes at 8 waves per workgroup).
   // 16-byte chunk c of row r sits at chunk c ^ (r % 16) of the row.
+  if (part >= 0) {
+    // A part of a split block (every wave of the workgroup takes this
+    // branch, so none waits at the barriers below): O^T rows unnormalized,
+    // with m_run and the query's sum over this part's keys.
+    const int64_t row = (int64_t)(blockIdx.x - a.nfull) * kAQ + wv * 32 + ql;
+    float* po = a.part_o + row * kAD;
+#pragma unroll
+    for (int dblk = 0; dblk < 4; ++dblk)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *(float4*)(po + 32 * dblk + 8 * g + 4 * hl) =
+            make_float4(o[dblk][4 * g], o[dblk][4 * g + 1], o[dblk][4 * g + 2], o[dblk][4 * g + 3]);
+    const float l_tot = sum_halves(l_run);
+    if (hl == 0) *(float2*)(a.part_ml + 2 * row) = make_float2(m_run, l_tot);
+    return;
+  }
   const float inv = 1.0f / sum_halves(l_run);
   __syncthreads();
   char* const otile = (char*)smem + wv * 8192;
@@ -469,6 +505,46 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int64_t qr = q0 + r;
     if (qr < a.nq) *(uint4*)(a.o + b * a.o_sb + qr * a.o_sn + (int64_t)h * a.o_sh + 8 * oc) = w;
   }
+}
+
+// The split blocks' parts merged: for query row r of split block sb (block
+// nfull + sb), with parts p of running max m_p and sum l_p,
+// O = sum_p 2^(m_p - M) O_p / sum_p 2^(m_p - M) l_p, M = max_p m_p. One
+// thread per (row, 8 consecutive d); rows past nq are not stored.
+__global__ __launch_bounds__(256) void k_attention_combine(AttnArgs a, int64_t rows) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= rows * (kAD / 8)) return;
+  const int c = (int)(idx % (kAD / 8));
+  const int64_t row = idx / (kAD / 8);
+  const int64_t sb = row / kAQ;
+  const int qr = (int)(row % kAQ);
+  const int64_t wg = a.nfull + sb;
+  const int qb = (int)(wg % a.nqb);
+  const int64_t bh = wg / a.nqb;
+  const int h = (int)(bh % a.heads);
+  const int64_t b = bh / a.heads;
+  const int64_t qi = (int64_t)qb * kAQ + qr;
+  if (qi >= a.nq) return;
+  const int64_t r0 = sb * a.ksplit * kAQ + qr;  // row of part 0; part p adds p * kAQ
+  float mx = -INFINITY;
+  for (int p = 0; p < a.ksplit; ++p) mx = __builtin_fmaxf(mx, a.part_ml[2 * (r0 + (int64_t)p * kAQ)]);
+  float l = 0.0f, acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  for (int p = 0; p < a.ksplit; ++p) {
+    const int64_t rp = r0 + (int64_t)p * kAQ;
+    const float w = __builtin_amdgcn_exp2f(a.part_ml[2 * rp] - mx);
+    l += w * a.part_ml[2 * rp + 1];
+    const float4 x0 = *(const float4*)(a.part_o + rp * kAD + 8 * c);
+    const float4 x1 = *(const float4*)(a.part_o + rp * kAD + 8 * c + 4);
+    acc[0] += w * x0.x; acc[1] += w * x0.y; acc[2] += w * x0.z; acc[3] += w * x0.w;
+    acc[4] += w * x1.x; acc[5] += w * x1.y; acc[6] += w * x1.z; acc[7] += w * x1.w;
+  }
+  const float inv = 1.0f / l;
+  uint4 w;
+  w.x = pack2(acc[0] * inv, acc[1] * inv);
+  w.y = pack2(acc[2] * inv, acc[3] * inv);
+  w.z = pack2(acc[4] * inv, acc[5] * inv);
+  w.w = pack2(acc[6] * inv, acc[7] * inv);
+  *(uint4*)(a.o + b * a.o_sb + qi * a.o_sn + (int64_t)h * a.o_sh + 8 * c) = w;
 }
 
 // out[b, n, h, d] = R(e4m3(x8[b, n, h, d]) * descale[b, h]); 16 values per
@@ -517,10 +593,50 @@ extern "C" int oga_fp8_dequant_per_head(const void* x8, const float* descale, vo
   return launch_status();
 }
 
-extern "C" int oga_attention(const void* q, const int64_t q_strides[3], const void* k, const int64_t k_strides[3],
-                             const void* v, const int64_t v_strides[3], void* o, const int64_t o_strides[3],
-                             int64_t batch, int64_t nq, int64_t nk, int64_t heads, int64_t head_dim,
-                             float softmax_scale, void* stream) {
+namespace {
+// Workgroups of k_attention resident at once on the current device (CUs x
+// workgroups per CU), cached per device; 0 if the runtime cannot say.
+int64_t attention_slots() {
+  static int64_t cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_attention, 64 * kAW, 0) != hipSuccess)
+      return 0;
+    cache[dev] = (int64_t)cus * per_cu > 0 ? (int64_t)cus * per_cu : -1;
+  }
+  return cache[dev] > 0 ? cache[dev] : 0;
+}
+
+struct AttnPlan {
+  int64_t wgs, nfull, units;  // query blocks, whole ones, split parts
+  int ksplit;
+};
+// Blocks beyond the last whole round of the CUs are cut into k parts over
+// their key steps (k <= 8 and <= the steps) when that shortens the last
+// round by at least a tenth of a round: rem blocks in k parts take
+// ceil(k rem / slots) rounds of 1/k of a block's time.
+AttnPlan attention_plan(int64_t wgs, int64_t nk, int64_t slots) {
+  AttnPlan p{wgs, wgs, 0, 1};
+  const int64_t rem = slots > 0 ? wgs % slots : 0;
+  if (rem == 0) return p;
+  const int64_t nsteps = (nk + kAK - 1) / kAK;
+  double best = 1.0;
+  for (int k = 2; k <= 8 && k <= nsteps; ++k) {
+    const double c = (double)((k * rem + slots - 1) / slots) / k;
+    if (c < best - 0.1) { best = c; p.ksplit = k; }
+  }
+  if (p.ksplit > 1) { p.nfull = wgs - rem; p.units = rem * p.ksplit; }
+  return p;
+}
+int64_t attention_ws_bytes(const AttnPlan& p) { return p.units * kAQ * (kAD + 2) * (int64_t)sizeof(float); }
+
+int attention_run(const void* q, const int64_t q_strides[3], const void* k, const int64_t k_strides[3],
+                  const void* v, const int64_t v_strides[3], void* o, const int64_t o_strides[3], int64_t batch,
+                  int64_t nq, int64_t nk, int64_t heads, int64_t head_dim, float softmax_scale, void* workspace,
+                  int64_t workspace_bytes, void* stream) {
   if (!q || !k || !v || !o || !q_strides || !k_strides || !v_strides || !o_strides) return fail("null pointer");
   if (head_dim != kAD) return unsupported("head_dim must be %d", kAD);
   if (batch < 0 || nq < 0 || nk < 0 || heads < 0) return fail("bad shape");
@@ -533,6 +649,8 @@ extern "C" int oga_attention(const void* q, const int64_t q_strides[3], const vo
   if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(o, 16))
     return fail("q/k/v/o must be 16-byte aligned");
   if (!(softmax_scale > 0.0f) || !__builtin_isfinite(softmax_scale)) return unsupported("softmax_scale must be positive");
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace)) return fail("bad workspace");
+  if (workspace && !aligned(workspace, 16)) return fail("workspace must be 16-byte aligned");
   AttnArgs a{};
   a.q = q; a.k = k; a.v = v; a.o = (uint16_t*)o;
   a.q_sb = q_strides[0]; a.q_sn = q_strides[1]; a.q_sh = q_strides[2];
@@ -543,9 +661,49 @@ extern "C" int oga_attention(const void* q, const int64_t q_strides[3], const vo
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   const int64_t nqb = (nq + kAQ - 1) / kAQ;
   const int64_t wgs = nqb * heads * batch;
-  if (nqb > INT32_MAX || wgs > UINT32_MAX) return unsupported("too many query blocks");
+  if (nqb > INT32_MAX || wgs > UINT32_MAX / 8) return unsupported("too many query blocks");
   a.nqb = (int)nqb;
-  a.xcd_remap = wgs % 8 == 0;
-  hipLaunchKernelGGL(k_attention, dim3((unsigned)wgs), dim3(64 * kAW), 0, (hipStream_t)stream, a);
+  AttnPlan plan{wgs, wgs, 0, 1};
+  if (workspace_bytes > 0) {
+    plan = attention_plan(wgs, nk, attention_slots());
+    if (attention_ws_bytes(plan) > workspace_bytes) return fail("workspace smaller than oga_attention_workspace_bytes");
+  }
+  a.nfull = plan.nfull;
+  a.ksplit = plan.ksplit;
+  a.part_o = (float*)workspace;
+  a.part_ml = plan.units ? (float*)workspace + plan.units * kAQ * kAD : nullptr;
+  a.xcd_remap = plan.nfull % 8 == 0;
+  hipLaunchKernelGGL(k_attention, dim3((unsigned)(plan.nfull + plan.units)), dim3(64 * kAW), 0,
+                     (hipStream_t)stream, a);
+  if (plan.units) {
+    const int64_t rows = (wgs - plan.nfull) * kAQ;
+    hipLaunchKernelGGL(k_attention_combine, dim3((unsigned)((rows * (kAD / 8) + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, a, rows);
+  }
   return launch_status();
+}
+}  // namespace
+
+extern "C" int oga_attention(const void* q, const int64_t q_strides[3], const void* k, const int64_t k_strides[3],
+                             const void* v, const int64_t v_strides[3], void* o, const int64_t o_strides[3],
+                             int64_t batch, int64_t nq, int64_t nk, int64_t heads, int64_t head_dim,
+                             float softmax_scale, void* stream) {
+  return attention_run(q, q_strides, k, k_strides, v, v_strides, o, o_strides, batch, nq, nk, heads, head_dim,
+                       softmax_scale, nullptr, 0, stream);
+}
+
+extern "C" int64_t oga_attention_workspace_bytes(int64_t batch, int64_t nq, int64_t nk, int64_t heads,
+                                                 int64_t head_dim) {
+  if (batch <= 0 || nq <= 0 || nk <= 0 || heads <= 0 || head_dim != kAD) return 0;
+  const int64_t nqb = (nq + kAQ - 1) / kAQ;
+  if (nqb > INT32_MAX || heads > INT32_MAX || nqb * heads > (int64_t)(UINT32_MAX / 8) / batch) return 0;
+  return attention_ws_bytes(attention_plan(nqb * heads * batch, nk, attention_slots()));
+}
+
+extern "C" int oga_attention_ws(const void* q, const int64_t q_strides[3], const void* k, const int64_t k_strides[3],
+                                const void* v, const int64_t v_strides[3], void* o, const int64_t o_strides[3],
+                                int64_t batch, int64_t nq, int64_t nk, int64_t heads, int64_t head_dim,
+                                float softmax_scale, void* workspace, int64_t workspace_bytes, void* stream) {
+  return attention_run(q, q_strides, k, k_strides, v, v_strides, o, o_strides, batch, nq, nk, heads, head_dim,
+                       softmax_scale, workspace, workspace_bytes, stream);
 }

@@ -72,6 +72,32 @@ def test_attention_matches_oracle(b, nq, nk, h):
     _check(out, _ref(q, k, v), f"attn b{b} nq{nq} nk{nk} h{h}")
 
 
+@pytest.mark.parametrize("b,nq,nk,h", [(1, 128, 1000, 1), (1, 2048, 700, 20)])
+def test_attention_key_split_and_whole_agree(b, nq, nk, h):
+    """flash_attn_func cuts a last partial round of query blocks into key
+    parts merged by a second kernel (oga_attention_ws); oga_attention runs
+    every block over all keys. Both meet the oracle bar, and they differ only
+    in float32 summation order."""
+    from opengenie_amd import _lib
+    from opengenie_amd.attention import _strides3, flash_attn_func
+
+    q = randn((b, nq, h, 128), 800 + nq).to(DEV)
+    k = randn((b, nk, h, 128), 801 + nk).to(DEV)
+    v = randn((b, nk, h, 128), 802 + nk).to(DEV)
+    assert _lib.load().oga_attention_workspace_bytes(b, nq, nk, h, 128) > 0  # the split path runs
+    split = flash_attn_func(q, k, v)
+    whole = torch.empty_like(q)
+    _lib.call("oga_attention", q.data_ptr(), _strides3(q), k.data_ptr(), _strides3(k), v.data_ptr(), _strides3(v),
+              whole.data_ptr(), _strides3(whole), b, nq, nk, h, 128, 128 ** -0.5,
+              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    ref = _ref(q.cpu(), k.cpu(), v.cpu())
+    _check(split, ref, f"attn split b{b} nq{nq} nk{nk} h{h}")
+    _check(whole, ref, f"attn whole b{b} nq{nq} nk{nk} h{h}")
+    diff = (split.float() - whole.float()).abs()
+    assert float(diff.max()) <= 2 ** -7 * float(whole.float().abs().max()), float(diff.max())
+
+
 def test_attention_scale_and_large_scores():
     """A larger softmax scale sharpens the distribution (online max matters)."""
     from opengenie_amd.attention import flash_attn_func
