@@ -98,6 +98,38 @@ def test_attention_key_split_and_whole_agree(b, nq, nk, h):
     assert float(diff.max()) <= 2 ** -7 * float(whole.float().abs().max()), float(diff.max())
 
 
+def test_attention_workspace_contract():
+    """A workspace smaller than the query's size is an argument error (the
+    output untouched); no workspace (null, 0 bytes) runs every block whole,
+    bit-identical to oga_attention."""
+    from opengenie_amd import _lib
+    from opengenie_amd.attention import _strides3
+
+    b, nq, nk, h = 1, 256, 400, 3
+    q = randn((b, nq, h, 128), 900).to(DEV)
+    k = randn((b, nk, h, 128), 901).to(DEV)
+    v = randn((b, nk, h, 128), 902).to(DEV)
+    lib = _lib.load()
+    st = torch.cuda.current_stream().cuda_stream
+    need = int(lib.oga_attention_workspace_bytes(b, nq, nk, h, 128))
+    assert need > 0 and need % 16 == 0
+    assert lib.oga_attention_workspace_bytes(b, nq, nk, h, 64) == 0
+    args = lambda o: (q.data_ptr(), _strides3(q), k.data_ptr(), _strides3(k), v.data_ptr(), _strides3(v),
+                      o.data_ptr(), _strides3(o), b, nq, nk, h, 128, 128 ** -0.5)
+    small = torch.empty((need // 4,), device=DEV, dtype=torch.float32)
+    out = torch.zeros_like(q)
+    rc = lib.oga_attention_ws(*args(out), small.data_ptr(), need - 16, st)
+    assert rc < 0 and b"workspace" in lib.oga_last_error()
+    torch.cuda.synchronize()
+    assert not out.any()
+    none = torch.empty_like(q)
+    assert lib.oga_attention_ws(*args(none), None, 0, st) == 0
+    whole = torch.empty_like(q)
+    assert lib.oga_attention(*args(whole), st) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(none.view(torch.int16), whole.view(torch.int16))
+
+
 def test_attention_scale_and_large_scores():
     """A larger softmax scale sharpens the distribution (online max matters)."""
     from opengenie_amd.attention import flash_attn_func
