@@ -34,6 +34,8 @@
 // LDS tiles: key row r (256 bytes = 16 chunks of 16 B) keeps chunk c at
 // physical chunk c ^ swz(r % 16), so both the 32-row fragment reads and the
 // transposing reads are free of bank conflicts.
+#include <atomic>
+
 #include "common.h"
 #include "host.h"
 
@@ -595,19 +597,22 @@ extern "C" int oga_fp8_dequant_per_head(const void* x8, const float* descale, vo
 
 namespace {
 // Workgroups of k_attention resident at once on the current device (CUs x
-// workgroups per CU), cached per device; 0 if the runtime cannot say.
+// workgroups per CU), cached per device (relaxed atomics: threads filling an
+// entry at once store the same value); 0 if the runtime cannot say.
 int64_t attention_slots() {
-  static int64_t cache[64] = {};
+  static std::atomic<int64_t> cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cache[dev] == 0) {
+  int64_t n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_attention, 64 * kAW, 0) != hipSuccess)
       return 0;
-    cache[dev] = (int64_t)cus * per_cu > 0 ? (int64_t)cus * per_cu : -1;
+    n = (int64_t)cus * per_cu > 0 ? (int64_t)cus * per_cu : -1;
+    cache[dev].store(n, std::memory_order_relaxed);
   }
-  return cache[dev] > 0 ? cache[dev] : 0;
+  return n > 0 ? n : 0;
 }
 
 struct AttnPlan {

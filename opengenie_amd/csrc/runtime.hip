@@ -1,5 +1,6 @@
 // Library identification, argument-error reporting and device queries.
 #include <stdarg.h>
+#include <atomic>
 #include <stdio.h>
 
 #include "host.h"
@@ -29,16 +30,18 @@ int unsupported(const char* fmt, ...) {
   return r;
 }
 
+// Per-device cache; callers on several threads may fill an entry at once
+// (with the same value), hence the relaxed atomics.
 int cu_count() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached[dev] = n;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 }  // namespace oga
