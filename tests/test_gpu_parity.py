@@ -464,10 +464,12 @@ def test_fp8_linear(m, n, k, bias_dtype):
     assert (bf16_ulp_distance(got, ref) > 1).mean() < 1e-2
 
 
-@pytest.mark.parametrize("m,n,k", [(2304, 8192, 512), (4352, 4096, 1024)])
+@pytest.mark.parametrize("m,n,k", [(4352, 4096, 4096), (4352, 4096, 8192)])
 def test_fp8_linear_split_k_through_c_abi(m, n, k):
     """The split-K schedule (workspace given) and the whole-tile schedule
-    (no workspace) through the C ABI, both against the oracle."""
+    (no workspace) through the C ABI, both against the oracle. 272 tiles on
+    256 CUs leave 16 for a last round, each cut into 16 K-chunks (of 256 at
+    K = 4096, of 512 at K = 8192)."""
     from opengenie_amd import _lib
 
     lib = _lib.load()
