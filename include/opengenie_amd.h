@@ -113,10 +113,19 @@ int oga_head_gate_mul_bf16(const void* x, const void* gates, int64_t g_s0, int64
 int oga_fp8_quantize_e4m3(const void* x, const float* scale, int scale_is_0dim, void* q, int64_t n,
                           void* stream);
 
-/* `fused_gelu_tanh_fp8_quantize_e4m3` (triton_ltx_ops.py:164-182): the
- * quantizer above applied to R(gelu_tanh(x)). */
+/* `fused_gelu_tanh_fp8_quantize_e4m3` (triton_ltx_ops.py:164-182; torch
+ * path :165-169): the quantizer above applied to R(gelu_tanh(x)), with the
+ * GELU evaluated in float32 exactly as torch's GPU kernel evaluates
+ * gelu(approximate='tanh') (the device tanhf), so the codes equal torch's. */
 int oga_gelu_tanh_fp8_quantize_e4m3(const void* x, const float* scale, int scale_is_0dim, void* q,
                                     int64_t n, void* stream);
+
+/* Opt-in inexact variant of oga_gelu_tanh_fp8_quantize_e4m3 (no reference
+ * counterpart): GELU as x / (1 + 2^a) with the hardware exp2 and reciprocal,
+ * about a fifth faster at the FFN shape; a small fraction of its bf16 GELU
+ * values (and the codes they feed) differ from torch's by one step. */
+int oga_gelu_tanh_fp8_quantize_e4m3_fast(const void* x, const float* scale, int scale_is_0dim, void* q,
+                                         int64_t n, void* stream);
 
 /*
  * `fused_fp8_quantize_e4m3_per_head_4d` (triton_ltx_ops.py:265-317; torch
@@ -262,6 +271,17 @@ int oga_fp8_dequant_per_head(const void* x8, const float* descale, void* out, in
  * lets a test pin the hardware conversions against the oracle bit by bit.
  */
 int oga_selftest_convert(const float* in, uint16_t* bf16_out, uint8_t* e4m3_out, int64_t n, void* stream);
+
+/*
+ * Schedule query of the token-row kernels: how many token rows of one batch
+ * a single wave streams in sequence for an op of `kind` at this shape on the
+ * current device (OGA_ROWS_ADAZERO: oga_adazero[_from_ada];
+ * OGA_ROWS_ELEMENTWISE: the AdaLN affine, mul and residual-gate ops). 0 for
+ * an unsupported shape. No reference counterpart; it lets a test show that
+ * a shape reaches the multi-row code path of a kernel.
+ */
+enum { OGA_ROWS_ADAZERO = 0, OGA_ROWS_ELEMENTWISE = 1 };
+int64_t oga_rows_per_wave(int kind, int64_t batch, int64_t tokens, int64_t cols);
 
 #ifdef __cplusplus
 }

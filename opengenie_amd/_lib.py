@@ -15,6 +15,8 @@ LIB_PATH = os.path.join(HERE, "libopengenie_amd.so")
 
 DT_BF16 = 0
 DT_F32 = 1
+ROWS_ADAZERO = 0
+ROWS_ELEMENTWISE = 1
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int
@@ -41,6 +43,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "oga_head_gate_mul_bf16": (_i32, [_p, _p, _i64, _i64, _p, _i64, _i64, _i64, _p]),
     "oga_fp8_quantize_e4m3": (_i32, [_p, _p, _i32, _p, _i64, _p]),
     "oga_gelu_tanh_fp8_quantize_e4m3": (_i32, [_p, _p, _i32, _p, _i64, _p]),
+    "oga_gelu_tanh_fp8_quantize_e4m3_fast": (_i32, [_p, _p, _i32, _p, _i64, _p]),
     "oga_fp8_per_head_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "oga_fp8_quantize_per_head": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _p]),
     "oga_video_qk_rmsnorm_rope": (_i32, [_p, _p, _p, _p, _i32, _p, _p, _i32, _i64p, _i64p, _p, _p, _i64, _i64,
@@ -62,6 +65,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                 _i64, _p]),
     "oga_fp8_dequant_per_head": (_i32, [_p, _p, _p, _i64, _i64, _i64, _i64, _p]),
     "oga_selftest_convert": (_i32, [_p, _p, _p, _i64, _p]),
+    "oga_rows_per_wave": (_i64, [_i32, _i64, _i64, _i64]),
 }
 
 _lock = threading.Lock()

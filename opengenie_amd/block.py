@@ -194,7 +194,7 @@ def video_text_cross_attention(block: VideoBlock, vx: torch.Tensor, context: tor
     v = L.fp8_linear_forward(a.to_v, enc)
     o = attention_video(q, k, v, a.heads)
     ca = L.fp8_linear_forward(a.to_out, o)
-    out = L.fused_residual_gate_from_ada(vx, ca, block.table, timesteps, gate_index=8)
+    out = L.fused_residual_gate_from_ada(vx, ca, block.table, timesteps, gate_index=8, count_video_ada=False)
     if stages is not None:
         for name, val in (("ca.x", vx), ("ca.enc", enc), ("ca.normed", normed), ("ca.in", attn_in), ("ca.q", q),
                           ("ca.k", k), ("ca.v", v), ("ca.attn", o), ("ca.proj", ca), ("ca.out", out)):

@@ -206,15 +206,6 @@ OGA_DEVICE double wave_sum_d(double v) {
   return __builtin_bit_cast(double, a) + __builtin_bit_cast(double, b);
 }
 
-// Max over the 16 lanes of each DPP row (all 16 lanes get the row's max).
-OGA_DEVICE float row16_max(float v) {
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true)));
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true)));
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true)));
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true)));
-  return v;
-}
-
 // Value held by lane (l ^ 8) inside the same 16-lane row: row_ror:8.
 OGA_DEVICE uint32_t row_swap8(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, true);

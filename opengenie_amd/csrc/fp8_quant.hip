@@ -16,19 +16,36 @@
 
 namespace oga {
 
-// GELU-tanh, torch gelu(approximate='tanh'): 0.5 x (1 + tanh(u)) with
-// u = sqrt(2/pi) (x + 0.044715 x^3), evaluated as the same function
-// x / (1 + exp(-2u)) = x / (1 + 2^a), a = x (c0 + c1 x^2): one v_exp_f32 and a
-// Newton-refined v_rcp_f32 instead of a library tanh, and no cancellation in
-// 1 + tanh(u) for negative x. Rounded once to bf16. Where 2^a would pass 2^64
-// (x below about -7.7) the result is x * 0: -0 as torch's saturated tanh
-// gives, and NaN for -inf as torch does.
+// GELU-tanh as torch's GPU kernel for gelu(approximate='tanh') evaluates it
+// in float32 for a bf16 input (ATen GeluCUDAKernelImpl):
+//   inner = kBeta * (x + kKappa * x^3),  x^3 = (x * x) * x,
+//   g     = (0.5 * x) * (1 + tanh(inner)),  rounded once to bf16,
+// kBeta = float(sqrt(2) * 2/sqrt(pi) * 0.5), kKappa = float(0.044715), tanh
+// the ROCm device library's tanhf. torch is compiled with the HIP default
+// -ffp-contract=fast, so x + kKappa * x^3 is one fused multiply-add; every
+// other step is a separate float32 operation. The result is the same bf16
+// value torch produces for every one of the 65536 bf16 inputs.
+constexpr int kGeluNone = 0, kGeluExact = 1, kGeluFast = 2;
+constexpr float kGeluBeta = (float)(M_SQRT2 * M_2_SQRTPI * 0.5);
+constexpr float kGeluKappa = 0.044715f;
+// The opt-in fast form (kGeluFast) evaluates the same function as
+// x / (1 + exp(-2 inner)) = x / (1 + 2^a), a = x (c0 + c1 x^2), with one
+// v_exp_f32 and a Newton-refined v_rcp_f32: about 20 % faster at the FFN
+// shape but rounded differently, so a small fraction of bf16 results (and
+// of the e4m3 codes they feed) differ from torch's by one step. Where 2^a
+// would pass 2^64 (x below about -7.7) it returns x * 0 (-0, or NaN for
+// -inf), as torch's saturated tanh does.
 constexpr double kLog2e = 1.4426950408889634;
 constexpr float kGeluC0 = (float)(-2.0 * 0.7978845608028654 * kLog2e);
 constexpr float kGeluC1 = (float)(-2.0 * 0.7978845608028654 * 0.044715 * kLog2e);
-template <bool GELU>
+template <int GELU>
 OGA_DEVICE float pre(float x) {
-  if (!GELU) return x;
+  if (GELU == kGeluNone) return x;
+  if (GELU == kGeluExact) {
+    const float x3 = (x * x) * x;
+    const float inner = kGeluBeta * fmaf(kGeluKappa, x3, x);
+    return rbf((0.5f * x) * (1.0f + tanhf(inner)));
+  }
   const float a = x * fmaf(kGeluC1, x * x, kGeluC0);
   const bool big = a > 64.0f;
   const float d = 1.0f + __builtin_amdgcn_exp2f(big ? 64.0f : a);
@@ -37,7 +54,7 @@ OGA_DEVICE float pre(float x) {
   return rbf(x * (big ? 0.0f : rc));
 }
 
-template <bool GELU>
+template <int GELU>
 __global__ __launch_bounds__(256) void k_fp8_quant(const uint16_t* x, const float* scale, int zero_dim, uint8_t* q,
                                                    int64_t n) {
   const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 16;
@@ -73,22 +90,40 @@ __global__ __launch_bounds__(256) void k_fp8_quant(const uint16_t* x, const floa
 }
 
 // ------------------------------------------------------------ per head
+// The amax of |x| is taken on bit patterns: with the sign bit cleared, a
+// bf16 (or float32) pattern orders as its magnitude, and every NaN pattern
+// lies above infinity, so the maximum is NaN when any element is NaN, as
+// torch's amax gives. Two bf16 magnitudes are kept per dword and combined
+// with one packed 16-bit max.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+OGA_DEVICE u16x2 abs_bits2(uint32_t w) { return __builtin_bit_cast(u16x2, w & 0x7FFF7FFFu); }
+OGA_DEVICE uint32_t umax_dpp(uint32_t v, int ctrl) {
+  uint32_t o;
+  switch (ctrl) {
+    case 0: o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true); break;   // lane ^ 1
+    case 1: o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, true); break;   // lane ^ 2
+    case 2: o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, true); break;  // half-row mirror
+    default: o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, true); break; // row mirror
+  }
+  return max(v, o);
+}
+
 // Pass 1: partial amax over a block of tokens, for every head. Block
 // (b, chunk) covers tokens [chunk*TPB, chunk*TPB + TPB); each wave walks
 // TPB/4 token rows; lane l of vector step j sees head (j*512 + 8l) / D.
-// partial[b, h, chunk] = max |x| over the block (a head's partials are
-// contiguous for the reduction in pass 2).
+// partial[b, h, chunk] = max |x| over the block as a float32 bit pattern
+// (a head's partials are contiguous for the reduction in pass 2).
 template <int CH, int D, int TPB>
 __global__ __launch_bounds__(256) void k_head_amax(const uint16_t* x, float* partial, int64_t tokens, int nchunk) {
   constexpr int H = CH * 512 / D;
   constexpr int LPH = D / 8;  // lanes per head inside one vector step
-  __shared__ float red[4][H];
+  __shared__ uint32_t red[4][H];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t b = blockIdx.y;
   const int chunk = blockIdx.x;
-  float m[CH];
+  u16x2 m[CH];
 #pragma unroll
-  for (int j = 0; j < CH; ++j) m[j] = 0.0f;
+  for (int j = 0; j < CH; ++j) m[j] = u16x2{0, 0};
   // The wave's TPB/4 token rows (CH 16-byte loads each) are all in flight
   // together before the maxima are taken.
   const int64_t t0 = (int64_t)chunk * TPB;
@@ -108,33 +143,34 @@ __global__ __launch_bounds__(256) void k_head_amax(const uint16_t* x, float* par
     if (t0 + w + 4 * u < tokens) {
 #pragma unroll
       for (int j = 0; j < CH; ++j) {
-        float f[8];
-        unpack8(xv[u][j], f);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) m[j] = fmaxf(m[j], fabsf(f[i]));
+        const uint4 v = xv[u][j];
+        m[j] = __builtin_elementwise_max(m[j], abs_bits2(v.x));
+        m[j] = __builtin_elementwise_max(m[j], abs_bits2(v.y));
+        m[j] = __builtin_elementwise_max(m[j], abs_bits2(v.z));
+        m[j] = __builtin_elementwise_max(m[j], abs_bits2(v.w));
       }
     }
   }
   // Reduce over the lanes of one head: 16 lanes (D=128) or 8 lanes (D=64).
 #pragma unroll
   for (int j = 0; j < CH; ++j) {
-    float v = m[j];
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true)));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true)));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true)));
-    if (LPH == 16) v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true)));
+    uint32_t v = max((uint32_t)m[j].x, (uint32_t)m[j].y) << 16;  // float32 pattern of the bf16 magnitude
+    v = umax_dpp(v, 0);
+    v = umax_dpp(v, 1);
+    v = umax_dpp(v, 2);
+    if (LPH == 16) v = umax_dpp(v, 3);
     if (lane % LPH == 0) red[w][(j * 512 + lane * 8) / D] = v;
   }
   __syncthreads();
   for (int h = threadIdx.x; h < H; h += 256) {
-    const float v = fmaxf(fmaxf(red[0][h], red[1][h]), fmaxf(red[2][h], red[3][h]));
-    partial[(b * H + h) * nchunk + chunk] = v;
+    const uint32_t v = max(max(red[0][h], red[1][h]), max(red[2][h], red[3][h]));
+    partial[(b * H + h) * nchunk + chunk] = __uint_as_float(v);
   }
 }
 
 // Pass 2: quantize. Workgroup (token chunk, h, b) first reduces the amax
-// partials of head (b, h) to scale = max(amax, 1e-12) / 448 (IEEE division;
-// workgroup 0 of the head stores it), then quantizes its chunk of tokens:
+// partials of head (b, h) to scale = max(amax, 1e-12) * float32(1/448)
+// (workgroup 0 of the head stores it), then quantizes its chunk of tokens:
 // q = e4m3(clamp(x / scale, +-448)). D/8 lanes cover one token's head slice
 // (16 bytes each), so every load is a whole 2*D-byte slice and every store
 // a whole D-byte slice.
@@ -144,19 +180,25 @@ __global__ __launch_bounds__(256) void k_head_scale_quant(const uint16_t* x, con
                                                           uint8_t* q, int64_t tokens, int heads, int nchunk) {
   constexpr int LPT = D / 8;      // lanes per token slice
   constexpr int TPP = 256 / LPT;  // token slices per pass
-  __shared__ float red[4];
+  __shared__ uint32_t red[4];
   const int h = blockIdx.y;
   const int64_t b = blockIdx.z;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  float m = 0.0f;
-  for (int c = threadIdx.x; c < nchunk; c += 256) m = fmaxf(m, partial[(b * heads + h) * nchunk + c]);
-  m = row16_max(m);
-  m = fmaxf(m, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(m), 0x401F)));
-  m = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0)),
-            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32)));
+  // Partials are magnitudes as float32 bit patterns: their integer maximum
+  // is the amax, NaN if any element of the head was NaN.
+  uint32_t m = 0;
+  for (int c = threadIdx.x; c < nchunk; c += 256) m = max(m, __float_as_uint(partial[(b * heads + h) * nchunk + c]));
+  m = umax_dpp(umax_dpp(umax_dpp(umax_dpp(m, 0), 1), 2), 3);
+  m = max(m, (uint32_t)__builtin_amdgcn_ds_swizzle((int)m, 0x401F));
+  m = max((uint32_t)__builtin_amdgcn_readlane((int)m, 0), (uint32_t)__builtin_amdgcn_readlane((int)m, 32));
   if (lane == 0) red[w] = m;
   __syncthreads();
-  const float s = fmaxf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), 1e-12f) / 448.0f;
+  // torch: clamp_min(amax, 1e-12) / 448, with a NaN amax kept (clamp
+  // propagates NaN) so the whole head quantizes to NaN codes. torch's GPU
+  // division of a tensor by a Python scalar multiplies by the float32
+  // reciprocal of the scalar, so that is what this computes.
+  const float amax = __uint_as_float(max(max(red[0], red[1]), max(red[2], red[3])));
+  const float s = (amax != amax ? amax : fmaxf(amax, 1e-12f)) * (1.0f / 448.0f);
   if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[b * heads + h] = s;
 
   // x / s as the compiler's IEEE float32 division computes it (v_div_scale,
@@ -223,21 +265,36 @@ extern "C" int oga_fp8_quantize_e4m3(const void* x, const float* scale, int scal
   if (n == 0) return OGA_OK;
   if (!aligned(x, 16) || !aligned(q, 16)) return fail("x/q must be 16-byte aligned");
   const int64_t threads = (n + 15) / 16;
-  hipLaunchKernelGGL(k_fp8_quant<false>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL(k_fp8_quant<kGeluNone>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t*)x, scale, scale_is_0dim ? 1 : 0, (uint8_t*)q, n);
   return launch_status();
 }
 
-extern "C" int oga_gelu_tanh_fp8_quantize_e4m3(const void* x, const float* scale, int scale_is_0dim, void* q,
-                                               int64_t n, void* stream) {
+static int gelu_quant(const void* x, const float* scale, int scale_is_0dim, void* q, int64_t n, bool fast,
+                      hipStream_t st) {
   if (!x || !scale || !q) return fail("null pointer");
   if (n < 0) return fail("bad size");
   if (n == 0) return OGA_OK;
   if (!aligned(x, 16) || !aligned(q, 16)) return fail("x/q must be 16-byte aligned");
   const int64_t threads = (n + 15) / 16;
-  hipLaunchKernelGGL(k_fp8_quant<true>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
-                     (const uint16_t*)x, scale, scale_is_0dim ? 1 : 0, (uint8_t*)q, n);
+  const dim3 grid((unsigned)((threads + 255) / 256));
+  if (fast)
+    hipLaunchKernelGGL(k_fp8_quant<kGeluFast>, grid, dim3(256), 0, st, (const uint16_t*)x, scale,
+                       scale_is_0dim ? 1 : 0, (uint8_t*)q, n);
+  else
+    hipLaunchKernelGGL(k_fp8_quant<kGeluExact>, grid, dim3(256), 0, st, (const uint16_t*)x, scale,
+                       scale_is_0dim ? 1 : 0, (uint8_t*)q, n);
   return launch_status();
+}
+
+extern "C" int oga_gelu_tanh_fp8_quantize_e4m3(const void* x, const float* scale, int scale_is_0dim, void* q,
+                                               int64_t n, void* stream) {
+  return gelu_quant(x, scale, scale_is_0dim, q, n, false, (hipStream_t)stream);
+}
+
+extern "C" int oga_gelu_tanh_fp8_quantize_e4m3_fast(const void* x, const float* scale, int scale_is_0dim, void* q,
+                                                    int64_t n, void* stream) {
+  return gelu_quant(x, scale, scale_is_0dim, q, n, true, (hipStream_t)stream);
 }
 
 extern "C" int64_t oga_fp8_per_head_workspace_bytes(int64_t batch, int64_t tokens, int64_t heads, int64_t head_dim) {

@@ -663,6 +663,23 @@ extern "C" int oga_residual_gate_bf16(const void* x, const void* y, const void* 
   return run_row<OP_RESID>(a, batch, (hipStream_t)stream);
 }
 
+extern "C" int64_t oga_rows_per_wave(int kind, int64_t batch, int64_t tokens, int64_t cols) {
+  if (batch < 1 || tokens < 1 || (cols != 2048 && cols != 4096)) return 0;
+  if (kind == OGA_ROWS_ADAZERO) {
+    dim3 grid;
+    int rpw = 0;
+    adazero_grid(batch, tokens, grid, rpw);
+    return rpw;
+  }
+  if (kind == OGA_ROWS_ELEMENTWISE) {
+    dim3 grid;
+    int64_t rpg = 0;
+    elem_grid(batch, tokens, cols == 4096 ? 8 : 4, grid, rpg);
+    return rpg;
+  }
+  return 0;
+}
+
 extern "C" int oga_bias_add_bf16(const void* x, const void* bias, int bias_dtype, void* out, int64_t rows,
                                  int64_t cols, void* stream) {
   if (!x || !bias || !out) return fail("null pointer");

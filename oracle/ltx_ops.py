@@ -168,27 +168,53 @@ def fp8_quantize_e4m3(x: T, input_scale: float, scale_is_0dim: bool, device: str
 
 
 def gelu_tanh(x: T) -> T:
-    """torch.nn.functional.gelu(x, approximate='tanh') for bf16 x: computed in
-    float32 as 0.5*x*(1+tanh(sqrt(2/pi)*(x+0.044715*x^3))), rounded once.
-    (float64 tanh here; parity unpinned at the last float32 bit.)"""
-    v = x.v.astype(np.float64)
-    g = 0.5 * v * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (v + 0.044715 * v * v * v)))
+    """torch.nn.functional.gelu(x, approximate='tanh') for bf16 x, step by step
+    as torch's GPU kernel evaluates it in float32 (the reference's torch path
+    :165-169 on the GPU):
+
+        x3 = (x * x) * x;  inner = beta * fma(kappa, x3, x);
+        g = (0.5 * x) * (1 + tanh(inner)), rounded once to bf16,
+
+    beta = float32(sqrt(2) * 2/sqrt(pi) * 0.5), kappa = float32(0.044715).
+    The fused multiply-add is evaluated in extended precision (the product
+    kappa * x3 is exact there) and rounded once to float32; tanh is the
+    float64 tanh rounded to float32. Pinned exhaustively (all 65536 bf16
+    inputs) against torch's gelu on the GPU by a GPU test."""
+    v = x.v.astype(np.float32)
+    beta = np.float32(np.sqrt(2.0) * (2.0 / np.sqrt(np.pi)) * 0.5)
+    kappa = np.float32(0.044715)
+    with np.errstate(over="ignore", invalid="ignore"):
+        x3 = (v * v) * v
+        ld = np.longdouble
+        inner = beta * (ld(kappa) * ld(x3) + ld(v)).astype(np.float32)
+        t = np.tanh(inner.astype(np.float64)).astype(np.float32)
+        g = (np.float32(0.5) * v) * (np.float32(1.0) + t)
     g = g.astype(np.float32)
     return T(bf16_round(g) if x.dt == "bf16" else g, x.dt)
 
 
-def fp8_per_head_quantize(x: np.ndarray):
+def fp8_per_head_quantize(x: np.ndarray, device: str = "cuda"):
     """`_torch_fp8_quantize_e4m3_per_head_4d` (:976-980) for x [B, N, H, D].
 
-    scale[b, h] = max(amax_{N,D} |x|, 1e-12) / 448 (float32 division);
-    q = e4m3(clamp(x / scale, -448, 448)) with a float32 division.
+    amax = max_{N,D} |x| (NaN if any element of the head is NaN, as torch's
+    amax gives); scale[b, h] = clamp_min(amax, 1e-12) / 448; q =
+    e4m3(clamp(x / scale, -448, 448)) with an IEEE float32 division.
+    `/ 448` divides a tensor by a Python scalar: on the GPU torch evaluates
+    that as a multiplication by the float32 reciprocal (`device="cuda"`,
+    the production device), on the CPU as a division (`device="cpu"`); the
+    two differ in the last bit of some scales.
     Returns (codes uint8 [B,N,H,D], scale float32 [B,H]).
     """
     xv = f32(x)
     amax = np.abs(xv).max(axis=(1, 3)).astype(np.float32)
-    scale = np.maximum(amax, np.float32(1e-12)) / np.float32(E4M3_MAX)
-    q = xv / scale[:, None, :, None]
-    q = np.minimum(np.maximum(q, np.float32(-E4M3_MAX)), np.float32(E4M3_MAX))
+    clamped = np.maximum(amax, np.float32(1e-12))
+    if device == "cuda":
+        scale = clamped * (np.float32(1.0) / np.float32(E4M3_MAX))
+    else:
+        scale = clamped / np.float32(E4M3_MAX)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        q = xv / scale[:, None, :, None]
+        q = np.minimum(np.maximum(q, np.float32(-E4M3_MAX)), np.float32(E4M3_MAX))
     return e4m3_encode(q), scale.astype(np.float32)
 
 

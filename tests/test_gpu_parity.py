@@ -280,20 +280,55 @@ def test_fp8_quantize_ragged_sizes(n):
     assert np.array_equal(q.view(torch.uint8).cpu().numpy(), ref)
 
 
-def test_gelu_tanh_fp8_quantize():
+ALL_BF16 = bf16_from_bits(np.arange(1 << 16, dtype=np.uint16))
+
+
+@pytest.mark.parametrize("zero_dim", [True, False])
+def test_gelu_tanh_fp8_quantize_exhaustive_vs_torch(zero_dim):
+    """Every bf16 input (65536 patterns, so the whole domain) at several
+    scales: the HIP codes equal torch evaluating the reference's torch path
+    (:165-169) on the GPU, bit for bit."""
     from opengenie_amd.ltx_ops import fused_gelu_tanh_fp8_quantize_e4m3
 
-    x = randn((64, 4096), 31, std=2.0)
-    s = torch.tensor(0.02)
-    q = fused_gelu_tanh_fp8_quantize_e4m3(g(x), g(s))
-    _ran("fused_gelu_tanh_fp8_quantize_e4m3")
-    torch.cuda.synchronize()
-    ref = O.fp8_quantize_e4m3(O.gelu_tanh(to_T(x)), 0.02, True, device="cuda")
-    got = q.view(torch.uint8).cpu().numpy()
-    # tanh's last float32 bit is library-specific: rare one-step bf16 GELU
-    # differences may move a code by one step.
-    assert (got != ref).mean() < 1e-3
-    d = np.abs(e4m3_decode(got).astype(np.float64) - e4m3_decode(ref))
+    xt = g(torch.from_numpy(ALL_BF16.copy()).to(torch.bfloat16))
+    for scale in (0.02, 0.37, 3.3e-3, 1.0, 0.11160714):
+        s = torch.tensor(scale, dtype=torch.float32)
+        if not zero_dim:
+            s = s.reshape(1)
+        q = fused_gelu_tanh_fp8_quantize_e4m3(xt, g(s))
+        _ran("fused_gelu_tanh_fp8_quantize_e4m3")
+        ref = tr.gelu_tanh_fp8_quantize_e4m3(xt, g(s)).view(torch.uint8).cpu().numpy()
+        got = q.view(torch.uint8).cpu().numpy()
+        assert np.array_equal(nan_canon(got), nan_canon(ref)), (scale, int((got != ref).sum()))
+
+
+def test_gelu_tanh_oracle_matches_torch_on_gpu():
+    """Pins the oracle's GELU on its whole bf16 domain against torch's GPU
+    gelu(approximate='tanh'), and the oracle's GELU quantizer codes against
+    the HIP kernel's."""
+    from opengenie_amd.ltx_ops import fused_gelu_tanh_fp8_quantize_e4m3
+
+    xt = torch.from_numpy(ALL_BF16.copy()).to(torch.bfloat16)
+    ref = torch.nn.functional.gelu(g(xt), approximate="tanh").float().cpu().numpy()
+    ours = O.gelu_tanh(T(ALL_BF16, "bf16")).v
+    assert_same_bits(ours, ref, "oracle gelu vs torch gpu")
+    q = fused_gelu_tanh_fp8_quantize_e4m3(g(xt), g(torch.tensor(0.02)))
+    with np.errstate(over="ignore", invalid="ignore"):
+        oq = O.fp8_quantize_e4m3(O.gelu_tanh(T(ALL_BF16, "bf16")), 0.02, True, device="cuda")
+    assert np.array_equal(nan_canon(q.view(torch.uint8).cpu().numpy()), nan_canon(oq))
+
+
+def test_gelu_tanh_fp8_quantize_fast_form_is_bounded():
+    """The opt-in inexact form (exact=False): codes within one e4m3 step of
+    torch's on the FFN activations' range, on few elements."""
+    from opengenie_amd.ltx_ops import fused_gelu_tanh_fp8_quantize_e4m3
+
+    x = g(randn((64, 4096), 31, std=2.0))
+    s = g(torch.tensor(0.02))
+    fast = fused_gelu_tanh_fp8_quantize_e4m3(x, s, exact=False).view(torch.uint8).cpu().numpy()
+    ref = tr.gelu_tanh_fp8_quantize_e4m3(x, s).view(torch.uint8).cpu().numpy()
+    assert (fast != ref).mean() < 1e-3
+    d = np.abs(e4m3_decode(fast).astype(np.float64) - e4m3_decode(ref))
     assert np.nanmax(d / np.maximum(np.abs(e4m3_decode(ref)), 2 ** -9)) <= 0.126
 
 
@@ -355,14 +390,23 @@ def test_fp8_per_head_special_values():
     h2[3::5] *= 1e-4
     x[0, :, 2, :] = h2.reshape(512, 128)
     x[0, :, 3, :] = rng.standard_normal((512, 128)).astype(np.float32) * 1e-30
+    # NaN: torch's amax propagates it, so the head's scale and codes are NaN
+    x[0, 200, 4, 17] = np.nan
+    x[0, 3, 5, 0] = np.nan
+    x[0, 4, 5, 1] = np.inf
     xt = torch.from_numpy(x).to(torch.bfloat16)
     q, s = fused_fp8_quantize_e4m3_per_head_4d(g(xt))
     _ran("fused_fp8_quantize_e4m3_per_head_4d")
     torch.cuda.synchronize()
     qr, sr = O.fp8_per_head_quantize(np32(xt))
+    assert np.isnan(sr[0, 4]) and np.isnan(sr[0, 5]) and np.isfinite(sr[0, 6])
     assert_same_bits(s.cpu().numpy(), sr, "per-head scale")
     got = q.view(torch.uint8).cpu().numpy()
     assert np.array_equal(nan_canon(got), nan_canon(qr))
+    # and torch evaluating the reference expression (:976-980) on the GPU
+    tq, ts = tr.fp8_per_head(g(xt))
+    assert_same_bits(s.cpu().numpy(), ts.cpu().numpy(), "per-head scale vs torch")
+    assert np.array_equal(nan_canon(got), nan_canon(tq.view(torch.uint8).cpu().numpy()))
 
 
 # ------------------------------------------------------------ Q/K preattention
@@ -498,6 +542,81 @@ def test_fp8_linear_split_k_through_c_abi(m, n, k):
         outs.append(got)
     # the two schedules differ only in the order of the float32 sums
     assert (bf16_ulp_distance(outs[0], outs[1]) > 1).mean() < 1e-3
+
+
+def _bias_epilogue_ref(out_nobias: np.ndarray, bias: torch.Tensor) -> np.ndarray:
+    """R(out + R(bias)): the second rounding of the FP8 linear (:1705-1709)."""
+    return bf16_round(out_nobias + bf16_round(np32(bias))[None, :])
+
+
+@pytest.mark.parametrize("m,n,k,bias_dtype,use_ws", [
+    (4352, 4096, 4096, torch.bfloat16, False),  # persistent whole-tile schedule
+    (4352, 4096, 4096, torch.bfloat16, True),   # + split-K last round (16 tiles x 16 K-chunks)
+    (2304, 16384, 512, torch.bfloat16, True),
+    (300, 520, 384, torch.float32, False),      # one-workgroup-per-tile kernel (N not a multiple of 128)
+    (300, 520, 384, torch.bfloat16, False),
+])
+def test_fp8_linear_bias_epilogue_is_exact(m, n, k, bias_dtype, use_ws):
+    """The bias epilogue pinned independently of the float32 accumulation
+    order: the same GEMM with and without the bias gives, on every element,
+    out_bias == R(out_nobias + R(bias)) bit for bit."""
+    from opengenie_amd import _lib
+
+    lib = _lib.load()
+    x = randn((m, k), 180 + m, std=1.0)
+    sa = (x.float().abs().amax() / 448.0).reshape(())
+    a = torch.clamp(x.float() / sa, -448, 448).to(torch.float8_e4m3fn)
+    w, sb = _fp8_weights(n, k, 181 + n)
+    bias = randn((n,), 182, dtype=bias_dtype, std=0.01)
+    ga, gw, gsa, gsb, gb = g(a), g(w), g(sa).float(), g(sb).float(), g(bias)
+    ws_bytes = int(lib.oga_fp8_linear_workspace_bytes(m, n, k)) if use_ws else 0
+    if use_ws:
+        assert ws_bytes > 0
+    ws = torch.empty((max(ws_bytes, 4) // 4,), device="cuda", dtype=torch.float32)
+    stream = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for bp in (None, gb):
+        out = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
+        _lib.call("oga_fp8_linear_ws", ga.data_ptr(), k, gw.data_ptr(), k, gsa.data_ptr(), gsb.data_ptr(),
+                  bp.data_ptr() if bp is not None else None, _lib.DT_BF16 if bias_dtype == torch.bfloat16 else
+                  _lib.DT_F32, out.data_ptr(), n, m, n, k, ws.data_ptr() if use_ws else None, ws_bytes, stream)
+        outs.append(out_np(out))
+    assert_same_bits(outs[1], _bias_epilogue_ref(outs[0], bias), "bias epilogue")
+
+
+def test_fp8_grouped_linear_bias_epilogue_is_exact():
+    """The grouped kernel's per-linear bias: with and without the biases,
+    out_bias == R(out_nobias + R(bias_i)) for every linear and element."""
+    import ctypes
+
+    from opengenie_amd import _lib
+
+    lib = _lib.load()
+    m, n, k, groups = 1536, 4096, 4096, 3
+    x = randn((m, k), 190, std=1.0)
+    sa = (x.float().abs().amax() / 448.0).reshape(())
+    a = g(torch.clamp(x.float() / sa, -448, 448).to(torch.float8_e4m3fn))
+    gsa = g(sa).float()
+    ws_ = [_fp8_weights(n, k, 191 + i) for i in range(groups)]
+    w = [g(t[0]) for t in ws_]
+    sb = [g(t[1]).float() for t in ws_]
+    biases = [g(randn((n,), 195 + i, std=0.01)) for i in range(groups)]
+    ws_bytes = int(lib.oga_fp8_linear_workspace_bytes(m, n * groups, k))
+    ws = torch.empty((max(ws_bytes, 4) // 4,), device="cuda", dtype=torch.float32)
+    arr = ctypes.c_void_p * groups
+    res = []
+    for with_bias in (False, True):
+        outs = [torch.empty((m, n), device="cuda", dtype=torch.bfloat16) for _ in range(groups)]
+        w_p = arr(*[t.data_ptr() for t in w])
+        s_p = arr(*[t.data_ptr() for t in sb])
+        b_p = arr(*[(t.data_ptr() if with_bias else None) for t in biases])
+        o_p = arr(*[o.data_ptr() for o in outs])
+        _lib.call("oga_fp8_linear_grouped_ws", a.data_ptr(), k, ctypes.addressof(w_p), k, gsa.data_ptr(),
+                  ctypes.addressof(s_p), ctypes.addressof(b_p), _lib.DT_BF16, ctypes.addressof(o_p), n, m, n, groups,
+                  k, ws.data_ptr() if ws_bytes else None, ws_bytes, torch.cuda.current_stream().cuda_stream)
+        res.append([out_np(o) for o in outs])
+    for i in range(groups):
+        assert_same_bits(res[1][i], _bias_epilogue_ref(res[0][i], biases[i]), f"grouped bias epilogue {i}")
 
 
 class _FP8Lin(torch.nn.Module):
