@@ -231,7 +231,10 @@ __global__ __launch_bounds__(256) void k_elem(RowArgs a, int64_t rows_per_group)
   }
 }
 
-// ------------------------------------------------------------ AdaZero
+// ------------------------------------------------------- AdaZero (gather)
+// The form of AdaZero for operands that cannot be read 16 bytes at a time
+// (a column stride other than 1, or misaligned rows); see k_adazero_rows
+// for the vectorised form.
 // y = R(R?(R(x * inv_rms) * R?(1 + scale)) + shift). A workgroup of CH waves
 // streams a run of consecutive token rows; wave w owns columns w*512 + 8l ..
 // +7 of every row. Each wave keeps the loads of the next kAdaAhead rows in
@@ -249,7 +252,7 @@ __global__ __launch_bounds__(256) void k_elem(RowArgs a, int64_t rows_per_group)
 constexpr int kAdaAhead = OGA_ADA_AHEAD;
 static_assert(kAdaAhead >= 1 && kAdaAhead <= 4, "prefetch depth");
 template <int CH, bool UNIFORM, int D0, int D1, bool VEC>
-__global__ __launch_bounds__(512) void k_adazero(RowArgs a, int rows_per_wg) {
+__global__ __launch_bounds__(512) void k_adazero_gather(RowArgs a, int rows_per_wg) {
   constexpr int C = CH * 512;
   constexpr bool B1 = D1 == OGA_DT_BF16;
   constexpr bool B0 = D0 == OGA_DT_BF16;
@@ -372,6 +375,220 @@ __global__ __launch_bounds__(512) void k_adazero(RowArgs a, int rows_per_wg) {
     if constexpr (kAdaAhead > 2) step(base, IC<2>{});
     if constexpr (kAdaAhead > 3) step(base, IC<3>{});
   }
+}
+
+// ------------------------------------------------ AdaZero, wave per row
+// y = R(R?(R(x * inv_rms) * R?(1 + scale)) + shift) with one wave per token
+// row: lane l holds columns j*512 + 8l .. +7 of every 512-column chunk j, so
+// a row's sum of squares is a wave reduction (DPP, no LDS, no barrier) and a
+// row is written as soon as its own loads have landed. The kAdaWaves waves
+// of a workgroup first fill LDS with the per-column constants in float32:
+// with one timestep row shared by all tokens, the finished Ada values (shift
+// and R?(1 + scale)); otherwise the table parts R?(table[i]), to which each
+// row adds its own timestep values. The constant loads go out before the row
+// loads (loads complete in order, so the fill never waits for a row) and one
+// barrier publishes the constants. A wave then streams rows t = v, v + V,
+// ... of its batch (V waves per batch), with the next row's loads in flight
+// while it finishes the current one when the timestep row is shared. Two
+// values are rounded per v_cvt_pk_bf16_f32.
+#ifndef OGA_ADA_WAVES
+#define OGA_ADA_WAVES 12
+#endif
+constexpr int kAdaWaves = OGA_ADA_WAVES;
+#ifndef OGA_ADA_SCHED_GROUP
+#define OGA_ADA_SCHED_GROUP 2
+#endif
+constexpr int kAdaSchedGroup = OGA_ADA_SCHED_GROUP;
+enum { TAB_NONE = 0, TAB_BF16 = 1, TAB_F32 = 2 };
+
+template <int CH, bool UNIFORM, int D0, int D1, int TAB>
+__global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int64_t waves_per_batch) {
+  constexpr int C = CH * 512;
+  constexpr int G = C / 8;  // groups of 8 columns
+  constexpr int NT = 64 * kAdaWaves;
+  constexpr int GPT = (G + NT - 1) / NT;
+  constexpr bool B0 = D0 == OGA_DT_BF16;
+  constexpr bool B1 = D1 == OGA_DT_BF16;
+  constexpr bool HT = TAB != TAB_NONE;
+  constexpr int TD = TAB == TAB_F32 ? OGA_DT_F32 : OGA_DT_BF16;
+  __shared__ float4 cst[2][2 * G];  // [shift | scale part][column / 4]
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int tid = threadIdx.x;
+  const int64_t b = blockIdx.y;
+  const int64_t V = waves_per_batch;
+  const int64_t v = (int64_t)blockIdx.x * kAdaWaves + w;
+  // A wave past the batch's V waves takes no rows but joins the fill.
+  const int64_t t_first = v < V ? v : a.tokens;
+
+  // Constant loads: table rows and, when shared, the timestep row.
+  Raw8<TD> tr0[GPT], tr1[GPT];
+  Raw8<D0> u0[GPT];
+  Raw8<D1> u1[GPT];
+#pragma unroll
+  for (int q = 0; q < GPT; ++q) {
+    const int gi = tid + q * NT;
+    if (gi < G) {
+      if constexpr (HT) {
+        tr0[q] = raw8_load<TD>(a.s0.tab, a.s0.tab_off + gi * 8);
+        tr1[q] = raw8_load<TD>(a.s1.tab, a.s1.tab_off + gi * 8);
+      }
+      if constexpr (UNIFORM) {
+        u0[q] = raw8_load<D0>(a.s0.ts, a.s0.ts_off + b * a.s0.ts_sb + gi * 8);
+        u1[q] = raw8_load<D1>(a.s1.ts, a.s1.ts_off + b * a.s1.ts_sb + gi * 8);
+      }
+    }
+  }
+  // The first row's loads.
+  const uint16_t* const xb = a.x + b * a.tokens * C + lane * 8;
+  uint16_t* const yb = a.out + b * a.tokens * C + lane * 8;
+  uint4 xv[CH];
+  if (t_first < a.tokens) {
+#pragma unroll
+    for (int j = 0; j < CH; ++j) xv[j] = *(const uint4*)(xb + t_first * C + j * 512);
+  }
+  // Constants to LDS.
+#pragma unroll
+  for (int q = 0; q < GPT; ++q) {
+    const int gi = tid + q * NT;
+    if (gi < G) {
+      float c0[8], c1[8];
+      if constexpr (HT) {
+        raw8_get<TD>(tr0[q], c0);
+        raw8_get<TD>(tr1[q], c1);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {  // table.to(ts dtype)
+          if (TAB == TAB_F32 && B0) c0[i] = rbf(c0[i]);
+          if (TAB == TAB_F32 && B1) c1[i] = rbf(c1[i]);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) c0[i] = c1[i] = 0.0f;
+      }
+      if constexpr (UNIFORM) {
+        float s[8];
+        raw8_get<D0>(u0[q], s);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float sum = HT ? c0[i] + s[i] : s[i];
+          c0[i] = (HT && B0) ? rbf(sum) : sum;
+        }
+        raw8_get<D1>(u1[q], s);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float sum = HT ? c1[i] + s[i] : s[i];
+          if (HT && B1) sum = rbf(sum);
+          const float f = 1.0f + sum;
+          c1[i] = B1 ? rbf(f) : f;
+        }
+      }
+      cst[0][2 * gi] = make_float4(c0[0], c0[1], c0[2], c0[3]);
+      cst[0][2 * gi + 1] = make_float4(c0[4], c0[5], c0[6], c0[7]);
+      cst[1][2 * gi] = make_float4(c1[0], c1[1], c1[2], c1[3]);
+      cst[1][2 * gi + 1] = make_float4(c1[4], c1[5], c1[6], c1[7]);
+    }
+  }
+  // LDS writes done, then the barrier; no vmcnt drain (the row loads stay
+  // in flight across it).
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  const int64_t ts0 = a.s0.ts_off + b * a.s0.ts_sb + lane * 8;
+  const int64_t ts1 = a.s1.ts_off + b * a.s1.ts_sb + lane * 8;
+  // Per-token timesteps in bf16 are loaded for the whole row up front; in
+  // float32 (twice the registers) chunk by chunk.
+  constexpr bool kTsRow = !UNIFORM && B0 && B1;
+  for (int64_t t = t_first; t < a.tokens; t += V) {
+    if (t != t_first && !UNIFORM) {
+#pragma unroll
+      for (int j = 0; j < CH; ++j) xv[j] = *(const uint4*)(xb + t * C + j * 512);
+    }
+    Raw8<D0> p0[kTsRow ? CH : 1];
+    Raw8<D1> p1[kTsRow ? CH : 1];
+    if constexpr (kTsRow) {
+#pragma unroll
+      for (int j = 0; j < CH; ++j) {
+        p0[j] = raw8_load<D0>(a.s0.ts, ts0 + t * a.s0.ts_st + j * 512);
+        p1[j] = raw8_load<D1>(a.s1.ts, ts1 + t * a.s1.ts_st + j * 512);
+      }
+    }
+    float f[CH][8];
+    double ss[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      unpack8(xv[j], f[j]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss[i & 3] = fma((double)f[j][i], (double)f[j][i], ss[i & 3]);
+    }
+    if constexpr (UNIFORM) {  // the next row's loads, into the buffer just unpacked
+      const int64_t tn = t + V;
+      if (tn < a.tokens) {
+#pragma unroll
+        for (int j = 0; j < CH; ++j) xv[j] = *(const uint4*)(xb + tn * C + j * 512);
+      }
+    }
+    const double tot = wave_sum_d((ss[0] + ss[1]) + (ss[2] + ss[3]));
+    const float inv = 1.0f / sqrtf((float)(tot / (double)C) + a.eps);
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      // Groups of kAdaSchedGroup chunks: keeps the constants' LDS reads (and
+      // float32 timestep loads) from being hoisted for all chunks at once.
+      if (kAdaSchedGroup > 0 && j % kAdaSchedGroup == 0) __builtin_amdgcn_sched_barrier(0);
+      const int gi = j * 64 + lane;
+      const float4 a0 = cst[0][2 * gi], a1 = cst[0][2 * gi + 1];
+      const float4 m0 = cst[1][2 * gi], m1 = cst[1][2 * gi + 1];
+      float v0[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      float v1[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+      if constexpr (!UNIFORM) {
+        float s0v[8], s1v[8];
+        if constexpr (kTsRow) {
+          raw8_get<D0>(p0[j], s0v);
+          raw8_get<D1>(p1[j], s1v);
+        } else {
+          raw8_get<D0>(raw8_load<D0>(a.s0.ts, ts0 + t * a.s0.ts_st + j * 512), s0v);
+          raw8_get<D1>(raw8_load<D1>(a.s1.ts, ts1 + t * a.s1.ts_st + j * 512), s1v);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float sum = HT ? v0[i] + s0v[i] : s0v[i];
+          v0[i] = (HT && B0) ? rbf(sum) : sum;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float sum = HT ? v1[i] + s1v[i] : s1v[i];
+          if (HT && B1) sum = rbf(sum);
+          const float fv = 1.0f + sum;
+          v1[i] = B1 ? rbf(fv) : fv;
+        }
+      }
+      uint32_t ow[4];
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) {
+        const uint32_t n = pack_bf16(f[j][i] * inv, f[j][i + 1] * inv);
+        float pa = bf16_lo(n) * v1[i], pb = bf16_hi(n) * v1[i + 1];
+        if constexpr (B1) {
+          const uint32_t p = pack_bf16(pa, pb);
+          pa = bf16_lo(p);
+          pb = bf16_hi(p);
+        }
+        ow[i / 2] = pack_bf16(pa + v0[i], pb + v0[i + 1]);
+      }
+      st_nt16(yb + t * C + j * 512, make_uint4(ow[0], ow[1], ow[2], ow[3]));
+    }
+  }
+}
+
+// Grid of k_adazero_rows: one workgroup of kAdaWaves waves per CU at most;
+// rows = ceil(batch*tokens / (CUs * kAdaWaves)) rows per wave, and V =
+// ceil(tokens / rows) waves per batch, so every wave gets rows or rows - 1.
+static void adazero_rows_grid(int64_t batch, int64_t tokens, dim3& grid, int64_t& waves_per_batch,
+                              int64_t& rows_per_wave) {
+  const int64_t slots = (int64_t)cu_count() * kAdaWaves;
+  int64_t rows = (batch * tokens + slots - 1) / slots;
+  if (rows < 1) rows = 1;
+  const int64_t v = (tokens + rows - 1) / rows;
+  rows_per_wave = (tokens + v - 1) / v;
+  waves_per_batch = v;
+  grid = dim3((unsigned)((v + kAdaWaves - 1) / kAdaWaves), (unsigned)batch);
 }
 
 // Grid of k_adazero: about OGA_ADA_WGS_PER_CU workgroups per CU, each
@@ -503,14 +720,22 @@ static void launch_row_v(RowArgs& a, int64_t batch, bool vec, hipStream_t st) {
       hipLaunchKernelGGL((k_elem<CH, OP, UNIFORM, D0, D1, true>), grid, dim3(256), 0, st, a, rpg);
     else
       hipLaunchKernelGGL((k_elem<CH, OP, UNIFORM, D0, D1, false>), grid, dim3(256), 0, st, a, rpg);
+  } else if (vec) {
+    dim3 grid;
+    int64_t vpb = 0, rpw = 0;
+    adazero_rows_grid(batch, a.tokens, grid, vpb, rpw);
+    const dim3 block(64 * kAdaWaves);
+    if (!a.s0.tab)
+      hipLaunchKernelGGL((k_adazero_rows<CH, UNIFORM, D0, D1, TAB_NONE>), grid, block, 0, st, a, vpb);
+    else if (a.s0.tab_dt == OGA_DT_BF16)
+      hipLaunchKernelGGL((k_adazero_rows<CH, UNIFORM, D0, D1, TAB_BF16>), grid, block, 0, st, a, vpb);
+    else
+      hipLaunchKernelGGL((k_adazero_rows<CH, UNIFORM, D0, D1, TAB_F32>), grid, block, 0, st, a, vpb);
   } else {
     dim3 grid;
     int rpw = 0;
     adazero_grid(batch, a.tokens, grid, rpw);
-    if (vec)
-      hipLaunchKernelGGL((k_adazero<CH, UNIFORM, D0, D1, true>), grid, dim3(64 * CH), 0, st, a, rpw);
-    else
-      hipLaunchKernelGGL((k_adazero<CH, UNIFORM, D0, D1, false>), grid, dim3(64 * CH), 0, st, a, rpw);
+    hipLaunchKernelGGL((k_adazero_gather<CH, UNIFORM, D0, D1, false>), grid, dim3(64 * CH), 0, st, a, rpw);
   }
 }
 
@@ -541,7 +766,9 @@ static int run_row(RowArgs& a, int64_t batch, hipStream_t st) {
   if (batch > 65535) return unsupported("batch > 65535");
   constexpr bool two = RowTraits<OP>::kTwo;
   const bool uniform = a.s0.ts_st == 0 && (!two || a.s1.ts_st == 0);
-  const bool vec = a.s0.ts_vec && (!two || a.s1.ts_vec);
+  bool vec = a.s0.ts_vec && (!two || a.s1.ts_vec);
+  if (OP == OP_ADAZERO && a.s0.tab)  // k_adazero_rows reads table rows 16 bytes at a time
+    vec = vec && a.s0.tab_vec && a.s1.tab_vec && a.s0.tab_dt == a.s1.tab_dt;
   return a.cols == 4096 ? launch_row_ch<8, OP>(a, batch, uniform, vec, st)
                         : launch_row_ch<4, OP>(a, batch, uniform, vec, st);
 }
@@ -665,10 +892,10 @@ extern "C" int oga_residual_gate_bf16(const void* x, const void* y, const void* 
 
 extern "C" int64_t oga_rows_per_wave(int kind, int64_t batch, int64_t tokens, int64_t cols) {
   if (batch < 1 || tokens < 1 || (cols != 2048 && cols != 4096)) return 0;
-  if (kind == OGA_ROWS_ADAZERO) {
+  if (kind == OGA_ROWS_ADAZERO) {  // the vectorised kernel, k_adazero_rows
     dim3 grid;
-    int rpw = 0;
-    adazero_grid(batch, tokens, grid, rpw);
+    int64_t vpb = 0, rpw = 0;
+    adazero_rows_grid(batch, tokens, grid, vpb, rpw);
     return rpw;
   }
   if (kind == OGA_ROWS_ELEMENTWISE) {

@@ -2,7 +2,7 @@
 
 The small-shape parity tests give every wave of the token-row kernels a
 single row. At the configured shapes the kernels stream several rows per
-wave (AdaZero at 2304 tokens, the continuation ops at 14080 tokens), with
+wave (AdaZero from 9216 tokens, the continuation ops at 14080 tokens), with
 later rows' loads in flight and a short last group; these tests run those
 schedules against the oracle, bit for bit, and assert from the library's own
 schedule query that the multi-row path is reached. Inputs are drawn on the
@@ -10,9 +10,9 @@ CPU with seeded generators, so the oracle and the kernels see the same bits.
 
 Shapes:
   AdaZero            (1, 2304, 4096), bf16 table, one timestep row for all
-                     tokens; (2, 1537, 4096) per-token timesteps with a float32
-                     table (a 1-row last workgroup); (1, 2305, 4096) float32
-                     timesteps broadcast
+                     tokens; (1, 9216, 4096) and (1, 9217, 4096) (3 and 4 rows
+                     per wave); (2, 1537, 4096) per-token timesteps with a
+                     float32 table; (1, 2305, 4096) float32 timesteps
   continuation ops   (1, 14080, 4096) and (1, 4999, 4096) (short last group),
                      per-token 9-row timestep embeddings with a t = 0 prefix
   Q/K RMSNorm+RoPE   (1, 9216, 4096) with the (16, 18, 32) grid table
@@ -91,19 +91,22 @@ def ada_rows(table: torch.Tensor, ts: torch.Tensor, indices) -> tuple[T, T]:
 
 # ------------------------------------------------------------------ AdaZero
 ADA_CASES = [
-    # batch, tokens, table dtype, ts dtype, broadcast ts
-    (1, 2304, torch.bfloat16, torch.bfloat16, True),   # config 1
-    (2, 1537, torch.float32, torch.bfloat16, False),   # per-token; 1-row last workgroup
-    (1, 2305, torch.bfloat16, torch.float32, True),    # float32 Ada values
+    # batch, tokens, table dtype, ts dtype, broadcast ts, several rows per wave
+    (1, 2304, torch.bfloat16, torch.bfloat16, True, False),  # config 1 (one row per wave)
+    (1, 9216, torch.bfloat16, torch.bfloat16, True, True),   # the 576p block shape, next row in flight
+    (1, 9217, torch.float32, torch.bfloat16, True, True),    # ragged: waves with 4 and with 3 rows
+    (2, 1537, torch.float32, torch.bfloat16, False, True),   # per-token timesteps, two batches
+    (1, 2305, torch.bfloat16, torch.float32, True, False),   # float32 Ada values
 ]
 
 
-@pytest.mark.parametrize("batch,tokens,tdt,sdt,bc", ADA_CASES)
-def test_adazero_from_ada_config_shape(batch, tokens, tdt, sdt, bc):
+@pytest.mark.parametrize("batch,tokens,tdt,sdt,bc,multi", ADA_CASES)
+def test_adazero_from_ada_config_shape(batch, tokens, tdt, sdt, bc, multi):
     from opengenie_amd import _lib
     from opengenie_amd.ltx_ops import fused_adazero_from_ada
 
-    assert rows_per_wave(_lib.ROWS_ADAZERO, batch, tokens) >= 2
+    rpw = rows_per_wave(_lib.ROWS_ADAZERO, batch, tokens)
+    assert rpw >= (2 if multi else 1), rpw
     x = randn((batch, tokens, C), 20260101)
     table = randn((6, C), 20260102, dtype=tdt, std=0.02)
     ts = randn((batch, 1 if bc else tokens, 6 * C), 20260103, dtype=sdt, std=0.5)
