@@ -385,12 +385,10 @@ __global__ __launch_bounds__(512) void k_adazero_gather(RowArgs a, int rows_per_
 // of a workgroup first fill LDS with the per-column constants in float32:
 // with one timestep row shared by all tokens, the finished Ada values (shift
 // and R?(1 + scale)); otherwise the table parts R?(table[i]), to which each
-// row adds its own timestep values. The constant loads go out before the row
-// loads (loads complete in order, so the fill never waits for a row) and one
-// barrier publishes the constants. A wave then streams rows t = v, v + V,
-// ... of its batch (V waves per batch), with the next row's loads in flight
-// while it finishes the current one when the timestep row is shared. Two
-// values are rounded per v_cvt_pk_bf16_f32.
+// row adds its own timestep values. One barrier publishes the constants. A
+// wave then streams rows t = v, v + V, ... of its batch (V waves per batch),
+// with the next row's loads in flight while it finishes the current one when
+// the timestep row is shared. Two values are rounded per v_cvt_pk_bf16_f32.
 #ifndef OGA_ADA_WAVES
 #define OGA_ADA_WAVES 12
 #endif
@@ -421,37 +419,42 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
   // A wave past the batch's V waves takes no rows but joins the fill.
   const int64_t t_first = v < V ? v : a.tokens;
 
-  // Constant loads: table rows and, when shared, the timestep row.
+  // The first row's loads, then the constant loads (table rows and, when
+  // shared, the timestep row). Every one is unconditional (a wave without
+  // rows loads row tokens - 1 and stores nothing; a thread past the column
+  // groups repeats group gi % G and writes the same values): a branch around
+  // a load would make the compiler wait for every outstanding load at its
+  // merge. The rows go first so that they are in flight as early as
+  // possible; the fill then waits for them too (loads complete in order),
+  // which costs nothing since the wave needs its row next anyway.
+  const uint16_t* const xb = a.x + b * a.tokens * C + lane * 8;
+  uint16_t* const yb = a.out + b * a.tokens * C + lane * 8;
+  uint4 xv[CH];
+  {
+    const int64_t tl = t_first < a.tokens ? t_first : a.tokens - 1;
+#pragma unroll
+    for (int j = 0; j < CH; ++j) xv[j] = *(const uint4*)(xb + tl * C + j * 512);
+  }
   Raw8<TD> tr0[GPT], tr1[GPT];
   Raw8<D0> u0[GPT];
   Raw8<D1> u1[GPT];
 #pragma unroll
   for (int q = 0; q < GPT; ++q) {
-    const int gi = tid + q * NT;
-    if (gi < G) {
-      if constexpr (HT) {
-        tr0[q] = raw8_load<TD>(a.s0.tab, a.s0.tab_off + gi * 8);
-        tr1[q] = raw8_load<TD>(a.s1.tab, a.s1.tab_off + gi * 8);
-      }
-      if constexpr (UNIFORM) {
-        u0[q] = raw8_load<D0>(a.s0.ts, a.s0.ts_off + b * a.s0.ts_sb + gi * 8);
-        u1[q] = raw8_load<D1>(a.s1.ts, a.s1.ts_off + b * a.s1.ts_sb + gi * 8);
-      }
+    const int gi = (tid + q * NT) % G;
+    if constexpr (HT) {
+      tr0[q] = raw8_load<TD>(a.s0.tab, a.s0.tab_off + gi * 8);
+      tr1[q] = raw8_load<TD>(a.s1.tab, a.s1.tab_off + gi * 8);
     }
-  }
-  // The first row's loads.
-  const uint16_t* const xb = a.x + b * a.tokens * C + lane * 8;
-  uint16_t* const yb = a.out + b * a.tokens * C + lane * 8;
-  uint4 xv[CH];
-  if (t_first < a.tokens) {
-#pragma unroll
-    for (int j = 0; j < CH; ++j) xv[j] = *(const uint4*)(xb + t_first * C + j * 512);
+    if constexpr (UNIFORM) {
+      u0[q] = raw8_load<D0>(a.s0.ts, a.s0.ts_off + b * a.s0.ts_sb + gi * 8);
+      u1[q] = raw8_load<D1>(a.s1.ts, a.s1.ts_off + b * a.s1.ts_sb + gi * 8);
+    }
   }
   // Constants to LDS.
 #pragma unroll
   for (int q = 0; q < GPT; ++q) {
-    const int gi = tid + q * NT;
-    if (gi < G) {
+    const int gi = (tid + q * NT) % G;
+    {
       float c0[8], c1[8];
       if constexpr (HT) {
         raw8_get<TD>(tr0[q], c0);

@@ -11,6 +11,10 @@ Every value that torch would hold as bfloat16 is held here as a float32 array
 whose values are exactly representable in bfloat16; `numerics.bf16_round` is
 applied at exactly the points where torch's result dtype is bfloat16.
 
+`oracle.torch_ref` holds the same expressions written in torch, so that torch
+itself evaluates them (on the CPU for the pins, on the GPU for the device
+semantics, and on the host cores as bench.py's CPU baseline).
+
 Parity pins (what checks each function; the tests named live in `tests/`):
 - numerics.bf16_round: torch CPU float32->bfloat16 conversion, exhaustive
   over structured and random float32 bit patterns (test_oracle_pins.py).
@@ -30,4 +34,11 @@ Parity pins (what checks each function; the tests named live in `tests/`):
   invariants cos=1/sin=0 -> rms_norm*w and sin=1/cos=0 -> a quarter turn.
 - ltx_ops.attention: torch.nn.functional.scaled_dot_product_attention in
   float64 on the CPU.
+- ltx_ops.gelu_tanh: torch's gelu(approximate='tanh') on the GPU over all
+  65536 bfloat16 inputs, bit for bit (test_gpu_parity.py), and on the CPU
+  except four inputs where torch's vectorised CPU tanh saturates early.
+- ltx_ops.fp8_per_head_quantize: torch's expression (:976-980) on the CPU
+  (device="cpu", division by 448) and on the GPU (device="cuda",
+  multiplication by float32(1/448), torch's GPU rule for a Python-scalar
+  divisor), including NaN heads.
 """

@@ -1,11 +1,12 @@
 """The reference's torch expressions for each fused op, evaluated by torch.
 
-These are the one-to-three-line torch fallbacks of
-`ltx_serve/triton_ltx_ops.py` (file:line cited per function), written out so
-that torch itself evaluates them on whatever device the inputs live on. They
-are the ground truth the numpy oracle is pinned against on the CPU, and a
-second check of the HIP kernels on the GPU. Nothing here is imported by the
-product package.
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py). These are the
+one-to-three-line torch fallbacks of `ltx_serve/triton_ltx_ops.py` (file:line
+cited per function), written out so that torch itself evaluates them on
+whatever device the inputs live on. They are the ground truth the numpy
+oracle is pinned against, a second check of the HIP kernels on the GPU, and
+the CPU baseline that bench.py times on the host's cores. Nothing here is
+imported by the product package.
 """
 
 from __future__ import annotations
@@ -122,3 +123,23 @@ def fp8_linear(qinput, weight, input_scale, weight_scale, bias):
     if bias is not None:
         out = out + bias.to(out.dtype)
     return out
+
+
+def fp8_linear_decoded(qinput, weight, input_scale, weight_scale, bias):
+    """The arithmetic of :1691-1709 with torch's float32 matmul of the decoded
+    e4m3 codes in place of torch._scaled_mm (which runs below 1 GFLOP/s on a
+    CPU): R(R(acc * (scale_a * scale_b)) + R(bias)), acc the float32 sum of
+    the exact code products."""
+    acc = qinput.float() @ weight.float().t()
+    out = (acc * (input_scale.float() * weight_scale.float())).to(torch.bfloat16)
+    if bias is not None:
+        out = out + bias.to(out.dtype)
+    return out
+
+
+def attention(q, k, v, scale=None):
+    """Dense video self-attention as the reference computes it with FA3
+    (official_ltx23_benchmark.py:3294-3369): softmax(q k^T * scale) v,
+    non-causal, here through torch's scaled_dot_product_attention on
+    [B, H, N, D] tensors."""
+    return torch.nn.functional.scaled_dot_product_attention(q, k, v, scale=scale)

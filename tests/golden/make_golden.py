@@ -27,7 +27,7 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
-import tests.torch_reference as tr  # noqa: E402
+import oracle.torch_ref as tr  # noqa: E402
 
 OUT = os.path.join(HERE, "golden.npz")
 

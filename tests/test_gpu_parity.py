@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-import tests.torch_reference as tr
+import oracle.torch_ref as tr
 from oracle import ltx_ops as O
 from oracle.numerics import T, bf16_from_bits, bf16_round, e4m3_decode, e4m3_encode
 from tests.helpers import assert_same_bits, bf16_ulp_distance, nan_canon, np32, randn, to_T

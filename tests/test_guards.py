@@ -10,7 +10,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-import tests.torch_reference as tr
+import oracle.torch_ref as tr
 from opengenie_amd import ltx_ops as L
 from tests.helpers import randn
 
