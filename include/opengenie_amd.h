@@ -273,6 +273,22 @@ int oga_fp8_dequant_per_head(const void* x8, const float* descale, void* out, in
 int oga_selftest_convert(const float* in, uint16_t* bf16_out, uint8_t* e4m3_out, int64_t n, void* stream);
 
 /*
+ * Allocation-free variant of oga_fp8_quantize_per_head. No counterpart in
+ * the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The amax partials live in a static device array of
+ * oga_fp8_per_head_noalloc_max_bytes() bytes (1 MiB) that each GPU holds
+ * until the process ends; a shape needing more (batch * ceil(tokens/16) *
+ * heads * 4 bytes, e.g. up to 131072 tokens at 32 heads) is rejected with
+ * OGA_EUNSUPPORTED. Nothing is allocated or freed. Calls on one GPU share
+ * that array, so calls that overlap in time on one GPU race. Same results as
+ * oga_fp8_quantize_per_head.
+ */
+int64_t oga_fp8_per_head_noalloc_max_bytes(void);
+int oga_fp8_quantize_per_head_noalloc(const void* x, void* q, float* scale_out, int64_t batch, int64_t tokens,
+                                      int64_t heads, int64_t head_dim, void* stream);
+
+/*
  * Schedule query of the token-row kernels: how many token rows of one batch
  * a single wave streams in sequence for an op of `kind` at this shape on the
  * current device (OGA_ROWS_ADAZERO: oga_adazero[_from_ada];

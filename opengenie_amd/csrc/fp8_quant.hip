@@ -11,6 +11,8 @@
 // float32. Every thread converts 16 elements: two 128-bit loads, one 128-bit
 // store. The e4m3 rounding is the hardware v_cvt_pk_fp8_f32 (nearest even),
 // applied after the clamp so saturation never engages.
+#include <atomic>
+
 #include "common.h"
 #include "host.h"
 
@@ -303,18 +305,19 @@ extern "C" int64_t oga_fp8_per_head_workspace_bytes(int64_t batch, int64_t token
   return batch * head_chunks(tokens) * heads * (int64_t)sizeof(float);
 }
 
-extern "C" int oga_fp8_quantize_per_head(const void* x, void* q, float* scale_out, void* workspace, int64_t batch,
-                                         int64_t tokens, int64_t heads, int64_t head_dim, void* stream) {
-  if (!x || !q || !scale_out || !workspace) return fail("null pointer");
+// Both passes of the per-head quantizer with the amax partials in `partial`
+// (batch * head_chunks(tokens) * heads floats; pass 1 writes every one that
+// pass 2 reads, so nothing needs clearing).
+static int per_head_run(const void* x, void* q, float* scale_out, float* partial, int64_t batch, int64_t tokens,
+                        int64_t heads, int64_t head_dim, hipStream_t st) {
+  if (!x || !q || !scale_out || !partial) return fail("null pointer");
   if (batch < 1 || tokens < 1 || heads < 1) return fail("empty shape");
   if (batch > 65535) return unsupported("batch > 65535");
   if (head_dim != 64 && head_dim != 128) return unsupported("head_dim must be 64 or 128");
   const int64_t row = heads * head_dim;
   if (row != 1024 && row != 2048 && row != 4096) return unsupported("heads*head_dim must be 1024, 2048 or 4096");
   if (!aligned(x, 16) || !aligned(q, 16)) return fail("x/q must be 16-byte aligned");
-  hipStream_t st = (hipStream_t)stream;
   const uint16_t* xs = (const uint16_t*)x;
-  float* partial = (float*)workspace;
   const int ch = (int)(row / 512);
   if (head_dim == 128) {
     if (ch == 8) launch_head_amax<8, 128>(xs, partial, batch, tokens, st);
@@ -335,6 +338,57 @@ extern "C" int oga_fp8_quantize_per_head(const void* x, void* q, float* scale_ou
     hipLaunchKernelGGL(k_head_scale_quant<64>, qgrid, dim3(256), 0, st, xs, partial, scale_out, (uint8_t*)q, tokens,
                        (int)heads, (int)head_chunks(tokens));
   return launch_status();
+}
+
+// ------------------------------------------- allocation-free entry point
+// The amax partials of oga_fp8_quantize_per_head_noalloc live in `scratch`,
+// a file-scope device array of kPerHeadScratchBytes that every GPU the
+// library runs on holds until the process ends. In host code `scratch` only
+// names the symbol; its address on a device comes from hipGetSymbolAddress,
+// called with that device current on the first call there and kept per
+// device. Calls on one device share the array: calls that overlap in time on
+// one GPU (different streams, or threads) race on it.
+constexpr int64_t kPerHeadScratchBytes = 1 << 20;
+static __device__ __align__(256) float scratch[kPerHeadScratchBytes / sizeof(float)];
+constexpr int kMaxScratchDevices = 64;
+static std::atomic<void*> g_scratch_ptr[kMaxScratchDevices];
+
+static int scratch_ptr(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxScratchDevices) return unsupported("device ordinal %d beyond %d", dev, kMaxScratchDevices);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return fail("scratch has no device address");
+    g_scratch_ptr[dev].store(p, std::memory_order_release);
+  }
+  *out = (float*)p;
+  return OGA_OK;
+}
+
+extern "C" int oga_fp8_quantize_per_head(const void* x, void* q, float* scale_out, void* workspace, int64_t batch,
+                                         int64_t tokens, int64_t heads, int64_t head_dim, void* stream) {
+  if (!workspace) return fail("null pointer");
+  return per_head_run(x, q, scale_out, (float*)workspace, batch, tokens, heads, head_dim, (hipStream_t)stream);
+}
+
+extern "C" int64_t oga_fp8_per_head_noalloc_max_bytes(void) { return kPerHeadScratchBytes; }
+
+extern "C" int oga_fp8_quantize_per_head_noalloc(const void* x, void* q, float* scale_out, int64_t batch,
+                                                 int64_t tokens, int64_t heads, int64_t head_dim, void* stream) {
+  if (batch < 1 || tokens < 1 || heads < 1) return fail("empty shape");
+  const int64_t need = oga_fp8_per_head_workspace_bytes(batch, tokens, heads, head_dim);
+  if (need > kPerHeadScratchBytes)
+    return unsupported("per-head amax partials need %lld bytes, more than the %lld-byte static scratch "
+                       "(use oga_fp8_quantize_per_head with a workspace)", (long long)need,
+                       (long long)kPerHeadScratchBytes);
+  float* partial = nullptr;
+  const int rc = scratch_ptr(&partial);
+  if (rc) return rc;
+  return per_head_run(x, q, scale_out, partial, batch, tokens, heads, head_dim, (hipStream_t)stream);
 }
 
 extern "C" int oga_selftest_convert(const float* in, uint16_t* bf16_out, uint8_t* e4m3_out, int64_t n, void* stream) {
