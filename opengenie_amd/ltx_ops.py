@@ -49,6 +49,10 @@ __all__ = [
     "fp8_qkv_from_shared_quantized_input",
     "fp8_qkv_from_grouped_mm",
     "fp8_qk_from_grouped_mm",
+    "fp8_qkv_from_packed_linear",
+    "fp8_qkv_from_packed_requant",
+    "collect_video_qkv_packed_linear_stats",
+    "collect_video_qkv_packed_requant_stats",
 ]
 
 _FP8 = torch.float8_e4m3fn
@@ -946,31 +950,47 @@ def _grouped_hip_ok(linears, qflat: torch.Tensor, out_dtype: torch.dtype) -> boo
     return True
 
 
-def _fp8_grouped_linear(linears, qinput: torch.Tensor, out_dtype: torch.dtype) -> tuple[torch.Tensor, ...]:
-    """One quantized input through several FP8 linears with their own weight
-    scales and biases: R(R(acc * sa * sb_i) + R(bias_i)) per linear, one HIP
-    launch for all; otherwise each as `fp8_linear_from_quantized_e4m3`."""
+def _grouped_launch(linears, qflat: torch.Tensor, weight_scales, outs, ldo: int) -> None:
+    """One launch of the grouped FP8 GEMM: linear i's weight, `weight_scales[i]`
+    and bias into `outs[i]` (column blocks with row stride `ldo`)."""
     import ctypes
 
-    qflat = qinput.reshape(-1, qinput.shape[-1]) if qinput.dim() == 3 else qinput
-    if not _grouped_hip_ok(linears, qflat, out_dtype):
-        _fallback("fp8_grouped_linear", qinput)
-        return tuple(fp8_linear_from_quantized_e4m3(lin, qinput, out_dtype=out_dtype) for lin in linears)
     m, k = qflat.shape
     n = linears[0].weight.shape[0]
-    outs = [torch.empty((m, n), device=qflat.device, dtype=out_dtype) for _ in linears]
     lib = _lib.load()
     ws_bytes = int(lib.oga_fp8_linear_workspace_bytes(m, n * len(linears), k))
     ws = torch.empty((ws_bytes // 4,), device=qflat.device, dtype=torch.float32) if ws_bytes else None
     arr = ctypes.c_void_p * len(linears)
     w_p = arr(*[lin.weight.data_ptr() for lin in linears])
-    s_p = arr(*[lin.weight_scale.data_ptr() for lin in linears])
+    s_p = arr(*[s.data_ptr() for s in weight_scales])
     b_p = arr(*[lin.bias.data_ptr() for lin in linears])
     o_p = arr(*[o.data_ptr() for o in outs])
     _hip("fp8_grouped_linear")
     _lib.call("oga_fp8_linear_grouped_ws", qflat.data_ptr(), qflat.stride(0), ctypes.addressof(w_p), k,
               linears[0].input_scale.data_ptr(), ctypes.addressof(s_p), ctypes.addressof(b_p), _lib.DT_BF16,
-              ctypes.addressof(o_p), n, m, n, len(linears), k, _ptr(ws), ws_bytes, _stream(qflat))
+              ctypes.addressof(o_p), ldo, m, n, len(linears), k, _ptr(ws), ws_bytes, _stream(qflat))
+
+
+def _packed_hip_ok(linears, qflat: torch.Tensor, out_dtype: torch.dtype) -> bool:
+    """The grouped kernel can write the packed output: grouped-kernel operands
+    and equal square weights."""
+    n = linears[0].weight.shape[0]
+    return _grouped_hip_ok(linears, qflat, out_dtype) and all(tuple(lin.weight.shape) == (n, qflat.shape[1])
+                                                              for lin in linears)
+
+
+def _fp8_grouped_linear(linears, qinput: torch.Tensor, out_dtype: torch.dtype) -> tuple[torch.Tensor, ...]:
+    """One quantized input through several FP8 linears with their own weight
+    scales and biases: R(R(acc * sa * sb_i) + R(bias_i)) per linear, one HIP
+    launch for all; otherwise each as `fp8_linear_from_quantized_e4m3`."""
+    qflat = qinput.reshape(-1, qinput.shape[-1]) if qinput.dim() == 3 else qinput
+    if not _grouped_hip_ok(linears, qflat, out_dtype):
+        _fallback("fp8_grouped_linear", qinput)
+        return tuple(fp8_linear_from_quantized_e4m3(lin, qinput, out_dtype=out_dtype) for lin in linears)
+    m = qflat.shape[0]
+    n = linears[0].weight.shape[0]
+    outs = [torch.empty((m, n), device=qflat.device, dtype=out_dtype) for _ in linears]
+    _grouped_launch(linears, qflat, [lin.weight_scale for lin in linears], outs, n)
     if qinput.dim() == 3:
         outs = [o.reshape(qinput.shape[0], qinput.shape[1], n) for o in outs]
     return tuple(outs)
@@ -1004,3 +1024,195 @@ def fp8_qk_from_grouped_mm(attn: torch.nn.Module, x: torch.Tensor):
         return None
     qinput = fused_fp8_quantize_e4m3(x.contiguous(), attn.to_q.input_scale)
     return _fp8_grouped_linear((attn.to_q, attn.to_k), qinput, x.dtype)
+
+
+# --------------------------------------------------------------------------
+# Packed Q/K/V projections (:822-887) and their fallback/check bookkeeping
+# (:1915-1924, :2072-2110, :2179-2198)
+# --------------------------------------------------------------------------
+_PACKED_STATS = {
+    "packed_linear": {"calls": 0, "fallbacks": 0, "fallback_reasons": {}},
+    "packed_requant": {"calls": 0, "fallbacks": 0, "fallback_reasons": {}, "checks": []},
+}
+_PACKED_REQUANT_CHECK_LIMIT = 0
+
+
+def _record_packed_fallback(kind: str, reason: str) -> None:
+    st = _PACKED_STATS[kind]
+    st["fallbacks"] += 1
+    st["fallback_reasons"][reason] = st["fallback_reasons"].get(reason, 0) + 1
+
+
+def reset_video_qkv_packed_stats(requant_checks: int = 0) -> None:
+    """Zeroes the packed-projection counters (what the reference's
+    patch_ltx_video_qkv_packed_linear / _requant(checks) do to them, :2072-2100);
+    `requant_checks` calls of the requantized form are compared with the
+    per-linear projections and recorded."""
+    global _PACKED_REQUANT_CHECK_LIMIT
+    for kind, st in _PACKED_STATS.items():
+        st["calls"] = 0
+        st["fallbacks"] = 0
+        st["fallback_reasons"] = {}
+        if kind == "packed_requant":
+            st["checks"] = []
+    _PACKED_REQUANT_CHECK_LIMIT = max(0, int(requant_checks)) * 3
+
+
+def collect_video_qkv_packed_linear_stats() -> dict:
+    """:2082-2087"""
+    st = _PACKED_STATS["packed_linear"]
+    return {"calls": st["calls"], "fallbacks": st["fallbacks"], "fallback_reasons": dict(st["fallback_reasons"])}
+
+
+def collect_video_qkv_packed_requant_stats() -> dict:
+    """:2104-2110"""
+    st = _PACKED_STATS["packed_requant"]
+    return {"calls": st["calls"], "fallbacks": st["fallbacks"], "fallback_reasons": dict(st["fallback_reasons"]),
+            "checks": list(st["checks"])}
+
+
+def _features(linear) -> tuple[int, int]:
+    """(in_features, out_features) of an FP8 linear; from the e4m3 weight's
+    [out, in] shape when the module carries no such attributes."""
+    w = linear.weight
+    return int(getattr(linear, "in_features", w.shape[1])), int(getattr(linear, "out_features", w.shape[0]))
+
+
+def _packed_guard_reason(attn: torch.nn.Module, x: torch.Tensor, *, equal_weight_scales: bool) -> str | None:
+    """:1099-1145 (equal_weight_scales) and :1146-1185, with FP8Linear
+    recognised by its attributes; the same reasons as the reference records."""
+    if not x.is_cuda or not x.is_contiguous() or x.dtype not in (torch.bfloat16, torch.float16):
+        return "input"
+    if x.ndim != 3 or x.shape[0] != 1 or x.shape[1] < 1 or x.shape[-1] != 4096:
+        return "shape"
+    linears = (getattr(attn, "to_q", None), getattr(attn, "to_k", None), getattr(attn, "to_v", None))
+    if not all(_is_fp8_linear(lin) for lin in linears):
+        return "linear_type"
+    if not all(getattr(lin, "bias", None) is not None for lin in linears):
+        return "bias"
+    q, k, v = linears
+    if not (torch.equal(q.input_scale, k.input_scale) and torch.equal(q.input_scale, v.input_scale)):
+        return "input_scale"
+    if equal_weight_scales and not (torch.equal(q.weight_scale, k.weight_scale)
+                                    and torch.equal(q.weight_scale, v.weight_scale)):
+        return "weight_scale"
+    feats = [_features(lin) for lin in linears]
+    if not all(fi == x.shape[-1] and fo == x.shape[-1] for fi, fo in feats):
+        return "features"
+    return None
+
+
+def _split_packed(output: torch.Tensor, x: torch.Tensor, out_features: int):
+    """(M, 3*out) -> the reference's `output.split(out_features, dim=-1)` of
+    the (B, N, 3*out) view."""
+    if output.dim() != len(x.shape):
+        output = output.reshape(x.shape[0], x.shape[1], output.shape[-1])
+    return output.split(out_features, dim=-1)
+
+
+def fp8_qkv_from_packed_linear(attn: torch.nn.Module, x: torch.Tensor):
+    """:822-850 — exact Q/K/V projections as one packed FP8 matmul, for three
+    FP8 linears with equal input and equal weight scales: R(R(acc * sa * sb) +
+    R(bias)) over the packed [Wq; Wk; Wv], returned as the three column views
+    of one (B, N, 3*4096) output. Here one launch of the grouped kernel writes
+    each linear's columns into that output (no packed copy of the weights).
+    None when the guard fails or the launch raises (reason recorded)."""
+    reason = _packed_guard_reason(attn, x, equal_weight_scales=True)
+    if reason is not None:
+        _record_packed_fallback("packed_linear", reason)
+        return None
+    try:
+        lins = (attn.to_q, attn.to_k, attn.to_v)
+        qinput = fused_fp8_quantize_e4m3(x.contiguous(), attn.to_q.input_scale)
+        qflat = qinput.reshape(-1, qinput.shape[-1]) if qinput.dim() == 3 else qinput
+        n = _features(attn.to_q)[1]
+        m, k = qflat.shape
+        if _packed_hip_ok(lins, qflat, x.dtype):
+            output = torch.empty((m, 3 * n), device=qflat.device, dtype=x.dtype)
+            _grouped_launch(lins, qflat, [attn.to_q.weight_scale] * 3, [output[:, i * n:(i + 1) * n] for i in range(3)],
+                            3 * n)
+        else:
+            wp = torch.cat([lin.weight for lin in lins], dim=0)
+            bp = torch.cat([lin.bias for lin in lins], dim=0)
+            output = fp8_scaled_mm(qflat, wp, attn.to_q.input_scale, attn.to_q.weight_scale, bp, out_dtype=x.dtype)
+        _PACKED_STATS["packed_linear"]["calls"] += 1
+        return _split_packed(output, x, n)
+    except _lib.LibraryMissing:
+        raise
+    except Exception as exc:  # the reference counts the exception and returns None (:847-849)
+        _record_packed_fallback("packed_linear", type(exc).__name__)
+        return None
+
+
+def _requantized_packed(attn: torch.nn.Module) -> dict:
+    """:1311-1345 — the packed weight requantized to one common scale (the
+    largest of the three weight scales): e4m3(clamp(W.float() * ws / common,
+    +-448)) per linear, cached on the module by weight/bias pointers and scale
+    values. A one-time weight transform, evaluated with the reference's own
+    torch expression on the weights' device."""
+    scales = (attn.to_q.weight_scale, attn.to_k.weight_scale, attn.to_v.weight_scale)
+    key = (attn.to_q.weight.data_ptr(), attn.to_k.weight.data_ptr(), attn.to_v.weight.data_ptr(),
+           attn.to_q.bias.data_ptr(), attn.to_k.bias.data_ptr(), attn.to_v.bias.data_ptr(),
+           tuple(float(s.detach().float().item()) for s in scales))
+    cached = getattr(attn, "_oga_qkv_packed_requant_cache", None)
+    if cached is not None and cached.get("key") == key:
+        return cached
+    common = torch.stack([s.detach().float().reshape(()) for s in scales]).amax().contiguous()
+
+    def requant(linear):
+        dequant = linear.weight.float() * linear.weight_scale.detach().float()
+        return torch.clamp(dequant / common, -_FP8_MAX, _FP8_MAX).to(_FP8)
+
+    packed = {
+        "key": key,
+        "weight": torch.cat((requant(attn.to_q), requant(attn.to_k), requant(attn.to_v)), dim=0).contiguous(),
+        "weight_scale": common,
+        "bias": torch.cat((attn.to_q.bias, attn.to_k.bias, attn.to_v.bias), dim=0).contiguous(),
+    }
+    attn._oga_qkv_packed_requant_cache = packed
+    return packed
+
+
+def _record_packed_requant_check(attn: torch.nn.Module, x: torch.Tensor, outs) -> None:
+    """:1412-1440 — error statistics of the requantized projections against
+    the per-linear FP8 projections, for the first checks."""
+    st = _PACKED_STATS["packed_requant"]
+    if len(st["checks"]) >= _PACKED_REQUANT_CHECK_LIMIT:
+        return
+    with torch.no_grad():
+        for name, lin, out in zip(("q", "k", "v"), (attn.to_q, attn.to_k, attn.to_v), outs):
+            ref = fp8_linear_forward(lin, x)
+            diff = (out.float() - ref.float()).abs()
+            denom = ref.float().abs().clamp_min(1e-6)
+            st["checks"].append({"tensor": name, "max_abs": float(diff.max().item()),
+                                 "mean_abs": float(diff.mean().item()),
+                                 "rms": float(torch.sqrt(torch.mean(diff.square())).item()),
+                                 "mean_rel": float((diff / denom).mean().item())})
+
+
+def fp8_qkv_from_packed_requant(attn: torch.nn.Module, x: torch.Tensor):
+    """:852-887 — Q/K/V as one packed FP8 matmul after requantizing the three
+    weights to their largest weight scale. Not exact to the checkpoint weights
+    (the reference keeps it behind --allow-quality-risk-packed-qkv-requant,
+    official_ltx23_benchmark.py:539-544). One FP8 GEMM of N = 3*4096 with the
+    bias epilogue; the three column views of its output. None when the guard
+    fails or the launch raises (reason recorded)."""
+    reason = _packed_guard_reason(attn, x, equal_weight_scales=False)
+    if reason is not None:
+        _record_packed_fallback("packed_requant", reason)
+        return None
+    try:
+        packed = _requantized_packed(attn)
+        qinput = fused_fp8_quantize_e4m3(x.contiguous(), attn.to_q.input_scale)
+        qflat = qinput.reshape(-1, qinput.shape[-1]) if qinput.dim() == 3 else qinput
+        output = fp8_scaled_mm(qflat, packed["weight"], attn.to_q.input_scale, packed["weight_scale"],
+                               packed["bias"], out_dtype=x.dtype)
+        q, k, v = _split_packed(output, x, _features(attn.to_q)[1])
+        _record_packed_requant_check(attn, x, (q, k, v))
+        _PACKED_STATS["packed_requant"]["calls"] += 1
+        return q, k, v
+    except _lib.LibraryMissing:
+        raise
+    except Exception as exc:  # :884-886
+        _record_packed_fallback("packed_requant", type(exc).__name__)
+        return None

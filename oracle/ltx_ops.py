@@ -245,6 +245,19 @@ def fp8_linear(a_codes, w_codes, scale_a, scale_b, bias: T | None) -> np.ndarray
     return bias_add(bf(out), bias).v
 
 
+def fp8_requantize_common_scale(w_codes: np.ndarray, w_scale: float, common: float) -> np.ndarray:
+    """`_get_video_qkv_packed_requant_cache._requant` (:1331-1333): the e4m3
+    weight dequantized with its own scale and requantized to the common one,
+    clamp(float32(W) * w_scale / common, -448, 448).to(float8_e4m3fn), with a
+    float32 product and an IEEE float32 division (both scales are tensors, so
+    neither operation takes torch's scalar shortcut)."""
+    deq = e4m3_decode(w_codes).astype(np.float32) * np.float32(w_scale)
+    with np.errstate(invalid="ignore", over="ignore"):
+        r = deq / np.float32(common)
+    r = np.where(np.isnan(r), r, np.minimum(np.maximum(r, np.float32(-E4M3_MAX)), np.float32(E4M3_MAX)))
+    return e4m3_encode(r.astype(np.float32))
+
+
 # --------------------------------------------------------------------------
 # Video Q/K preattention
 # --------------------------------------------------------------------------

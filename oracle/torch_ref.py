@@ -143,3 +143,11 @@ def attention(q, k, v, scale=None):
     non-causal, here through torch's scaled_dot_product_attention on
     [B, H, N, D] tensors."""
     return torch.nn.functional.scaled_dot_product_attention(q, k, v, scale=scale)
+
+
+def fp8_requantize_common_scale(weight, weight_scale, common_scale):
+    """:1331-1333"""
+    dequant = weight.float() * weight_scale.detach().float()
+    lo = torch.finfo(torch.float8_e4m3fn).min
+    hi = torch.finfo(torch.float8_e4m3fn).max
+    return torch.clamp(dequant / common_scale, lo, hi).to(torch.float8_e4m3fn)

@@ -683,6 +683,86 @@ def test_fp8_qkv_shared_quantized_input_and_guard():
     assert L.fp8_qk_from_grouped_mm(attn, g(randn((2, 8, 4096), 97))) is None
 
 
+def _qkv_attn(seed, s_in=0.0123, equal_weight_scales=False):
+    attn = torch.nn.Module()
+    si = g(torch.tensor(s_in))
+    for i, nm in enumerate(("to_q", "to_k", "to_v")):
+        setattr(attn, nm, _FP8Lin(4096, 4096, seed + 7 * i, si))
+    if equal_weight_scales:  # one scale for all three (the weights stay as drawn)
+        attn.to_k.weight_scale = attn.to_q.weight_scale.clone()
+        attn.to_v.weight_scale = attn.to_q.weight_scale.clone()
+    return attn
+
+
+def _close_to(got, ref, what):
+    close = np.isclose(got, ref, rtol=1e-2, atol=1e-3 * float(np.abs(ref).max()))
+    assert (~close).mean() < 1e-5 and (bf16_ulp_distance(got[~close], ref[~close]) <= 2).all(), what
+    assert (bf16_ulp_distance(got, ref) > 1).mean() < 1e-2, what
+
+
+@pytest.mark.parametrize("tokens", [300, 1536])
+def test_fp8_qkv_from_packed_linear(tokens):
+    """:822-850 — one launch writes the three linears into the columns of one
+    (1, N, 3*4096) output whose split views are returned; equal to the grouped
+    projection bit for bit and to the oracle per linear."""
+    from opengenie_amd import ltx_ops as L
+
+    attn = _qkv_attn(140, equal_weight_scales=True)
+    x = g(randn((1, tokens, 4096), 141))
+    L.reset_video_qkv_packed_stats()
+    out = L.fp8_qkv_from_packed_linear(attn, x)
+    assert out is not None and len(out) == 3
+    q, k, v = out
+    assert q.shape == (1, tokens, 4096) and q.stride() == (tokens * 3 * 4096, 3 * 4096, 1)
+    assert k.data_ptr() == q.data_ptr() + 4096 * 2 and v.data_ptr() == q.data_ptr() + 2 * 4096 * 2
+    grouped = L.fp8_qkv_from_grouped_mm(attn, x)
+    qx = O.fp8_quantize_e4m3(to_T(x.cpu()), 0.0123, True, device="cuda").reshape(tokens, 4096)
+    sb = float(attn.to_q.weight_scale)
+    for nm, a, b in zip(("to_q", "to_k", "to_v"), out, grouped):
+        assert_same_bits(out_np(a), out_np(b), f"packed vs grouped {nm}")
+        lin = getattr(attn, nm)
+        ref = O.fp8_linear(qx, lin.weight.view(torch.uint8).cpu().numpy(), 0.0123, sb, to_T(lin.bias.cpu()))
+        _close_to(out_np(a).reshape(tokens, 4096), ref, nm)
+    assert L.collect_video_qkv_packed_linear_stats() == {"calls": 1, "fallbacks": 0, "fallback_reasons": {}}
+    # the reference's guards: unequal weight scales, batch 2
+    attn.to_v.weight_scale = attn.to_v.weight_scale * 2
+    assert L.fp8_qkv_from_packed_linear(attn, x) is None
+    assert L.fp8_qkv_from_packed_linear(attn, g(randn((2, 8, 4096), 142))) is None
+    assert L.collect_video_qkv_packed_linear_stats()["fallback_reasons"] == {"weight_scale": 1, "shape": 1}
+
+
+def test_fp8_qkv_from_packed_requant():
+    """:852-887 — the three weights requantized to their largest scale (the
+    cached packed weight equals the oracle's requantization bit for bit), one
+    GEMM of N = 3*4096, each projection against the oracle on the requantized
+    weights; the check recorder compares with the exact per-linear projections."""
+    from opengenie_amd import ltx_ops as L
+
+    tokens = 700
+    attn = _qkv_attn(150)
+    scales = [float(getattr(attn, nm).weight_scale) for nm in ("to_q", "to_k", "to_v")]
+    assert len(set(scales)) == 3
+    x = g(randn((1, tokens, 4096), 151))
+    L.reset_video_qkv_packed_stats(requant_checks=1)
+    out = L.fp8_qkv_from_packed_requant(attn, x)
+    assert out is not None
+    common = float(np.max(np.float32(scales)))
+    packed = attn._oga_qkv_packed_requant_cache["weight"].view(torch.uint8).cpu().numpy()
+    qx = O.fp8_quantize_e4m3(to_T(x.cpu()), 0.0123, True, device="cuda").reshape(tokens, 4096)
+    for i, nm in enumerate(("to_q", "to_k", "to_v")):
+        lin = getattr(attn, nm)
+        wr = O.fp8_requantize_common_scale(lin.weight.view(torch.uint8).cpu().numpy(), scales[i], common)
+        assert np.array_equal(nan_canon(packed[i * 4096:(i + 1) * 4096]), nan_canon(wr)), nm
+        ref = O.fp8_linear(qx, wr, 0.0123, common, to_T(lin.bias.cpu()))
+        _close_to(out_np(out[i]).reshape(tokens, 4096), ref, nm)
+    st = L.collect_video_qkv_packed_requant_stats()
+    assert st["calls"] == 1 and len(st["checks"]) == 3
+    assert all(np.isfinite(c["rms"]) and c["rms"] < 0.1 for c in st["checks"]), st["checks"]
+    attn.to_k.input_scale = g(torch.tensor(0.02))
+    assert L.fp8_qkv_from_packed_requant(attn, x) is None
+    assert L.collect_video_qkv_packed_requant_stats()["fallback_reasons"] == {"input_scale": 1}
+
+
 def test_fp8_linear_forward_module():
     """The patched FP8Linear.forward on a duck-typed module, 3-D input."""
     from opengenie_amd.ltx_ops import fp8_linear_forward

@@ -332,3 +332,17 @@ def test_fp8_dequant_per_head_matches_torch():
     ref = (t * torch.from_numpy(descale)[:, None, :, None]).to(torch.bfloat16).float().numpy()
     got = O.fp8_dequant_per_head(codes, descale)
     np.testing.assert_array_equal(np.asarray(got, dtype=np.float32), ref)
+
+
+def test_fp8_requantize_common_scale_matches_torch():
+    """Every e4m3 code (NaN included) requantized from several weight scales to
+    common scales at and above them, against torch's expression (:1331-1333)."""
+    codes = np.arange(256, dtype=np.uint8)
+    w = torch.from_numpy(codes.copy()).view(torch.float8_e4m3fn)
+    for ws in (3.1e-5, 4.4643e-05, 1.0e-3, 0.37):
+        for ratio in (1.0, 1.37, 2.0, 7.91, 300.0):
+            cs = np.float32(ws) * np.float32(ratio)
+            ref = tr.fp8_requantize_common_scale(w, torch.tensor(ws, dtype=torch.float32),
+                                                 torch.tensor(float(cs), dtype=torch.float32))
+            ours = O.fp8_requantize_common_scale(codes, ws, float(cs))
+            assert np.array_equal(nan_canon(ours), nan_canon(ref.view(torch.uint8).numpy())), (ws, ratio)
