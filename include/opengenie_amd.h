@@ -265,6 +265,25 @@ int oga_fp8_dequant_per_head(const void* x8, const float* descale, void* out, in
                              int64_t heads, int64_t head_dim, void* stream);
 
 /*
+ * FP8 attention: FlashAttention-3's flash_attn_func on per-head e4m3 q, k, v
+ * with float32 [B, H] descales, as the reference calls it for FP8 video
+ * self-attention (official_ltx23_benchmark.py:3330-3340):
+ *   O = softmax(q8 k8^T * qd kd * softmax_scale) v8 * vd,
+ * both products on e4m3 MFMA, P rounded to e4m3 for the second (float32 row
+ * sums). q8/k8/v8 [B, N, H, 128] e4m3 with element strides (b, n, h), each a
+ * multiple of 16; o as for oga_attention. The workspace (256-byte aligned,
+ * oga_attention_fp8_workspace_bytes) holds V rewritten d-major for the
+ * second product, then float32 partials of a key-split last round of the CUs
+ * when it is large enough.
+ */
+int64_t oga_attention_fp8_workspace_bytes(int64_t batch, int64_t nq, int64_t nk, int64_t heads, int64_t head_dim);
+int oga_attention_fp8_ws(const void* q8, const int64_t q_strides[3], const void* k8, const int64_t k_strides[3],
+                         const void* v8, const int64_t v_strides[3], const float* q_descale, const float* k_descale,
+                         const float* v_descale, void* o, const int64_t o_strides[3], int64_t batch, int64_t nq,
+                         int64_t nk, int64_t heads, int64_t head_dim, float softmax_scale, void* workspace,
+                         int64_t workspace_bytes, void* stream);
+
+/*
  * Conversion self-test: runs the device rounding primitives every kernel
  * uses on n float32 inputs: bf16_out[i] = bf16 bits of R(in[i]) and
  * e4m3_out[i] = e4m3fn(clamp(in[i], +-448)). No reference counterpart; it

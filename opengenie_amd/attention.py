@@ -9,8 +9,9 @@ v_descale=..., window_size=...)` and reshapes the [B, N, H, D] result back
 per-head quantizer (`_to_fp8_per_head`, :3333-3340) with descales [B, H].
 
 `flash_attn_func` here takes the same arguments for the configuration the
-reference uses (non-causal, no window) and runs the gfx950 HIP kernel
-`oga_attention` on torch's current stream. Inputs the kernel does not cover
+reference uses (non-causal, no window) and runs the gfx950 HIP kernels
+`oga_attention_ws` (bf16) and `oga_attention_fp8_ws` (e4m3 with descales) on
+torch's current stream. Inputs the kernel does not cover
 (CPU tensors, head_dim != 128, causal or windowed attention, a softmax scale
 that is not positive, other dtypes)
 take torch's scaled_dot_product_attention, like the fused ops' torch paths;
@@ -54,6 +55,33 @@ def _dequant(x: torch.Tensor, descale: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def _fp8_kernel_ok(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, descales) -> bool:
+    for t in (q, k, v):
+        if not t.is_cuda or t.ndim != 4 or t.shape[-1] != 128 or t.stride(-1) != 1:
+            return False
+        if any(s % 16 for s in t.stride()[:3]) or t.data_ptr() % 16:
+            return False
+    if q.shape[0] != k.shape[0] or k.shape != v.shape or q.shape[2] != k.shape[2] or k.shape[1] < 1:
+        return False
+    b, h = q.shape[0], q.shape[2]
+    return b <= 65535 and h <= 65535 and all(d.is_cuda and d.numel() == b * h for d in descales)
+
+
+def _fp8_attention(q, k, v, q_descale, k_descale, v_descale, softmax_scale) -> torch.Tensor:
+    """The e4m3 kernel: both products on FP8 MFMA, P rounded to e4m3."""
+    b, nq, h, d = q.shape
+    nk = k.shape[1]
+    ds = [t.to(torch.float32).reshape(b, h).contiguous() for t in (q_descale, k_descale, v_descale)]
+    out = torch.empty((b, nq, h, d), device=q.device, dtype=torch.bfloat16)
+    ws_bytes = int(_lib.load().oga_attention_fp8_workspace_bytes(b, nq, nk, h, d))
+    ws = torch.empty((ws_bytes,), device=q.device, dtype=torch.uint8)
+    _hip("flash_attn_func_fp8")
+    _lib.call("oga_attention_fp8_ws", q.data_ptr(), _strides3(q), k.data_ptr(), _strides3(k), v.data_ptr(),
+              _strides3(v), ds[0].data_ptr(), ds[1].data_ptr(), ds[2].data_ptr(), out.data_ptr(), _strides3(out),
+              b, nq, nk, h, d, float(softmax_scale), ws.data_ptr(), ws_bytes, _stream(q))
+    return out
+
+
 def _torch_attention(q, k, v, softmax_scale, causal):
     qf, kf, vf = (t.float().transpose(1, 2) for t in (q, k, v))
     o = torch.nn.functional.scaled_dot_product_attention(qf, kf, vf, is_causal=causal, scale=softmax_scale)
@@ -76,13 +104,21 @@ def flash_attn_func(
 ) -> torch.Tensor:
     """softmax(q k^T * scale) v for q [B, Nq, H, D], k/v [B, Nk, H, D] -> [B, Nq, H, D] bf16.
 
-    e4m3 inputs are dequantized with their [B, H] descales (value * descale,
-    rounded to bf16) before the bf16 kernel. `attention_chunk`, `num_splits`
-    and `sm_margin` are FA3 scheduling knobs with no effect on the result.
+    e4m3 q, k and v with their [B, H] descales run the FP8 kernel, as FA3's
+    FP8 path does: S = (q8 k8^T) qd kd scale on e4m3 MFMA, P rounded to e4m3,
+    O = (P8 v8) vd / l. Other e4m3 inputs (mixed dtypes, layouts the kernel
+    does not take) are dequantized with their descales (value * descale,
+    rounded to bf16) for the bf16 kernel. `attention_chunk`, `num_splits` and
+    `sm_margin` are FA3 scheduling knobs with no effect on the result.
     """
     del attention_chunk, num_splits, sm_margin
     if softmax_scale is None:
         softmax_scale = q.shape[-1] ** -0.5
+    unsupported = causal or tuple(window_size) != (-1, -1) or not (0.0 < float(softmax_scale) < float("inf"))
+    descales = (q_descale, k_descale, v_descale)
+    if (not unsupported and all(t.dtype == _FP8 for t in (q, k, v)) and all(d is not None for d in descales)
+            and _fp8_kernel_ok(q, k, v, descales)):
+        return _fp8_attention(q, k, v, q_descale, k_descale, v_descale, softmax_scale)
     deq = []
     for t, ds in ((q, q_descale), (k, k_descale), (v, v_descale)):
         if t.dtype == _FP8:
@@ -97,7 +133,6 @@ def flash_attn_func(
     q, k, v = deq
     # The kernel takes the scale into its base-2 exponent with the running
     # max, which needs a positive scale.
-    unsupported = causal or tuple(window_size) != (-1, -1) or not (0.0 < float(softmax_scale) < float("inf"))
     if unsupported or any(t.dtype != torch.bfloat16 for t in (q, k, v)) or not _kernel_ok(q, k, v):
         _fallback("flash_attn_func", q, k, v)
         return _torch_attention(q, k, v, softmax_scale, causal)

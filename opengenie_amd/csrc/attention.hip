@@ -87,6 +87,13 @@ struct AttnArgs {
   int ksplit;
   float* part_o;
   float* part_ml;
+  // FP8 kernel only: V rewritten as [B, H, D, vt_npad] (k_fp8_v_transpose)
+  // and the [B, H] descales of q, k and v.
+  const uint8_t* vt;
+  int64_t vt_npad;
+  const float* q_ds;
+  const float* k_ds;
+  const float* v_ds;
 };
 
 OGA_DEVICE f32x16 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
@@ -509,6 +516,334 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
 }
 
+// ------------------------------------------------------- FP8 attention
+// FlashAttention-3's FP8 path, as the reference calls it with per-head e4m3
+// q, k, v and their [B, H] descales (official_ltx23_benchmark.py:3330-3340):
+//   S = (q8 . k8) * qd * kd * scale,  P = softmax(S) rounded to e4m3,
+//   O = (P8 . v8) * vd / l,  l the float32 row sum of P.
+// Both products run on v_mfma_f32_32x32x64_f8f6f4 (e4m3 x e4m3): per 64-key
+// step and wave, 2 key blocks x 2 d-steps of 64 for S^T and 4 d-blocks for
+// O^T, 8 MFMAs where the bf16 kernel issues 32.
+//
+// Operands (lane l, h = l / 32). S^T = K Q^T: A = K row 32j + l%32, bytes
+// 64s + 32h .. +31 of it; B = Q^T, the same bytes of query l%32, held in
+// registers. The accumulator layout, the masking and the online softmax are
+// the bf16 kernel's (lane l: query l%32, keys 8g + 4h + r of each 32-key
+// block). O^T = V^T P^T: B = P^T, lane l holding the e4m3 P of its own 32
+// keys kappa(h, s) = 32(s/16) + 8((s%16)/4) + 4h + s%4 in k-slot s, so P
+// stays in its lane; A = V^T, lane l needing V[kappa(h, s)][d] for d-row
+// 32 dblk + l%32. k_fp8_v_transpose first rewrites V as vt [B, H, D, npad]
+// with each 64-key step in slot order (position 32h + s of step t holds key
+// 64t + kappa(h, s), zero past the last key), so those 32 bytes are
+// contiguous in a d-row.
+//
+// LDS per step: the K tile (64 rows x 128 bytes) in the FP8 GEMM's slab
+// layout (two rows per 256-byte line, chunk c of row r at
+// (8(r%2) + c) ^ ((r/2)%8)) and the V^T tile (128 d-rows x 64 bytes, chunk c
+// of row d at c ^ ((d/4)%4)); three such 16 KiB pairs in a ring.
+constexpr int kF8Tile = kAK * kAD;  // bytes of a K or V^T tile: 8 KiB
+constexpr int kF8Pair = 2 * kF8Tile;
+constexpr int k8_off(int r, int c) { return (r >> 1) * 256 + (((r & 1) * 8 + c) ^ ((r >> 1) & 7)) * 16; }
+constexpr int vt_off(int d, int c) { return d * 64 + ((c ^ ((d >> 2) & 3)) << 4); }
+constexpr int kappa(int h, int slot) { return 32 * (slot >> 4) + 8 * ((slot & 15) >> 2) + 4 * h + (slot & 3); }
+// Each 16-lane group of a ds_read_b128 touches 64 distinct banks.
+constexpr bool f8_reads_conflict_free() {
+  for (int grp = 0; grp < 4; ++grp)
+    for (int j = 0; j < 2; ++j)
+      for (int s = 0; s < 2; ++s)
+        for (int q = 0; q < 2; ++q) {
+          unsigned long long kb = 0, vb = 0;
+          for (int l = 16 * grp; l < 16 * grp + 16; ++l) {
+            const int ql = l & 31, h = l >> 5;
+            const int bk = (k8_off(32 * j + ql, 4 * s + 2 * h + q) >> 2) & 63;
+            const int bv = (vt_off(32 * (2 * j + s) + ql, 2 * h + q) >> 2) & 63;
+            for (int i = 0; i < 4; ++i) {
+              if (((kb >> ((bk + i) & 63)) & 1ull) || ((vb >> ((bv + i) & 63)) & 1ull)) return false;
+              kb |= 1ull << ((bk + i) & 63);
+              vb |= 1ull << ((bv + i) & 63);
+            }
+          }
+        }
+  return true;
+}
+static_assert(f8_reads_conflict_free(), "FP8 attention fragment reads would conflict");
+// kappa is a bijection from (h, slot) onto the 64 keys of a step.
+constexpr bool kappa_is_bijective() {
+  unsigned long long seen = 0;
+  for (int h = 0; h < 2; ++h)
+    for (int sl = 0; sl < 32; ++sl) seen |= 1ull << kappa(h, sl);
+  return seen == ~0ull;
+}
+static_assert(kappa_is_bijective(), "slot order must cover every key of a step once");
+
+OGA_DEVICE f32x16 mfma_f8(const i32x8& a, const i32x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+template <int OFF>
+OGA_DEVICE i32x8 lds_b256(uint32_t a0, uint32_t a1) {
+  static_assert(OFF >= 0 && OFF < 65536, "LDS offset");
+  uint4 lo, hi;
+  asm volatile("ds_read_b128 %0, %2 offset:%4\n\tds_read_b128 %1, %3 offset:%4"
+               : "=v"(lo), "=v"(hi)
+               : "v"(a0), "v"(a1), "i"(OFF));
+  i32x8 r = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+  return r;
+}
+
+static_assert(kAW == 8, "the FP8 kernel's DMA gives each of 8 waves one 1 KiB instruction per tile");
+constexpr int kF8Lds = kABufs * kF8Pair > kAW * 8192 ? kABufs * kF8Pair : kAW * 8192;
+
+__global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attention_fp8(AttnArgs a) {
+  __shared__ uint4 smem[kF8Lds / 16];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  int64_t wg = blockIdx.x;
+  int part = -1;
+  if (wg < a.nfull) {
+    if (a.xcd_remap) wg = (wg & 7) * (a.nfull >> 3) + (wg >> 3);
+  } else {
+    const int64_t u = wg - a.nfull;
+    wg = a.nfull + u / a.ksplit;
+    part = (int)(u % a.ksplit);
+  }
+  const int qb = (int)(wg % a.nqb);
+  const int64_t bh = wg / a.nqb;
+  const int h = (int)(bh % a.heads);
+  const int64_t b = bh / a.heads;
+  const int64_t q0 = (int64_t)qb * kAQ + wv * 32;
+  const int hl = lane >> 5;
+  const int ql = lane & 31;
+  const float qd = a.q_ds[b * a.heads + h], kd = a.k_ds[b * a.heads + h], vd = a.v_ds[b * a.heads + h];
+  const float sl2 = a.scale_log2 * (qd * kd);
+
+  // Q^T fragments of d-steps 0, 1: bytes 64s + 32hl .. +31 of query q0 + ql.
+  i32x8 qf[2];
+  {
+    const int64_t qi = min(q0 + ql, a.nq - 1);
+    const uint8_t* qrow = (const uint8_t*)a.q + b * a.q_sb + qi * a.q_sn + (int64_t)h * a.q_sh;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const uint4 lo = *(const uint4*)(qrow + 64 * s + 32 * hl);
+      const uint4 hi = *(const uint4*)(qrow + 64 * s + 32 * hl + 16);
+      qf[s] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    }
+  }
+  const uint8_t* kbase = (const uint8_t*)a.k + b * a.k_sb + (int64_t)h * a.k_sh;
+  const uint8_t* vtbase = a.vt + (b * a.heads + h) * (int64_t)kAD * a.vt_npad;
+  const int64_t nsteps_all = (a.nk + kAK - 1) / kAK;
+  const int64_t st_begin = part < 0 ? 0 : nsteps_all * part / a.ksplit;
+  const int64_t st_end = part < 0 ? nsteps_all : nsteps_all * (part + 1) / a.ksplit;
+
+  f32x16 o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[i][e] = 0.0f;
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  // DMA: wave wv fills bytes [1024 wv, 1024 wv + 1024) of each tile. K: lane
+  // p writes line L = 4wv + p/16, position p%16, holding row 2L + v/8, chunk
+  // v%8 with v = (p%16) ^ (L%8). V^T: lane p writes d-row 16wv + p/4,
+  // position p%4, holding chunk (p%4) ^ ((d/4)%4) of the row.
+  const int kL = 4 * wv + (lane >> 4);
+  const int kv = (lane & 15) ^ (kL & 7);
+  const int krow = 2 * kL + (kv >> 3);
+  const uint32_t koff_c = (uint32_t)((kv & 7) * 16);
+  const int vd_row = 16 * wv + (lane >> 2);
+  const int64_t vt_src = vd_row * a.vt_npad + (((lane & 3) ^ ((vd_row >> 2) & 3)) * 16);
+  auto dma_step = [&](int64_t s2, uint4* dst) {
+    const int64_t key0 = s2 * kAK;
+    const int64_t r = min((int64_t)krow, a.nk - 1 - key0);
+    __builtin_amdgcn_global_load_lds((const void*)(kbase + (key0 + r) * a.k_sn + koff_c),
+                                     (lds_void*)(dst + wv * 64), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void*)(vtbase + key0 + vt_src),
+                                     (lds_void*)(dst + kF8Tile / 16 + wv * 64), 16, 0, 0);
+  };
+  dma_step(st_begin, smem);
+  if (kABufs == 3) dma_step(min(st_begin + 1, st_end - 1), smem + kF8Pair / 16);
+
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
+  uint32_t kaddr[2][2], vaddr[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int q = 0; q < 2; ++q) kaddr[s][q] = lds0 + k8_off(ql, 4 * s + 2 * hl + q);
+#pragma unroll
+  for (int q = 0; q < 2; ++q) vaddr[q] = lds0 + kF8Tile + vt_off(ql, 2 * hl + q);
+  const int hl4 = 4 * hl;
+
+  auto step = [&](auto par_c, int64_t st) {
+    constexpr int PAR = decltype(par_c)::value;
+    constexpr int KB = PAR * kF8Pair;
+    // This wave's two DMA instructions of step st have landed (those of
+    // step st + 1 may still be in flight), then every wave's.
+    if (kABufs == 3)
+      asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+    {
+      constexpr int NP = (PAR + kABufs - 1) % kABufs;
+      if (kABufs == 3)
+        dma_step(min(st + 2, st_end - 1), smem + NP * (kF8Pair / 16));
+      else if (st + 1 < st_end)
+        dma_step(st + 1, smem + NP * (kF8Pair / 16));
+    }
+    f32x16 sacc[2];
+    auto s_block = [&](auto j_c) {
+      constexpr int J = decltype(j_c)::value;
+      i32x8 kf0 = lds_b256<KB + 4096 * J>(kaddr[0][0], kaddr[0][1]);
+      i32x8 kf1 = lds_b256<KB + 4096 * J>(kaddr[1][0], kaddr[1][1]);
+      OGA_LGKM(0, "+v"(kf0), "+v"(kf1));
+      f32x16 acc;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+      acc = mfma_f8(kf0, qf[0], acc);
+      return mfma_f8(kf1, qf[1], acc);
+    };
+    sacc[0] = s_block(IC<0>{});
+    sacc[1] = s_block(IC<1>{});
+    // V^T fragments of the four d-blocks, in flight under the softmax.
+    i32x8 vf[4];
+    vf[0] = lds_b256<KB + 0 * 2048>(vaddr[0], vaddr[1]);
+    vf[1] = lds_b256<KB + 1 * 2048>(vaddr[0], vaddr[1]);
+    vf[2] = lds_b256<KB + 2 * 2048>(vaddr[0], vaddr[1]);
+    vf[3] = lds_b256<KB + 3 * 2048>(vaddr[0], vaddr[1]);
+
+    const int64_t rem64 = a.nk - st * kAK;
+    if (rem64 < kAK) {
+      const int remh = (int)rem64 - hl4;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          if (32 * j + 8 * (e >> 2) + (e & 3) >= remh) sacc[j][e] = -INFINITY;
+    }
+    float mx = sacc[0][0];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = (j == 0 ? 1 : 0); e < 16; ++e) mx = __builtin_fmaxf(mx, sacc[j][e]);
+    const float ms = max_halves(mx) * sl2;
+    if (__any(ms > m_run + 8.0f)) {
+      const float m_new = __builtin_fmaxf(m_run, ms);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+      m_run = m_new;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
+    }
+    // P = 2^(s sl2 - m_run) <= 2^8: float32 into l, e4m3 (nearest even) into
+    // the B operand, byte 16j + e = P of accumulator e of block j.
+    const float nm = -m_run;
+    i32x8 pf;
+    float ps0 = 0.0f, ps1 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; e += 4) {
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j][e], sl2, nm));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j][e + 1], sl2, nm));
+        const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j][e + 2], sl2, nm));
+        const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j][e + 3], sl2, nm));
+        ps0 += p0 + p2;
+        ps1 += p1 + p3;
+        pf[4 * j + (e >> 2)] = (int)e4m3x4(p0, p1, p2, p3);
+      }
+    l_run += ps0 + ps1;
+    OGA_LGKM(0, "+v"(vf[0]), "+v"(vf[1]), "+v"(vf[2]), "+v"(vf[3]));
+#pragma unroll
+    for (int dblk = 0; dblk < 4; ++dblk) o[dblk] = mfma_f8(vf[dblk], pf, o[dblk]);
+  };
+
+  for (int64_t st = st_begin; st < st_end; st += kABufs) {
+    step(IC<0>{}, st);
+    if (st + 1 < st_end) step(IC<1>{}, st + 1);
+    if constexpr (kABufs == 3)
+      if (st + 2 < st_end) step(IC<2 % kABufs>{}, st + 2);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  if (part >= 0) {
+    const int64_t row = (int64_t)(blockIdx.x - a.nfull) * kAQ + wv * 32 + ql;
+    float* po = a.part_o + row * kAD;
+#pragma unroll
+    for (int dblk = 0; dblk < 4; ++dblk)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *(float4*)(po + 32 * dblk + 8 * g + 4 * hl) = make_float4(o[dblk][4 * g] * vd, o[dblk][4 * g + 1] * vd,
+                                                                  o[dblk][4 * g + 2] * vd, o[dblk][4 * g + 3] * vd);
+    const float l_tot = sum_halves(l_run);
+    if (hl == 0) *(float2*)(a.part_ml + 2 * row) = make_float2(m_run, l_tot);
+    return;
+  }
+  const float inv = vd / sum_halves(l_run);
+  __syncthreads();
+  char* const otile = (char*)smem + wv * 8192;
+#pragma unroll
+  for (int dblk = 0; dblk < 4; ++dblk)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      uint2 w;
+      w.x = pack2(o[dblk][4 * g] * inv, o[dblk][4 * g + 1] * inv);
+      w.y = pack2(o[dblk][4 * g + 2] * inv, o[dblk][4 * g + 3] * inv);
+      *(uint2*)(otile + ql * 256 + (((4 * dblk + g) ^ (ql & 15)) << 4) + 8 * hl) = w;
+    }
+  __syncthreads();
+  const int oc = lane & 15;
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int r = 4 * it + (lane >> 4);
+    const uint4 w = *(const uint4*)(otile + r * 256 + ((oc ^ (r & 15)) << 4));
+    const int64_t qr = q0 + r;
+    if (qr < a.nq) *(uint4*)(a.o + b * a.o_sb + qr * a.o_sn + (int64_t)h * a.o_sh + 8 * oc) = w;
+  }
+}
+
+// vt[b, h, d, 64t + 32h' + s] = v[b, 64t + kappa(h', s), h, d] (zero for keys
+// past nk): one workgroup per (64-key step t, head, batch) stages the 64 x
+// 128-byte tile in LDS (rows padded to 144 bytes) and writes the 128 d-rows
+// of 64 bytes in slot order.
+__global__ __launch_bounds__(256) void k_fp8_v_transpose(const uint8_t* v, int64_t v_sb, int64_t v_sn, int64_t v_sh,
+                                                         uint8_t* vt, int64_t nk, int64_t npad, int heads) {
+  constexpr int kPitch = kAD + 16;
+  __shared__ uint8_t tile[kAK * kPitch];
+  const int64_t t = blockIdx.x;
+  const int h = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const int64_t key0 = t * kAK;
+  const uint8_t* src = v + b * v_sb + (int64_t)h * v_sh;
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int i = threadIdx.x + 256 * it;  // 512 chunks of 16 bytes
+    const int r = i >> 3, c = i & 7;
+    uint4 val = {0u, 0u, 0u, 0u};
+    if (key0 + r < nk) val = *(const uint4*)(src + (key0 + r) * v_sn + 16 * c);
+    *(uint4*)(tile + r * kPitch + 16 * c) = val;
+  }
+  __syncthreads();
+  uint8_t* dst = vt + ((b * heads + h) * (int64_t)kAD) * npad + key0;
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int i = threadIdx.x + 256 * it;  // 128 d-rows x 4 chunks of 16 positions
+    const int d = i >> 2, c = i & 3;
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t x = 0;
+#pragma unroll
+      for (int bb = 0; bb < 4; ++bb) {
+        const int pos = 16 * c + 4 * k + bb;
+        x |= (uint32_t)tile[kappa(pos >> 5, pos & 31) * kPitch + d] << (8 * bb);
+      }
+      w[k] = x;
+    }
+    *(uint4*)(dst + (int64_t)d * npad + 16 * c) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 // The split blocks' parts merged: for query row r of split block sb (block
 // nfull + sb), with parts p of running max m_p and sum l_p,
 // O = sum_p 2^(m_p - M) O_p / sum_p 2^(m_p - M) l_p, M = max_p m_p. One
@@ -599,18 +934,19 @@ namespace {
 // Workgroups of k_attention resident at once on the current device (CUs x
 // workgroups per CU), cached per device (relaxed atomics: threads filling an
 // entry at once store the same value); 0 if the runtime cannot say.
-int64_t attention_slots() {
-  static std::atomic<int64_t> cache[64];
+int64_t attention_slots(bool fp8 = false) {
+  static std::atomic<int64_t> cache[2][64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  int64_t n = cache[dev].load(std::memory_order_relaxed);
+  int64_t n = cache[fp8][dev].load(std::memory_order_relaxed);
   if (n == 0) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_attention, 64 * kAW, 0) != hipSuccess)
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fp8 ? k_attention_fp8 : k_attention, 64 * kAW, 0) !=
+            hipSuccess)
       return 0;
     n = (int64_t)cus * per_cu > 0 ? (int64_t)cus * per_cu : -1;
-    cache[dev].store(n, std::memory_order_relaxed);
+    cache[fp8][dev].store(n, std::memory_order_relaxed);
   }
   return n > 0 ? n : 0;
 }
@@ -687,6 +1023,73 @@ int attention_run(const void* q, const int64_t q_strides[3], const void* k, cons
   }
   return launch_status();
 }
+
+// FP8 attention: the V rewrite (vt, ceil(nk/64)*64 keys per d-row) at the
+// start of the workspace, then the split parts' partials when the workspace
+// also holds them.
+int64_t vt_bytes(int64_t batch, int64_t heads, int64_t nk) {
+  const int64_t npad = (nk + kAK - 1) / kAK * kAK;
+  return (batch * heads * kAD * npad + 255) / 256 * 256;
+}
+
+int attention_fp8_run(const void* q, const int64_t q_strides[3], const void* k, const int64_t k_strides[3],
+                      const void* v, const int64_t v_strides[3], const float* q_descale, const float* k_descale,
+                      const float* v_descale, void* o, const int64_t o_strides[3], int64_t batch, int64_t nq,
+                      int64_t nk, int64_t heads, int64_t head_dim, float softmax_scale, void* workspace,
+                      int64_t workspace_bytes, void* stream) {
+  if (!q || !k || !v || !o || !q_strides || !k_strides || !v_strides || !o_strides) return fail("null pointer");
+  if (!q_descale || !k_descale || !v_descale) return fail("null descale");
+  if (head_dim != kAD) return unsupported("head_dim must be %d", kAD);
+  if (batch < 0 || nq < 0 || nk < 0 || heads < 0) return fail("bad shape");
+  if (batch == 0 || nq == 0 || heads == 0) return OGA_OK;
+  if (nk == 0) return unsupported("no keys");
+  if (heads > 65535 || batch > 65535) return unsupported("batch and heads must be below 65536");
+  for (const int64_t* st : {q_strides, k_strides, v_strides})
+    for (int i = 0; i < 3; ++i)
+      if (st[i] % 16) return fail("e4m3 strides must be multiples of 16 elements");
+  for (int i = 0; i < 3; ++i)
+    if (o_strides[i] % 8) return fail("output strides must be multiples of 8 elements");
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(o, 16))
+    return fail("q/k/v/o must be 16-byte aligned");
+  if (!(softmax_scale > 0.0f) || !__builtin_isfinite(softmax_scale)) return unsupported("softmax_scale must be positive");
+  const int64_t vtb = vt_bytes(batch, heads, nk);
+  if (!workspace || workspace_bytes < vtb) return fail("workspace smaller than oga_attention_fp8_workspace_bytes");
+  if (!aligned(workspace, 256)) return fail("workspace must be 256-byte aligned");
+  AttnArgs a{};
+  a.q = q; a.k = k; a.v = v; a.o = (uint16_t*)o;
+  a.q_sb = q_strides[0]; a.q_sn = q_strides[1]; a.q_sh = q_strides[2];
+  a.k_sb = k_strides[0]; a.k_sn = k_strides[1]; a.k_sh = k_strides[2];
+  a.v_sb = v_strides[0]; a.v_sn = v_strides[1]; a.v_sh = v_strides[2];
+  a.o_sb = o_strides[0]; a.o_sn = o_strides[1]; a.o_sh = o_strides[2];
+  a.nq = nq; a.nk = nk; a.heads = (int)heads;
+  a.scale_log2 = softmax_scale * 1.4426950408889634f;
+  a.vt = (const uint8_t*)workspace;
+  a.vt_npad = (nk + kAK - 1) / kAK * kAK;
+  a.q_ds = q_descale; a.k_ds = k_descale; a.v_ds = v_descale;
+  const int64_t nqb = (nq + kAQ - 1) / kAQ;
+  const int64_t wgs = nqb * heads * batch;
+  if (nqb > INT32_MAX || wgs > UINT32_MAX / 8) return unsupported("too many query blocks");
+  a.nqb = (int)nqb;
+  AttnPlan plan = attention_plan(wgs, nk, attention_slots(true));
+  if (vtb + attention_ws_bytes(plan) > workspace_bytes) plan = AttnPlan{wgs, wgs, 0, 1};
+  a.nfull = plan.nfull;
+  a.ksplit = plan.ksplit;
+  a.part_o = plan.units ? (float*)((char*)workspace + vtb) : nullptr;
+  a.part_ml = plan.units ? a.part_o + plan.units * kAQ * kAD : nullptr;
+  a.xcd_remap = plan.nfull % 8 == 0;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_fp8_v_transpose, dim3((unsigned)(a.vt_npad / kAK), (unsigned)heads, (unsigned)batch), dim3(256),
+                     0, st, (const uint8_t*)v, a.v_sb, a.v_sn, a.v_sh, (uint8_t*)workspace, nk, a.vt_npad, (int)heads);
+  int rc = launch_status();
+  if (rc) return rc;
+  hipLaunchKernelGGL(k_attention_fp8, dim3((unsigned)(plan.nfull + plan.units)), dim3(64 * kAW), 0, st, a);
+  if (plan.units) {
+    const int64_t rows = (wgs - plan.nfull) * kAQ;
+    hipLaunchKernelGGL(k_attention_combine, dim3((unsigned)((rows * (kAD / 8) + 255) / 256)), dim3(256), 0, st, a,
+                       rows);
+  }
+  return launch_status();
+}
 }  // namespace
 
 extern "C" int oga_attention(const void* q, const int64_t q_strides[3], const void* k, const int64_t k_strides[3],
@@ -711,4 +1114,22 @@ extern "C" int oga_attention_ws(const void* q, const int64_t q_strides[3], const
                                 float softmax_scale, void* workspace, int64_t workspace_bytes, void* stream) {
   return attention_run(q, q_strides, k, k_strides, v, v_strides, o, o_strides, batch, nq, nk, heads, head_dim,
                        softmax_scale, workspace, workspace_bytes, stream);
+}
+
+extern "C" int64_t oga_attention_fp8_workspace_bytes(int64_t batch, int64_t nq, int64_t nk, int64_t heads,
+                                                     int64_t head_dim) {
+  if (batch <= 0 || nq <= 0 || nk <= 0 || heads <= 0 || head_dim != kAD) return 0;
+  const int64_t nqb = (nq + kAQ - 1) / kAQ;
+  if (nqb > INT32_MAX || heads > 65535 || batch > 65535) return 0;
+  return vt_bytes(batch, heads, nk) + attention_ws_bytes(attention_plan(nqb * heads * batch, nk, attention_slots(true)));
+}
+
+extern "C" int oga_attention_fp8_ws(const void* q8, const int64_t q_strides[3], const void* k8,
+                                    const int64_t k_strides[3], const void* v8, const int64_t v_strides[3],
+                                    const float* q_descale, const float* k_descale, const float* v_descale, void* o,
+                                    const int64_t o_strides[3], int64_t batch, int64_t nq, int64_t nk, int64_t heads,
+                                    int64_t head_dim, float softmax_scale, void* workspace, int64_t workspace_bytes,
+                                    void* stream) {
+  return attention_fp8_run(q8, q_strides, k8, k_strides, v8, v_strides, q_descale, k_descale, v_descale, o, o_strides,
+                           batch, nq, nk, heads, head_dim, softmax_scale, workspace, workspace_bytes, stream);
 }

@@ -91,3 +91,14 @@ def test_attention_barriers_wait_for_lds_dma():
     assert n_barriers >= 2
     assert any("load_lds" in ins for ins in body)
     assert barrier_violations(body, max_vmcnt=4) == []
+
+
+@pytest.mark.skipif(not os.path.exists("/opt/rocm/bin/hipcc") and not os.environ.get("HIPCC"),
+                    reason="hipcc not present")
+def test_fp8_attention_barriers_wait_for_lds_dma():
+    """The FP8 kernel sends two DMA instructions per wave and step (the K
+    tile and the V^T tile), so the wait may leave the next step's two in flight."""
+    body = _kernel_body(_device_asm(os.path.join(CSRC, "attention.hip")), "k_attention_fp8")
+    assert sum(1 for ins in body if ins == "s_barrier") >= 2
+    assert any("load_lds" in ins for ins in body)
+    assert barrier_violations(body, max_vmcnt=2) == []
