@@ -6,16 +6,18 @@
 // (benchmarks/official_ltx23_benchmark.py:3294-3369; FlashAttention3.__call__
 // of ltx_core), with softmax scale D^-0.5:
 //   O[b, n, h] = sum_m softmax_m(q[b,n,h] . k[b,m,h] * scale) v[b,m,h].
-// FP8 inputs (e4m3 with per-(b, h) descales, :3333-3340) go through
-// oga_fp8_dequant_per_head first: each value times its float32 descale,
-// rounded to bf16 (FA3 computes in FP8 directly; the reference benchmark
-// checks the FP8 result against the bf16 one within a tolerance,
-// video_self_attention_bench.py:288-305, and so do the tests here).
+// FP8 inputs (e4m3 with per-(b, h) descales, :3330-3340) run k_attention_fp8
+// below, both products on e4m3 MFMA as FlashAttention-3's FP8 path does (the
+// reference benchmark checks the FP8 result against the bf16 one within a
+// tolerance, video_self_attention_bench.py:288-305, and so do the tests
+// here); oga_fp8_dequant_per_head (each value times its float32 descale,
+// rounded to bf16) serves e4m3 inputs that kernel does not take.
 //
-// Work decomposition. A workgroup of 4 waves owns 128 queries of one (b, h);
-// wave w owns queries 32w .. 32w+31. Keys are visited 64 at a time; the K
-// and V tiles of a step (64 x 128 bf16 each) are copied to LDS by DMA
-// (global_load_lds_dwordx4), two steps in flight.
+// Work decomposition. A workgroup of kAW waves (8) owns 32 kAW queries of one
+// (b, h); wave w owns queries 32w .. 32w+31. Keys are visited 64 at a time;
+// the K and V tiles of a step (64 x 128 bf16 each) are copied to LDS by DMA
+// (global_load_lds_dwordx4) into a ring of kABufs (3) tile pairs, two steps
+// in flight.
 //
 // Per step and wave, with v_mfma_f32_32x32x16_bf16:
 //  * S^T = K Q^T as two 32-key x 32-query blocks (8 MFMAs each over d):
