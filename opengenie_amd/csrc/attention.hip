@@ -593,7 +593,9 @@ OGA_DEVICE i32x8 lds_b256(uint32_t a0, uint32_t a1) {
 }
 
 static_assert(kAW == 8, "the FP8 kernel's DMA gives each of 8 waves one 1 KiB instruction per tile");
-constexpr int kF8Lds = kABufs * kF8Pair > kAW * 8192 ? kABufs * kF8Pair : kAW * 8192;
+constexpr int kF8Bufs = kABufs;  // K/V^T tile pairs in the FP8 kernel's ring
+constexpr int kF8Lds = kF8Bufs * kF8Pair > kAW * 8192 ? kF8Bufs * kF8Pair : kAW * 8192;
+static_assert(kF8Lds <= 65536, "the FP8 fragment reads address LDS with 16-bit offsets");
 
 __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attention_fp8(AttnArgs a) {
   __shared__ uint4 smem[kF8Lds / 16];
@@ -662,7 +664,7 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
                                      (lds_void*)(dst + kF8Tile / 16 + wv * 64), 16, 0, 0);
   };
   dma_step(st_begin, smem);
-  if (kABufs == 3) dma_step(min(st_begin + 1, st_end - 1), smem + kF8Pair / 16);
+  if (kF8Bufs == 3) dma_step(min(st_begin + 1, st_end - 1), smem + kF8Pair / 16);
 
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
   uint32_t kaddr[2][2], vaddr[2];
@@ -674,24 +676,9 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
   for (int q = 0; q < 2; ++q) vaddr[q] = lds0 + kF8Tile + vt_off(ql, 2 * hl + q);
   const int hl4 = 4 * hl;
 
-  auto step = [&](auto par_c, int64_t st) {
-    constexpr int PAR = decltype(par_c)::value;
-    constexpr int KB = PAR * kF8Pair;
-    // This wave's two DMA instructions of step st have landed (those of
-    // step st + 1 may still be in flight), then every wave's.
-    if (kABufs == 3)
-      asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    asm volatile("s_barrier" ::: "memory");
-    {
-      constexpr int NP = (PAR + kABufs - 1) % kABufs;
-      if (kABufs == 3)
-        dma_step(min(st + 2, st_end - 1), smem + NP * (kF8Pair / 16));
-      else if (st + 1 < st_end)
-        dma_step(st + 1, smem + NP * (kF8Pair / 16));
-    }
-    f32x16 sacc[2];
+  // S^T of the step in pair PAR: two 32-key blocks, two d-steps each.
+  auto s_phase = [&](auto par_c, f32x16(&sacc)[2]) {
+    constexpr int KB = decltype(par_c)::value * kF8Pair;
     auto s_block = [&](auto j_c) {
       constexpr int J = decltype(j_c)::value;
       i32x8 kf0 = lds_b256<KB + 4096 * J>(kaddr[0][0], kaddr[0][1]);
@@ -705,13 +692,20 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
     };
     sacc[0] = s_block(IC<0>{});
     sacc[1] = s_block(IC<1>{});
-    // V^T fragments of the four d-blocks, in flight under the softmax.
-    i32x8 vf[4];
+  };
+  // V^T fragments of the four d-blocks of pair PAR (waited for in pv).
+  auto v_read = [&](auto par_c, i32x8(&vf)[4]) {
+    constexpr int KB = decltype(par_c)::value * kF8Pair;
     vf[0] = lds_b256<KB + 0 * 2048>(vaddr[0], vaddr[1]);
     vf[1] = lds_b256<KB + 1 * 2048>(vaddr[0], vaddr[1]);
     vf[2] = lds_b256<KB + 2 * 2048>(vaddr[0], vaddr[1]);
     vf[3] = lds_b256<KB + 3 * 2048>(vaddr[0], vaddr[1]);
-
+  };
+  // Online softmax of step st: masking past the last key, the running max
+  // (O and l rescaled when it grows by more than 2^8), P = 2^(s sl2 - m)
+  // <= 2^8 in float32 into l and as e4m3 (nearest even) into the B operand,
+  // byte 16j + e = P of accumulator e of block j.
+  auto softmax = [&](int64_t st, f32x16(&sacc)[2], i32x8& pf) {
     const int64_t rem64 = a.nk - st * kAK;
     if (rem64 < kAK) {
       const int remh = (int)rem64 - hl4;
@@ -737,10 +731,7 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
     }
-    // P = 2^(s sl2 - m_run) <= 2^8: float32 into l, e4m3 (nearest even) into
-    // the B operand, byte 16j + e = P of accumulator e of block j.
     const float nm = -m_run;
-    i32x8 pf;
     float ps0 = 0.0f, ps1 = 0.0f;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -755,16 +746,43 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
         pf[4 * j + (e >> 2)] = (int)e4m3x4(p0, p1, p2, p3);
       }
     l_run += ps0 + ps1;
+  };
+  auto pv = [&](i32x8(&vf)[4], const i32x8& pf) {
     OGA_LGKM(0, "+v"(vf[0]), "+v"(vf[1]), "+v"(vf[2]), "+v"(vf[3]));
 #pragma unroll
     for (int dblk = 0; dblk < 4; ++dblk) o[dblk] = mfma_f8(vf[dblk], pf, o[dblk]);
   };
 
-  for (int64_t st = st_begin; st < st_end; st += kABufs) {
+  auto step = [&](auto par_c, int64_t st) {
+    constexpr int PAR = decltype(par_c)::value;
+    // This wave's two DMA instructions of step st have landed (those of
+    // step st + 1 may still be in flight), then every wave's.
+    if (kF8Bufs == 3)
+      asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+    {
+      constexpr int NP = (PAR + kF8Bufs - 1) % kF8Bufs;
+      if (kF8Bufs == 3)
+        dma_step(min(st + 2, st_end - 1), smem + NP * (kF8Pair / 16));
+      else if (st + 1 < st_end)
+        dma_step(st + 1, smem + NP * (kF8Pair / 16));
+    }
+    f32x16 sacc[2];
+    i32x8 vf[4], pf;
+    s_phase(par_c, sacc);
+    // V^T fragments in flight under the softmax.
+    v_read(par_c, vf);
+    softmax(st, sacc, pf);
+    pv(vf, pf);
+  };
+
+  for (int64_t st = st_begin; st < st_end; st += kF8Bufs) {
     step(IC<0>{}, st);
     if (st + 1 < st_end) step(IC<1>{}, st + 1);
-    if constexpr (kABufs == 3)
-      if (st + 2 < st_end) step(IC<2 % kABufs>{}, st + 2);
+    if constexpr (kF8Bufs == 3)
+      if (st + 2 < st_end) step(IC<2 % kF8Bufs>{}, st + 2);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
