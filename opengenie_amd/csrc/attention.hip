@@ -230,8 +230,11 @@ OGA_DEVICE float sum_halves(float v) {
 // st % kABufs, and the DMA of step st + kABufs - 1 goes out during step st.
 constexpr int kKBuf = 0, kVBuf = 16384, kParBytes = 32768;
 
+constexpr int kBfBufs = kABufs;  // K/V tile pairs in the bf16 kernel's ring
+static_assert(2 * kBfBufs * kATileU4 * 16 <= 160 * 1024, "LDS budget");
+
 __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attention(AttnArgs a) {
-  __shared__ uint4 smem[2 * kABufs * kATileU4];
+  __shared__ uint4 smem[2 * kBfBufs * kATileU4];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   // Workgroups go to the 8 XCDs round-robin. With the remap, XCD x runs a
@@ -300,7 +303,7 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
   // into a pair no later step reads, so that exactly one tile's DMA is sent
   // after each step's own.
   dma_step(st_begin, smem, smem + kATileU4);
-  if (kABufs == 3) dma_step(min(st_begin + 1, st_end - 1), smem + 2 * kATileU4, smem + 3 * kATileU4);
+  if (kBfBufs == 3) dma_step(min(st_begin + 1, st_end - 1), smem + 2 * kATileU4, smem + 3 * kATileU4);
 
   // LDS read addresses (tile_off with the swizzle folded per lane):
   //  K fragment (key row 32j + ql, d = 16s + 8hl): kaddr[s] + 8192 j;
@@ -323,34 +326,10 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
   // Key offset of accumulator e within a 32-key block, minus this lane's 4 hl.
   const int hl4 = 4 * hl;
 
-  auto step = [&](auto par_c, int64_t st) {
-    constexpr int PAR = decltype(par_c)::value;
-    constexpr int KB = PAR * kParBytes + kKBuf;
-    constexpr int VB = PAR * kParBytes;  // vaddr already includes kVBuf
-    // This wave's DMA of step st has landed (with three pairs, the one DMA
-    // sent after it, of step st + 1, may stay in flight), then every wave's;
-    // every wave has also finished step st - 1, so its pair is free for the
-    // DMA of step st + kABufs - 1. The wait is explicit because the
-    // barrier's workgroup fence does not wait for loads, and the LDS reads
-    // below are inline assembly the compiler does not order after the DMA.
-    if (kABufs == 3)
-      asm volatile("s_waitcnt vmcnt(%0)" ::"i"(2 * kADmaI) : "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    // A bare barrier: __syncthreads()'s fence would add a vmcnt(0) (draining
-    // the DMA sent ahead); this wave's LDS reads of step st - 1 completed at
-    // that step's end (lgkmcnt(0)), and it writes LDS only by DMA.
-    asm volatile("s_barrier" ::: "memory");
-    {
-      constexpr int NP = (PAR + kABufs - 1) % kABufs;  // pair of step st + kABufs - 1
-      if (kABufs == 3)
-        dma_step(min(st + 2, st_end - 1), smem + 2 * NP * kATileU4, smem + (2 * NP + 1) * kATileU4);
-      else if (st + 1 < st_end)
-        dma_step(st + 1, smem + 2 * NP * kATileU4, smem + (2 * NP + 1) * kATileU4);
-    }
-
-    // S^T blocks: key block j (keys 32j .. 32j+31) x the wave's 32 queries.
-    f32x16 sacc[2];
+  // S^T blocks of the step in pair PAR: key block j (keys 32j .. 32j+31) x
+  // the wave's 32 queries.
+  auto s_phase = [&](auto par_c, f32x16(&sacc)[2]) {
+    constexpr int KB = decltype(par_c)::value * kParBytes + kKBuf;
     auto s_block = [&](auto j_c) {
       constexpr int OFF = KB + 8192 * decltype(j_c)::value;
       bf16x8 kf[8];
@@ -373,23 +352,27 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
     };
     sacc[0] = s_block(IC<0>{});
     sacc[1] = s_block(IC<1>{});
-    // V^T fragments of 16-key chunk C (4 d-blocks x 2 transposing reads).
-    auto read_v = [&](auto c_c, u32x2(&vr)[8]) {
-      constexpr int C = decltype(c_c)::value;
-      constexpr int OFF = VB + 4096 * C;
-      vr[0] = lds_tr16<OFF>(vaddr[0][0]);
-      vr[1] = lds_tr16<OFF + 2048>(vaddr[0][1]);
-      vr[2] = lds_tr16<OFF>(vaddr[1][0]);
-      vr[3] = lds_tr16<OFF + 2048>(vaddr[1][1]);
-      vr[4] = lds_tr16<OFF>(vaddr[2][0]);
-      vr[5] = lds_tr16<OFF + 2048>(vaddr[2][1]);
-      vr[6] = lds_tr16<OFF>(vaddr[3][0]);
-      vr[7] = lds_tr16<OFF + 2048>(vaddr[3][1]);
-    };
-    u32x2 vr0[8], vr1[8];
-    read_v(IC<0>{}, vr0);  // in flight under the softmax
-
-    // Keys past nk (last step only) get score -inf.
+  };
+  // V^T fragments of 16-key chunk C of pair PAR (4 d-blocks x 2 transposing
+  // reads).
+  auto read_v = [&](auto par_c, auto c_c, u32x2(&vr)[8]) {
+    constexpr int C = decltype(c_c)::value;
+    constexpr int OFF = decltype(par_c)::value * kParBytes + 4096 * C;  // vaddr includes kVBuf
+    vr[0] = lds_tr16<OFF>(vaddr[0][0]);
+    vr[1] = lds_tr16<OFF + 2048>(vaddr[0][1]);
+    vr[2] = lds_tr16<OFF>(vaddr[1][0]);
+    vr[3] = lds_tr16<OFF + 2048>(vaddr[1][1]);
+    vr[4] = lds_tr16<OFF>(vaddr[2][0]);
+    vr[5] = lds_tr16<OFF + 2048>(vaddr[2][1]);
+    vr[6] = lds_tr16<OFF>(vaddr[3][0]);
+    vr[7] = lds_tr16<OFF + 2048>(vaddr[3][1]);
+  };
+  // Online softmax of step st: keys past nk get score -inf; the running max
+  // moves lazily (only when some query of the wave sees a score more than 8
+  // above it, always on the first step), so P = 2^(s scale_log2 - m_run) <=
+  // 256 and O, l are rescaled rarely. The float32 P feed l, their bf16
+  // roundings the P.V product (as FlashAttention does).
+  auto softmax = [&](int64_t st, f32x16(&sacc)[2], uint32_t(&pb)[2][8]) {
     const int64_t rem64 = a.nk - st * kAK;
     if (rem64 < kAK) {
       const int remh = (int)rem64 - hl4;
@@ -406,9 +389,6 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
       for (int e = (j == 0 ? 1 : 0); e < 16; ++e) mx = __builtin_fmaxf(mx, sacc[j][e]);
     // Base-2 scores s * scale_log2 (scale_log2 > 0, so the max commutes).
     const float ms = max_halves(mx) * a.scale_log2;
-    // Lazy rescaling: m_run moves only when some query of the wave sees a
-    // score more than 8 above it (always on the first step), so
-    // P = 2^(s - m_run) <= 256 and O, l are rescaled rarely.
     if (__any(ms > m_run + 8.0f)) {
       const float m_new = __builtin_fmaxf(m_run, ms);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first step (m_run = -inf)
@@ -419,10 +399,7 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
     }
-    // P = 2^(s scale_log2 - m_run): the float32 values feed l, their bf16
-    // roundings feed the P.V product (as FlashAttention does).
     const float nm = -m_run;
-    uint32_t pb[2][8];
     float ps0 = 0.0f, ps1 = 0.0f;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -435,13 +412,16 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
         pb[j][e >> 1] = pack2(p0, p1);
       }
     l_run += ps0 + ps1;
-
-    // O^T += V^T P^T over 16-key chunks c2 (keys 16 c2 .. 16 c2 + 15); the
-    // next chunk's V^T reads go out before this chunk's MFMAs.
+  };
+  // O^T += V^T P^T over the 16-key chunks c2 (keys 16 c2 .. 16 c2 + 15) of
+  // pair PAR, chunk 0's V^T fragments already read into vr0; each next
+  // chunk's reads go out before this chunk's MFMAs.
+  auto pv_phase = [&](auto par_c, const uint32_t(&pb)[2][8], u32x2(&vr0)[8]) {
+    u32x2 vr1[8];
     auto pv = [&](auto c_c, u32x2(&cur)[8], u32x2(&nxt)[8]) {
       constexpr int C = decltype(c_c)::value;
       if constexpr (C + 1 < 4) {
-        read_v(IC<C + 1>{}, nxt);
+        read_v(par_c, IC<C + 1>{}, nxt);
         OGA_LGKM(8, "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3]), "+v"(cur[4]), "+v"(cur[5]),
                  "+v"(cur[6]), "+v"(cur[7]));
       } else {
@@ -463,12 +443,45 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
     pv(IC<2>{}, vr0, vr1);
     pv(IC<3>{}, vr1, vr0);
   };
+  // Wait until this wave's DMA of step st has landed (with three pairs, the
+  // one DMA sent after it, of step st + 1, may stay in flight), join the
+  // barrier (every wave's DMA of step st landed, every wave is past its last
+  // read of the pair the next DMA fills) and send the DMA of step st + 2
+  // (st + 1 with two pairs). The wait is explicit because the
+  // barrier's workgroup fence does not wait for loads, and the LDS reads are
+  // inline assembly the compiler does not order after the DMA; the barrier
+  // is bare because __syncthreads()'s fence would add a vmcnt(0) (draining
+  // the DMA sent ahead).
+  auto bar_dma = [&](auto par_c, int64_t st) {
+    constexpr int PAR = decltype(par_c)::value;
+    if (kBfBufs == 3)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"i"(2 * kADmaI) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+    constexpr int NP = (PAR + kBfBufs - 1) % kBfBufs;  // pair of step st + kBfBufs - 1
+    if (kBfBufs == 3)
+      dma_step(min(st + 2, st_end - 1), smem + 2 * NP * kATileU4, smem + (2 * NP + 1) * kATileU4);
+    else if (st + 1 < st_end)
+      dma_step(st + 1, smem + 2 * NP * kATileU4, smem + (2 * NP + 1) * kATileU4);
+  };
 
-  for (int64_t st = st_begin; st < st_end; st += kABufs) {
+  auto step = [&](auto par_c, int64_t st) {
+    bar_dma(par_c, st);
+    f32x16 sacc[2];
+    uint32_t pb[2][8];
+    u32x2 vr0[8];
+    s_phase(par_c, sacc);
+    read_v(par_c, IC<0>{}, vr0);  // in flight under the softmax
+    softmax(st, sacc, pb);
+    pv_phase(par_c, pb, vr0);
+  };
+
+  for (int64_t st = st_begin; st < st_end; st += kBfBufs) {
     step(IC<0>{}, st);
     if (st + 1 < st_end) step(IC<1>{}, st + 1);
-    if constexpr (kABufs == 3)
-      if (st + 2 < st_end) step(IC<2 % kABufs>{}, st + 2);
+    if constexpr (kBfBufs == 3)
+      if (st + 2 < st_end) step(IC<2 % kBfBufs>{}, st + 2);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the re-reads past the last step
 
