@@ -199,6 +199,12 @@ def fused_op_rows(seed: int) -> dict:
     fn = lambda: L.fused_fp8_quantize_e4m3(xq, sq)  # noqa: E731
     rec("fp8_quantize_e4m3", M * K * 3, _graph_time_us(fn), "x(9216,4096)", fn)
 
+    # GELU-tanh quantizer on the FFN hidden (9216, 16384): the down-projection's input.
+    xh = (torch.randn((M, 4 * K), generator=g, device=dev) * 2.0).to(torch.bfloat16)
+    fn = lambda: L.fused_gelu_tanh_fp8_quantize_e4m3(xh, sq)  # noqa: E731
+    rec("gelu_tanh_fp8_quantize_e4m3", M * 4 * K * 3, _graph_time_us(fn, inner=10), "x(9216,16384)")
+    del xh
+
     # Q/K RMSNorm + split RoPE at N = 9216.
     q = torch.randn((1, M, 4096), generator=g, device=dev).to(torch.bfloat16)
     k = torch.randn((1, M, 4096), generator=g, device=dev).to(torch.bfloat16)

@@ -116,16 +116,12 @@ int oga_fp8_quantize_e4m3(const void* x, const float* scale, int scale_is_0dim, 
 /* `fused_gelu_tanh_fp8_quantize_e4m3` (triton_ltx_ops.py:164-182; torch
  * path :165-169): the quantizer above applied to R(gelu_tanh(x)), with the
  * GELU evaluated in float32 exactly as torch's GPU kernel evaluates
- * gelu(approximate='tanh') (the device tanhf), so the codes equal torch's. */
+ * gelu(approximate='tanh') (the device tanhf), so the codes equal torch's.
+ * Each call first writes R(gelu) of all 65536 bf16 inputs into a 128 KiB
+ * table in a file-scope device array of the library (the same values every
+ * time), then quantizes by looking the elements up in it. */
 int oga_gelu_tanh_fp8_quantize_e4m3(const void* x, const float* scale, int scale_is_0dim, void* q,
                                     int64_t n, void* stream);
-
-/* Opt-in inexact variant of oga_gelu_tanh_fp8_quantize_e4m3 (no reference
- * counterpart): GELU as x / (1 + 2^a) with the hardware exp2 and reciprocal,
- * about a fifth faster at the FFN shape; a small fraction of its bf16 GELU
- * values (and the codes they feed) differ from torch's by one step. */
-int oga_gelu_tanh_fp8_quantize_e4m3_fast(const void* x, const float* scale, int scale_is_0dim, void* q,
-                                         int64_t n, void* stream);
 
 /*
  * `fused_fp8_quantize_e4m3_per_head_4d` (triton_ltx_ops.py:265-317; torch

@@ -43,7 +43,6 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "oga_head_gate_mul_bf16": (_i32, [_p, _p, _i64, _i64, _p, _i64, _i64, _i64, _p]),
     "oga_fp8_quantize_e4m3": (_i32, [_p, _p, _i32, _p, _i64, _p]),
     "oga_gelu_tanh_fp8_quantize_e4m3": (_i32, [_p, _p, _i32, _p, _i64, _p]),
-    "oga_gelu_tanh_fp8_quantize_e4m3_fast": (_i32, [_p, _p, _i32, _p, _i64, _p]),
     "oga_fp8_per_head_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "oga_fp8_quantize_per_head": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _p]),
     "oga_video_qk_rmsnorm_rope": (_i32, [_p, _p, _p, _p, _i32, _p, _p, _i32, _i64p, _i64p, _p, _p, _i64, _i64,

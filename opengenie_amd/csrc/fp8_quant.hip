@@ -27,33 +27,15 @@ namespace oga {
 // -ffp-contract=fast, so x + kKappa * x^3 is one fused multiply-add; every
 // other step is a separate float32 operation. The result is the same bf16
 // value torch produces for every one of the 65536 bf16 inputs.
-constexpr int kGeluNone = 0, kGeluExact = 1, kGeluFast = 2;
+constexpr int kGeluNone = 0, kGeluExact = 1;
 constexpr float kGeluBeta = (float)(M_SQRT2 * M_2_SQRTPI * 0.5);
 constexpr float kGeluKappa = 0.044715f;
-// The opt-in fast form (kGeluFast) evaluates the same function as
-// x / (1 + exp(-2 inner)) = x / (1 + 2^a), a = x (c0 + c1 x^2), with one
-// v_exp_f32 and a Newton-refined v_rcp_f32: about 20 % faster at the FFN
-// shape but rounded differently, so a small fraction of bf16 results (and
-// of the e4m3 codes they feed) differ from torch's by one step. Where 2^a
-// would pass 2^64 (x below about -7.7) it returns x * 0 (-0, or NaN for
-// -inf), as torch's saturated tanh does.
-constexpr double kLog2e = 1.4426950408889634;
-constexpr float kGeluC0 = (float)(-2.0 * 0.7978845608028654 * kLog2e);
-constexpr float kGeluC1 = (float)(-2.0 * 0.7978845608028654 * 0.044715 * kLog2e);
 template <int GELU>
 OGA_DEVICE float pre(float x) {
   if (GELU == kGeluNone) return x;
-  if (GELU == kGeluExact) {
-    const float x3 = (x * x) * x;
-    const float inner = kGeluBeta * fmaf(kGeluKappa, x3, x);
-    return rbf((0.5f * x) * (1.0f + tanhf(inner)));
-  }
-  const float a = x * fmaf(kGeluC1, x * x, kGeluC0);
-  const bool big = a > 64.0f;
-  const float d = 1.0f + __builtin_amdgcn_exp2f(big ? 64.0f : a);
-  float rc = __builtin_amdgcn_rcpf(d);
-  rc = fmaf(fmaf(-d, rc, 1.0f), rc, rc);
-  return rbf(x * (big ? 0.0f : rc));
+  const float x3 = (x * x) * x;
+  const float inner = kGeluBeta * fmaf(kGeluKappa, x3, x);
+  return rbf((0.5f * x) * (1.0f + tanhf(inner)));
 }
 
 template <int GELU>
@@ -87,6 +69,78 @@ __global__ __launch_bounds__(256) void k_fp8_quant(const uint16_t* x, const floa
       if (zero_dim) v = rbf(v);
       v = clamp448(v);
       q[i] = (uint8_t)(e4m3x4(v, 0.0f, 0.0f, 0.0f) & 0xFF);
+    }
+  }
+}
+
+// ------------------------------------------------------------ GELU table
+// The GELU quantizer reads R(gelu(x)) from a table: a bf16 input has 65536
+// patterns, so k_gelu_table evaluates the formula of pre<kGeluExact> once
+// per pattern (128 KiB of bf16 results, written on every call; every call
+// writes the same values) and the streaming kernel looks each element up in
+// an LDS copy of it, which makes the pass HBM-bound instead of bound by
+// tanhf's VALU work. The table lives in a file-scope device array per GPU;
+// its address comes from hipGetSymbolAddress.
+static __device__ __align__(256) uint16_t gelu_table[65536];
+__global__ __launch_bounds__(256) void k_gelu_table(uint16_t* table) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;  // grid: 256 x 256
+  table[i] = (uint16_t)(__float_as_uint(pre<kGeluExact>(__uint_as_float(i << 16))) >> 16);
+}
+
+// q = e4m3(clamp(table[x] * r)) with the rounding rule of k_fp8_quant. One
+// 1024-lane workgroup per CU (the table takes 128 KiB of LDS) walks the
+// tensor in steps of gridDim.x * 1024 lanes * 32 elements; per step a lane
+// converts two 16-element groups with all four 16-byte loads in flight.
+constexpr int kGeluLanes = 1024;
+__global__ __launch_bounds__(kGeluLanes) void k_gelu_quant(const uint16_t* x, const float* scale, int zero_dim,
+                                                           uint8_t* q, int64_t n, const uint16_t* table) {
+  __shared__ uint4 tab[65536 * 2 / 16];
+  for (int k = threadIdx.x; k < 65536 * 2 / 16; k += kGeluLanes) tab[k] = ((const uint4*)table)[k];
+  __syncthreads();
+  const uint16_t* const t16 = (const uint16_t*)tab;
+  float r = 1.0f / scale[0];
+  if (zero_dim) r = rbf(r);
+  auto code = [&](uint32_t xb) {  // one element, x as bf16 bits
+    float v = __uint_as_float((uint32_t)t16[xb] << 16) * r;
+    if (zero_dim) v = rbf(v);
+    return clamp448(v);
+  };
+  auto conv16 = [&](const uint4& u0, const uint4& u1, int64_t i0) {
+    const uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+    float f[16];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      f[2 * k] = code(w[k] & 0xFFFFu);
+      f[2 * k + 1] = code(w[k] >> 16);
+    }
+    uint4 o;
+    o.x = e4m3x4(f[0], f[1], f[2], f[3]);
+    o.y = e4m3x4(f[4], f[5], f[6], f[7]);
+    o.z = e4m3x4(f[8], f[9], f[10], f[11]);
+    o.w = e4m3x4(f[12], f[13], f[14], f[15]);
+    st_nt16(q + i0, o);
+  };
+  // A group of 16 elements at g < n, whole or the tensor's ragged end.
+  auto group = [&](int64_t g) {
+    if (g + 16 <= n) {
+      conv16(*(const uint4*)(x + g), *(const uint4*)(x + g + 8), g);
+    } else {
+      for (int64_t i = g; i < n; ++i) q[i] = (uint8_t)(e4m3x4(code(x[i]), 0.0f, 0.0f, 0.0f) & 0xFF);
+    }
+  };
+  const int64_t step = (int64_t)gridDim.x * kGeluLanes * 32;
+  // Workgroup b's lanes cover elements 32768 b .. +32767 of every step: the
+  // first group of lane t at 16 t, the second 16384 further on.
+  for (int64_t base = ((int64_t)blockIdx.x * 2 * kGeluLanes + threadIdx.x) * 16; base < n; base += step) {
+    const int64_t i1 = base + (int64_t)kGeluLanes * 16;
+    if (i1 + 16 <= n) {
+      const uint4 a0 = *(const uint4*)(x + base), a1 = *(const uint4*)(x + base + 8);
+      const uint4 b0 = *(const uint4*)(x + i1), b1 = *(const uint4*)(x + i1 + 8);
+      conv16(a0, a1, base);
+      conv16(b0, b1, i1);
+    } else {
+      group(base);
+      if (i1 < n) group(i1);
     }
   }
 }
@@ -272,31 +326,40 @@ extern "C" int oga_fp8_quantize_e4m3(const void* x, const float* scale, int scal
   return launch_status();
 }
 
-static int gelu_quant(const void* x, const float* scale, int scale_is_0dim, void* q, int64_t n, bool fast,
-                      hipStream_t st) {
-  if (!x || !scale || !q) return fail("null pointer");
-  if (n < 0) return fail("bad size");
-  if (n == 0) return OGA_OK;
-  if (!aligned(x, 16) || !aligned(q, 16)) return fail("x/q must be 16-byte aligned");
-  const int64_t threads = (n + 15) / 16;
-  const dim3 grid((unsigned)((threads + 255) / 256));
-  if (fast)
-    hipLaunchKernelGGL(k_fp8_quant<kGeluFast>, grid, dim3(256), 0, st, (const uint16_t*)x, scale,
-                       scale_is_0dim ? 1 : 0, (uint8_t*)q, n);
-  else
-    hipLaunchKernelGGL(k_fp8_quant<kGeluExact>, grid, dim3(256), 0, st, (const uint16_t*)x, scale,
-                       scale_is_0dim ? 1 : 0, (uint8_t*)q, n);
-  return launch_status();
+// Per-GPU address of the GELU table (hipGetSymbolAddress, once per device).
+static std::atomic<void*> g_gelu_table[64];
+static int gelu_table_ptr(uint16_t** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail("no current device");
+  void* p = g_gelu_table[dev].load(std::memory_order_acquire);
+  if (!p) {
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(gelu_table));
+    if (e != hipSuccess) return (int)e;
+    g_gelu_table[dev].store(p, std::memory_order_release);
+  }
+  *out = (uint16_t*)p;
+  return OGA_OK;
 }
 
 extern "C" int oga_gelu_tanh_fp8_quantize_e4m3(const void* x, const float* scale, int scale_is_0dim, void* q,
                                                int64_t n, void* stream) {
-  return gelu_quant(x, scale, scale_is_0dim, q, n, false, (hipStream_t)stream);
-}
-
-extern "C" int oga_gelu_tanh_fp8_quantize_e4m3_fast(const void* x, const float* scale, int scale_is_0dim, void* q,
-                                                    int64_t n, void* stream) {
-  return gelu_quant(x, scale, scale_is_0dim, q, n, true, (hipStream_t)stream);
+  if (!x || !scale || !q) return fail("null pointer");
+  if (n < 0) return fail("bad size");
+  if (n == 0) return OGA_OK;
+  if (!aligned(x, 16) || !aligned(q, 16)) return fail("x/q must be 16-byte aligned");
+  uint16_t* table = nullptr;
+  int rc = gelu_table_ptr(&table);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_gelu_table, dim3(256), dim3(256), 0, st, table);
+  rc = launch_status();
+  if (rc) return rc;
+  // Steps of 1024 lanes x 32 elements; at most one workgroup per CU.
+  const int64_t steps = (n + 32 * kGeluLanes - 1) / (32 * kGeluLanes);
+  const int64_t wgs = steps < (int64_t)cu_count() ? steps : (int64_t)cu_count();
+  hipLaunchKernelGGL(k_gelu_quant, dim3((unsigned)wgs), dim3(kGeluLanes), 0, st, (const uint16_t*)x, scale,
+                     scale_is_0dim ? 1 : 0, (uint8_t*)q, n, (const uint16_t*)table);
+  return launch_status();
 }
 
 extern "C" int64_t oga_fp8_per_head_workspace_bytes(int64_t batch, int64_t tokens, int64_t heads, int64_t head_dim) {

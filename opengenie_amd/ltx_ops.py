@@ -628,14 +628,12 @@ def fused_fp8_quantize_e4m3(x: torch.Tensor, input_scale: torch.Tensor) -> torch
     return q
 
 
-def fused_gelu_tanh_fp8_quantize_e4m3(x: torch.Tensor, input_scale: torch.Tensor, *,
-                                      exact: bool = True) -> torch.Tensor:
+def fused_gelu_tanh_fp8_quantize_e4m3(x: torch.Tensor, input_scale: torch.Tensor) -> torch.Tensor:
     """:164-182 — quantize gelu(x, approximate='tanh').
 
-    The HIP kernel evaluates the GELU as torch's GPU kernel does, so the codes
-    equal torch's. `exact=False` (no reference counterpart) selects a faster
-    form of the same function whose rounding differs from torch's in a small
-    fraction of elements by one bf16 step."""
+    The HIP path looks R(gelu(x)) up in a table of all 65536 bf16 inputs,
+    built on the device with the float32 steps of torch's GPU kernel (the
+    device tanhf), so the codes equal torch's."""
     if not _can_use_fused_fp8_quantize(x, input_scale):
         _fallback("fused_gelu_tanh_fp8_quantize_e4m3", x, input_scale)
         gelu = torch.nn.functional.gelu(x, approximate="tanh")
@@ -644,7 +642,7 @@ def fused_gelu_tanh_fp8_quantize_e4m3(x: torch.Tensor, input_scale: torch.Tensor
         return torch.clamp(gelu * input_scale.reciprocal(), fp8_min, fp8_max).to(_FP8)
     q = torch.empty_strided(x.shape, x.stride(), device=x.device, dtype=_FP8)
     _hip("fused_gelu_tanh_fp8_quantize_e4m3")
-    _lib.call("oga_gelu_tanh_fp8_quantize_e4m3" if exact else "oga_gelu_tanh_fp8_quantize_e4m3_fast", _ptr(x), _ptr(input_scale), int(input_scale.dim() == 0), _ptr(q),
+    _lib.call("oga_gelu_tanh_fp8_quantize_e4m3", _ptr(x), _ptr(input_scale), int(input_scale.dim() == 0), _ptr(q),
               x.numel(), _stream(x))
     return q
 
