@@ -513,10 +513,14 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
   // Per-token timesteps in bf16 are loaded for the whole row up front; in
   // float32 (twice the registers) chunk by chunk.
   constexpr bool kTsRow = !UNIFORM && B0 && B1;
-  for (int64_t t = t_first; t < a.tokens; t += V) {
-    if (t != t_first && !UNIFORM) {
+  // One row t from the loaded buffer `cur`; with a shared timestep row the
+  // loads of the wave's next row go into `nxt` right after `cur` is
+  // unpacked. The first row is peeled off the loop: with one row per wave
+  // (2304 tokens) no loop-carried register copies are made at all.
+  auto row = [&](auto first_c, int64_t t, uint4(&cur)[CH], uint4(&nxt)[CH]) {
+    if (!decltype(first_c)::value && !UNIFORM) {
 #pragma unroll
-      for (int j = 0; j < CH; ++j) xv[j] = *(const uint4*)(xb + t * C + j * 512);
+      for (int j = 0; j < CH; ++j) cur[j] = *(const uint4*)(xb + t * C + j * 512);
     }
     Raw8<D0> p0[kTsRow ? CH : 1];
     Raw8<D1> p1[kTsRow ? CH : 1];
@@ -531,15 +535,15 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
     double ss[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
-      unpack8(xv[j], f[j]);
+      unpack8(cur[j], f[j]);
 #pragma unroll
       for (int i = 0; i < 8; ++i) ss[i & 3] = fma((double)f[j][i], (double)f[j][i], ss[i & 3]);
     }
-    if constexpr (UNIFORM) {  // the next row's loads, into the buffer just unpacked
+    if constexpr (UNIFORM) {  // the next row's loads
       const int64_t tn = t + V;
       if (tn < a.tokens) {
 #pragma unroll
-        for (int j = 0; j < CH; ++j) xv[j] = *(const uint4*)(xb + tn * C + j * 512);
+        for (int j = 0; j < CH; ++j) nxt[j] = *(const uint4*)(xb + tn * C + j * 512);
       }
     }
     const double tot = wave_sum_d((ss[0] + ss[1]) + (ss[2] + ss[3]));
@@ -590,6 +594,10 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
       }
       st_nt16(yb + t * C + j * 512, make_uint4(ow[0], ow[1], ow[2], ow[3]));
     }
+  };
+  if (t_first < a.tokens) {
+    row(IC<1>{}, t_first, xv, xv);  // its loads went out before the fill
+    for (int64_t t = t_first + V; t < a.tokens; t += V) row(IC<0>{}, t, xv, xv);
   }
 }
 
