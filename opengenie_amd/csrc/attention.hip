@@ -76,15 +76,16 @@ struct AttnArgs {
   int64_t o_sb, o_sn, o_sh;
   int64_t nq, nk;
   int heads;
-  int nqb;        // query blocks of kAQ per (batch, head)
+  int nqb;        // query blocks per (batch, head)
+  int qpb;        // queries per block (kAQ, or kF8Q for the FP8 kernel)
   int xcd_remap;  // nfull divisible by the 8 XCDs
   float scale_log2;  // softmax scale * log2(e)
   // Workgroups 0 .. nfull-1 each own query block blockIdx.x (remapped) over
   // all keys. The blocks nfull .. end, which would fill only part of a last
   // round of the CUs, are cut into ksplit parts over their key steps: later
   // workgroup nfull + u owns part u % ksplit of block nfull + u / ksplit and
-  // leaves its unnormalized O (part_o, [u][kAQ][kAD] float32) and its
-  // running max and sum (part_ml, [u][kAQ][2]) for k_attention_combine.
+  // leaves its unnormalized O (part_o, [u][qpb][kAD] float32) and its
+  // running max and sum (part_ml, [u][qpb][2]) for k_attention_combine.
   int64_t nfull;
   int ksplit;
   float* part_o;
@@ -605,12 +606,24 @@ OGA_DEVICE i32x8 lds_b256(uint32_t a0, uint32_t a1) {
   return r;
 }
 
-static_assert(kAW == 8, "the FP8 kernel's DMA gives each of 8 waves one 1 KiB instruction per tile");
+#ifndef OGA_F8_WAVES
+#define OGA_F8_WAVES 12
+#endif
+constexpr int kF8W = OGA_F8_WAVES;  // waves per FP8 workgroup, 32 queries each
+constexpr int kF8Q = 32 * kF8W;      // queries per FP8 workgroup
+constexpr int kF8DmaW = 8;           // waves whose DMA fills the tiles: one 1 KiB instruction per tile each
+static_assert(kF8W == 8 || kF8W == 12, "8 waves (2 per SIMD) or 12 (3 per SIMD)");
 constexpr int kF8Bufs = kABufs;  // K/V^T tile pairs in the FP8 kernel's ring
-constexpr int kF8Lds = kF8Bufs * kF8Pair > kAW * 8192 ? kF8Bufs * kF8Pair : kAW * 8192;
-static_assert(kF8Lds <= 65536, "the FP8 fragment reads address LDS with 16-bit offsets");
+// Waves past the eighth send the same two DMA instructions per step as the
+// others (so that every wave waits for the same count) into 2 KiB of their
+// own after the ring, re-reading tile rows the first eight fetch.
+constexpr int kF8DummyOff = kF8Bufs * kF8Pair;
+constexpr int kF8Ring = kF8DummyOff + (kF8W - kF8DmaW) * 2048;
+constexpr int kF8Lds = kF8Ring > kF8W * 8192 ? kF8Ring : kF8W * 8192;
+static_assert(kF8Ring <= 65536, "the FP8 fragment reads address LDS with 16-bit offsets");
 
-__global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attention_fp8(AttnArgs a) {
+__global__ __launch_bounds__(64 * kF8W) __attribute__((amdgpu_waves_per_eu(kF8W / 4, kF8W / 4))) void k_attention_fp8(
+    AttnArgs a) {
   __shared__ uint4 smem[kF8Lds / 16];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -627,7 +640,7 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int64_t bh = wg / a.nqb;
   const int h = (int)(bh % a.heads);
   const int64_t b = bh / a.heads;
-  const int64_t q0 = (int64_t)qb * kAQ + wv * 32;
+  const int64_t q0 = (int64_t)qb * kF8Q + wv * 32;
   const int hl = lane >> 5;
   const int ql = lane & 31;
   const float qd = a.q_ds[b * a.heads + h], kd = a.k_ds[b * a.heads + h], vd = a.v_ds[b * a.heads + h];
@@ -662,19 +675,25 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
   // p writes line L = 4wv + p/16, position p%16, holding row 2L + v/8, chunk
   // v%8 with v = (p%16) ^ (L%8). V^T: lane p writes d-row 16wv + p/4,
   // position p%4, holding chunk (p%4) ^ ((d/4)%4) of the row.
-  const int kL = 4 * wv + (lane >> 4);
+  const int wd = wv % kF8DmaW;  // the tile part this wave's DMA reads
+  const int kL = 4 * wd + (lane >> 4);
   const int kv = (lane & 15) ^ (kL & 7);
   const int krow = 2 * kL + (kv >> 3);
   const uint32_t koff_c = (uint32_t)((kv & 7) * 16);
-  const int vd_row = 16 * wv + (lane >> 2);
+  const int vd_row = 16 * wd + (lane >> 2);
   const int64_t vt_src = vd_row * a.vt_npad + (((lane & 3) ^ ((vd_row >> 2) & 3)) * 16);
+  // LDS destinations (wave-uniform): the wave's 1 KiB of the pair's K and
+  // V^T tiles, or, for a wave past the eighth, its own 2 KiB after the ring.
+  const bool tile_wave = wv < kF8DmaW;
+  const int k_dst = tile_wave ? wv * 64 : kF8DummyOff / 16 + (wv - kF8DmaW) * 128;
+  const int v_dst = tile_wave ? kF8Tile / 16 + wv * 64 : kF8DummyOff / 16 + (wv - kF8DmaW) * 128 + 64;
   auto dma_step = [&](int64_t s2, uint4* dst) {
     const int64_t key0 = s2 * kAK;
     const int64_t r = min((int64_t)krow, a.nk - 1 - key0);
-    __builtin_amdgcn_global_load_lds((const void*)(kbase + (key0 + r) * a.k_sn + koff_c),
-                                     (lds_void*)(dst + wv * 64), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((const void*)(vtbase + key0 + vt_src),
-                                     (lds_void*)(dst + kF8Tile / 16 + wv * 64), 16, 0, 0);
+    uint4* const kd = tile_wave ? dst + k_dst : smem + k_dst;
+    uint4* const vdp = tile_wave ? dst + v_dst : smem + v_dst;
+    __builtin_amdgcn_global_load_lds((const void*)(kbase + (key0 + r) * a.k_sn + koff_c), (lds_void*)kd, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void*)(vtbase + key0 + vt_src), (lds_void*)vdp, 16, 0, 0);
   };
   dma_step(st_begin, smem);
   if (kF8Bufs == 3) dma_step(min(st_begin + 1, st_end - 1), smem + kF8Pair / 16);
@@ -785,9 +804,16 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
     f32x16 sacc[2];
     i32x8 vf[4], pf;
     s_phase(par_c, sacc);
-    // V^T fragments in flight under the softmax.
-    v_read(par_c, vf);
-    softmax(st, sacc, pf);
+    if constexpr (kF8W == 8) {
+      // V^T fragments in flight under the softmax.
+      v_read(par_c, vf);
+      softmax(st, sacc, pf);
+    } else {
+      // With three waves per SIMD the fragments are read after the softmax
+      // (168 VGPRs), the other waves covering the reads' latency.
+      softmax(st, sacc, pf);
+      v_read(par_c, vf);
+    }
     pv(vf, pf);
   };
 
@@ -800,7 +826,7 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   if (part >= 0) {
-    const int64_t row = (int64_t)(blockIdx.x - a.nfull) * kAQ + wv * 32 + ql;
+    const int64_t row = (int64_t)(blockIdx.x - a.nfull) * kF8Q + wv * 32 + ql;
     float* po = a.part_o + row * kAD;
 #pragma unroll
     for (int dblk = 0; dblk < 4; ++dblk)
@@ -886,21 +912,21 @@ __global__ __launch_bounds__(256) void k_attention_combine(AttnArgs a, int64_t r
   if (idx >= rows * (kAD / 8)) return;
   const int c = (int)(idx % (kAD / 8));
   const int64_t row = idx / (kAD / 8);
-  const int64_t sb = row / kAQ;
-  const int qr = (int)(row % kAQ);
+  const int64_t sb = row / a.qpb;
+  const int qr = (int)(row % a.qpb);
   const int64_t wg = a.nfull + sb;
   const int qb = (int)(wg % a.nqb);
   const int64_t bh = wg / a.nqb;
   const int h = (int)(bh % a.heads);
   const int64_t b = bh / a.heads;
-  const int64_t qi = (int64_t)qb * kAQ + qr;
+  const int64_t qi = (int64_t)qb * a.qpb + qr;
   if (qi >= a.nq) return;
-  const int64_t r0 = sb * a.ksplit * kAQ + qr;  // row of part 0; part p adds p * kAQ
+  const int64_t r0 = sb * a.ksplit * a.qpb + qr;  // row of part 0; part p adds p * qpb
   float mx = -INFINITY;
-  for (int p = 0; p < a.ksplit; ++p) mx = __builtin_fmaxf(mx, a.part_ml[2 * (r0 + (int64_t)p * kAQ)]);
+  for (int p = 0; p < a.ksplit; ++p) mx = __builtin_fmaxf(mx, a.part_ml[2 * (r0 + (int64_t)p * a.qpb)]);
   float l = 0.0f, acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
   for (int p = 0; p < a.ksplit; ++p) {
-    const int64_t rp = r0 + (int64_t)p * kAQ;
+    const int64_t rp = r0 + (int64_t)p * a.qpb;
     const float w = __builtin_amdgcn_exp2f(a.part_ml[2 * rp] - mx);
     l += w * a.part_ml[2 * rp + 1];
     const float4 x0 = *(const float4*)(a.part_o + rp * kAD + 8 * c);
@@ -975,7 +1001,8 @@ int64_t attention_slots(bool fp8 = false) {
   if (n == 0) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fp8 ? k_attention_fp8 : k_attention, 64 * kAW, 0) !=
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fp8 ? k_attention_fp8 : k_attention,
+                                                     fp8 ? 64 * kF8W : 64 * kAW, 0) !=
             hipSuccess)
       return 0;
     n = (int64_t)cus * per_cu > 0 ? (int64_t)cus * per_cu : -1;
@@ -1005,7 +1032,7 @@ AttnPlan attention_plan(int64_t wgs, int64_t nk, int64_t slots) {
   if (p.ksplit > 1) { p.nfull = wgs - rem; p.units = rem * p.ksplit; }
   return p;
 }
-int64_t attention_ws_bytes(const AttnPlan& p) { return p.units * kAQ * (kAD + 2) * (int64_t)sizeof(float); }
+int64_t attention_ws_bytes(const AttnPlan& p, int qpb) { return p.units * qpb * (kAD + 2) * (int64_t)sizeof(float); }
 
 int attention_run(const void* q, const int64_t q_strides[3], const void* k, const int64_t k_strides[3],
                   const void* v, const int64_t v_strides[3], void* o, const int64_t o_strides[3], int64_t batch,
@@ -1037,10 +1064,11 @@ int attention_run(const void* q, const int64_t q_strides[3], const void* k, cons
   const int64_t wgs = nqb * heads * batch;
   if (nqb > INT32_MAX || wgs > UINT32_MAX / 8) return unsupported("too many query blocks");
   a.nqb = (int)nqb;
+  a.qpb = kAQ;
   AttnPlan plan{wgs, wgs, 0, 1};
   if (workspace_bytes > 0) {
     plan = attention_plan(wgs, nk, attention_slots());
-    if (attention_ws_bytes(plan) > workspace_bytes) return fail("workspace smaller than oga_attention_workspace_bytes");
+    if (attention_ws_bytes(plan, kAQ) > workspace_bytes) return fail("workspace smaller than oga_attention_workspace_bytes");
   }
   a.nfull = plan.nfull;
   a.ksplit = plan.ksplit;
@@ -1099,25 +1127,26 @@ int attention_fp8_run(const void* q, const int64_t q_strides[3], const void* k, 
   a.vt = (const uint8_t*)workspace;
   a.vt_npad = (nk + kAK - 1) / kAK * kAK;
   a.q_ds = q_descale; a.k_ds = k_descale; a.v_ds = v_descale;
-  const int64_t nqb = (nq + kAQ - 1) / kAQ;
+  const int64_t nqb = (nq + kF8Q - 1) / kF8Q;
   const int64_t wgs = nqb * heads * batch;
   if (nqb > INT32_MAX || wgs > UINT32_MAX / 8) return unsupported("too many query blocks");
   a.nqb = (int)nqb;
+  a.qpb = kF8Q;
   AttnPlan plan = attention_plan(wgs, nk, attention_slots(true));
-  if (vtb + attention_ws_bytes(plan) > workspace_bytes) plan = AttnPlan{wgs, wgs, 0, 1};
+  if (vtb + attention_ws_bytes(plan, kF8Q) > workspace_bytes) plan = AttnPlan{wgs, wgs, 0, 1};
   a.nfull = plan.nfull;
   a.ksplit = plan.ksplit;
   a.part_o = plan.units ? (float*)((char*)workspace + vtb) : nullptr;
-  a.part_ml = plan.units ? a.part_o + plan.units * kAQ * kAD : nullptr;
+  a.part_ml = plan.units ? a.part_o + plan.units * kF8Q * kAD : nullptr;
   a.xcd_remap = plan.nfull % 8 == 0;
   hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(k_fp8_v_transpose, dim3((unsigned)(a.vt_npad / kAK), (unsigned)heads, (unsigned)batch), dim3(256),
                      0, st, (const uint8_t*)v, a.v_sb, a.v_sn, a.v_sh, (uint8_t*)workspace, nk, a.vt_npad, (int)heads);
   int rc = launch_status();
   if (rc) return rc;
-  hipLaunchKernelGGL(k_attention_fp8, dim3((unsigned)(plan.nfull + plan.units)), dim3(64 * kAW), 0, st, a);
+  hipLaunchKernelGGL(k_attention_fp8, dim3((unsigned)(plan.nfull + plan.units)), dim3(64 * kF8W), 0, st, a);
   if (plan.units) {
-    const int64_t rows = (wgs - plan.nfull) * kAQ;
+    const int64_t rows = (wgs - plan.nfull) * kF8Q;
     hipLaunchKernelGGL(k_attention_combine, dim3((unsigned)((rows * (kAD / 8) + 255) / 256)), dim3(256), 0, st, a,
                        rows);
   }
@@ -1138,7 +1167,7 @@ extern "C" int64_t oga_attention_workspace_bytes(int64_t batch, int64_t nq, int6
   if (batch <= 0 || nq <= 0 || nk <= 0 || heads <= 0 || head_dim != kAD) return 0;
   const int64_t nqb = (nq + kAQ - 1) / kAQ;
   if (nqb > INT32_MAX || heads > INT32_MAX || nqb * heads > (int64_t)(UINT32_MAX / 8) / batch) return 0;
-  return attention_ws_bytes(attention_plan(nqb * heads * batch, nk, attention_slots()));
+  return attention_ws_bytes(attention_plan(nqb * heads * batch, nk, attention_slots()), kAQ);
 }
 
 extern "C" int oga_attention_ws(const void* q, const int64_t q_strides[3], const void* k, const int64_t k_strides[3],
@@ -1152,9 +1181,10 @@ extern "C" int oga_attention_ws(const void* q, const int64_t q_strides[3], const
 extern "C" int64_t oga_attention_fp8_workspace_bytes(int64_t batch, int64_t nq, int64_t nk, int64_t heads,
                                                      int64_t head_dim) {
   if (batch <= 0 || nq <= 0 || nk <= 0 || heads <= 0 || head_dim != kAD) return 0;
-  const int64_t nqb = (nq + kAQ - 1) / kAQ;
+  const int64_t nqb = (nq + kF8Q - 1) / kF8Q;
   if (nqb > INT32_MAX || heads > 65535 || batch > 65535) return 0;
-  return vt_bytes(batch, heads, nk) + attention_ws_bytes(attention_plan(nqb * heads * batch, nk, attention_slots(true)));
+  return vt_bytes(batch, heads, nk) +
+         attention_ws_bytes(attention_plan(nqb * heads * batch, nk, attention_slots(true)), kF8Q);
 }
 
 extern "C" int oga_attention_fp8_ws(const void* q8, const int64_t q_strides[3], const void* k8,

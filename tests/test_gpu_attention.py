@@ -206,7 +206,7 @@ def _check_fp8(out: np.ndarray, ref: np.ndarray, what: str) -> float:
 def test_fp8_attention_kernel(b, nq, nk, h):
     """e4m3 Q/K/V from the per-head quantizer through the FP8 kernel, against
     float64 attention on the dequantized inputs (ragged key counts, batch 2,
-    nq != nk, grids that take the key-split last round and one that does not)."""
+    nq != nk, a partial query block)."""
     from opengenie_amd.attention import flash_attn_func
     from opengenie_amd.ltx_ops import fused_fp8_quantize_e4m3_per_head_4d
 
@@ -222,6 +222,34 @@ def test_fp8_attention_kernel(b, nq, nk, h):
     qe, ke, ve = (_fp8_exact(t, s) for t, s in ((q8, qs), (k8, ks), (v8, vs)))
     ref = O.attention(*[np.ascontiguousarray(x.transpose(0, 2, 1, 3)) for x in (qe, ke, ve)]).transpose(0, 2, 1, 3)
     _check_fp8(out.float().cpu().numpy(), ref, f"fp8 kernel {b}x{nq}x{nk}x{h}")
+
+
+def test_fp8_attention_key_split():
+    """17 query blocks x 16 heads = 272 workgroups of the FP8 kernel: on a
+    256-CU device the 16 past the whole round run as key parts merged by the
+    combine kernel (asserted from the workspace query, which then exceeds the
+    V rewrite). Against float64 attention with the e4m3 bars."""
+    from opengenie_amd import _lib
+    from opengenie_amd.attention import flash_attn_func
+    from opengenie_amd.ltx_ops import fused_fp8_quantize_e4m3_per_head_4d
+
+    b, nq, nk, h = 1, 17 * 384, 512, 16
+    lib = _lib.load()
+    vt_bytes = b * h * 128 * nk
+    if int(lib.oga_attention_fp8_workspace_bytes(b, nq, nk, h, 128)) <= vt_bytes:
+        pytest.skip("this device runs the 272 workgroups without a key split")
+    q = randn((b, nq, h, 128), 940).to(DEV)
+    k = randn((b, nk, h, 128), 941).to(DEV)
+    v = randn((b, nk, h, 128), 942).to(DEV)
+    q8, qs = fused_fp8_quantize_e4m3_per_head_4d(q)
+    k8, ks = fused_fp8_quantize_e4m3_per_head_4d(k)
+    v8, vs = fused_fp8_quantize_e4m3_per_head_4d(v)
+    out = flash_attn_func(q8, k8, v8, q_descale=qs, k_descale=ks, v_descale=vs)
+    torch.cuda.synchronize()
+    _ran("flash_attn_func_fp8")
+    qe, ke, ve = (_fp8_exact(t, s) for t, s in ((q8, qs), (k8, ks), (v8, vs)))
+    ref = O.attention(*[np.ascontiguousarray(x.transpose(0, 2, 1, 3)) for x in (qe, ke, ve)]).transpose(0, 2, 1, 3)
+    _check_fp8(out.float().cpu().numpy(), ref, "fp8 key split")
 
 
 def test_fp8_attention_strided_views():
