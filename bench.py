@@ -304,16 +304,23 @@ def attention_rows(seed: int, reps: int = 10) -> dict:
     flops = 4.0 * ATT_N * ATT_N * ATT_H * ATT_D
     st = torch.cuda.current_stream()
 
-    def timed(fn):
-        for _ in range(2):
+    def timed(fn, settle_s: float = 0.5, batches: int = 5):
+        # Calls until the clock has settled after the previous parts, then the
+        # median over batches of the mean time of `reps` back-to-back calls.
+        t0 = time.time()
+        while time.time() - t0 < settle_s:
             fn()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(st)
-        for _ in range(reps):
-            fn()
-        e1.record(st)
-        e1.synchronize()
-        return e0.elapsed_time(e1) * 1000.0 / reps
+            st.synchronize()
+        per = []
+        for _ in range(batches):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            for _ in range(reps):
+                fn()
+            e1.record(st)
+            e1.synchronize()
+            per.append(e0.elapsed_time(e1) * 1000.0 / reps)
+        return statistics.median(per)
 
     us = timed(lambda: A.flash_attn_func(q, k, v))
     rows = {"bf16": {"shape": "q,k,v [1,9216,32,128]", "us": round(us, 1),
