@@ -999,10 +999,17 @@ using namespace oga;
 namespace {
 
 // Split-K plan of the persistent kernel for tiles that do not fill a last
-// round: with R whole rounds over the CUs and r < CUs tiles left, each of the
-// r tiles is cut into S K-chunks (the largest power of two with r * S <= CUs
-// and at least two slabs per chunk), so every workgroup ends with about the
-// same work. S = 1: no split.
+// round: with R >= 0 whole rounds over the CUs and r < CUs tiles left, each
+// of the r tiles may be cut into S K-chunks (a power of two with r * S <= CUs
+// and at least two slabs per chunk). The chunks run at once, so the round
+// they form takes about nslab / S slab-times, and their float32 partials
+// (r * S tiles of 256 KiB, written and read back by the reduce) cost about
+// r * S / 15 slab-times at the device's bandwidth (a 256x256x128 slab takes
+// ~1.56 us on one CU; a tile's partial round trip, 512 KiB at ~5 TB/s,
+// ~0.1 us), plus ~2 slab-times for the two extra launches. S minimises that
+// sum; S = 1: no split. With R = 0 (fewer tiles than CUs: the text
+// projections of 256 context tokens make 16) the split spreads the tiles'
+// K over the idle CUs.
 struct SplitPlan {
   int nfull, split, kchunk, units;
   int64_t ws_bytes;
@@ -1012,9 +1019,14 @@ SplitPlan split_plan(int64_t m, int64_t n, int64_t k, int64_t cus) {
   const int64_t nslab = k / GKS;
   SplitPlan p{(int)nt, 1, (int)nslab, (int)nt, 0};
   const int64_t rounds = nt / cus, rest = nt % cus;
-  if (rounds < 1 || rest == 0) return p;
+  if (rest == 0) return p;
+  // costs in fifteenths of a slab-time
+  int64_t best = 15 * nslab;
   int sp = 1;
-  while (rest * sp * 2 <= cus && nslab % (sp * 2) == 0 && nslab / (sp * 2) >= 2) sp *= 2;
+  for (int s = 2; rest * s <= cus && nslab % s == 0 && nslab / s >= 2; s *= 2) {
+    const int64_t c = 15 * nslab / s + rest * s + 30;
+    if (c < best) { best = c; sp = s; }
+  }
   if (sp == 1) return p;
   p.nfull = (int)(rounds * cus);
   p.split = sp;
@@ -1061,7 +1073,8 @@ int launch_ring(GemmArgs& g, void* workspace, int64_t workspace_bytes, hipStream
   g.units = p.nfull;
   int64_t grid = g.units < cus ? g.units : cus;
   g.xcd_remap = (g.units % 8) == 0 && (grid % 8) == 0;
-  hipLaunchKernelGGL(k_fp8_gemm_ring<false>, dim3((unsigned)grid), dim3(64 * kWaves), 0, stream, g);
+  if (grid > 0)  // none when every tile is split (fewer tiles than CUs)
+    hipLaunchKernelGGL(k_fp8_gemm_ring<false>, dim3((unsigned)grid), dim3(64 * kWaves), 0, stream, g);
   if (p.split > 1) {
     g.units = p.units - p.nfull;
     grid = g.units < cus ? g.units : cus;

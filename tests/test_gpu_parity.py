@@ -509,12 +509,13 @@ def test_fp8_linear(m, n, k, bias_dtype):
     assert (bf16_ulp_distance(got, ref) > 1).mean() < 1e-2
 
 
-@pytest.mark.parametrize("m,n,k", [(4352, 4096, 4096), (4352, 4096, 8192)])
+@pytest.mark.parametrize("m,n,k", [(4352, 4096, 4096), (4352, 4096, 8192), (256, 4096, 4096)])
 def test_fp8_linear_split_k_through_c_abi(m, n, k):
     """The split-K schedule (workspace given) and the whole-tile schedule
     (no workspace) through the C ABI, both against the oracle. 272 tiles on
-    256 CUs leave 16 for a last round, each cut into 16 K-chunks (of 256 at
-    K = 4096, of 512 at K = 8192)."""
+    256 CUs leave 16 for a last round, each cut into K-chunks (4 of 1024 at
+    K = 4096, 8 of 1024 at K = 8192); 256 rows make 16 tiles and no whole
+    round, all of them cut (4 chunks each, the text projections' shape)."""
     from opengenie_amd import _lib
 
     lib = _lib.load()
@@ -552,8 +553,8 @@ def _bias_epilogue_ref(out_nobias: np.ndarray, bias: torch.Tensor) -> np.ndarray
 
 @pytest.mark.parametrize("m,n,k,bias_dtype,use_ws", [
     (4352, 4096, 4096, torch.bfloat16, False),  # persistent whole-tile schedule
-    (4352, 4096, 4096, torch.bfloat16, True),   # + split-K last round (16 tiles x 16 K-chunks)
-    (2304, 16384, 512, torch.bfloat16, True),
+    (4352, 4096, 4096, torch.bfloat16, True),   # + split-K last round (16 tiles x 4 K-chunks)
+    (256, 4096, 4096, torch.bfloat16, True),    # split-K only (16 tiles x 4 K-chunks, no whole round)
     (300, 520, 384, torch.float32, False),      # one-workgroup-per-tile kernel (N not a multiple of 128)
     (300, 520, 384, torch.bfloat16, False),
 ])
