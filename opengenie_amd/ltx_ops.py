@@ -20,6 +20,7 @@ bf16 result; FP8 codes equal torch's conversion of the same expression.
 from __future__ import annotations
 
 import os
+import weakref
 
 import torch
 
@@ -898,6 +899,32 @@ def _is_fp8_linear(linear) -> bool:
             and getattr(linear, "weight_scale", None) is not None)
 
 
+_EQUAL_MEMO: dict = {}
+
+
+def _all_equal(tensors) -> bool:
+    """torch.equal of every tensor with the first, as the reference's guards
+    evaluate it, remembered per tuple of tensors: on GPU tensors each
+    torch.equal is a device-to-host synchronisation, which stalls the launch
+    queue in the middle of a block, and a loaded model's scales do not change
+    between calls. The remembered result is used only while every tensor is
+    the same object (weak reference), with the same storage and the same
+    in-place version counter, so reassigning or modifying a scale in place
+    makes the next call compare again."""
+    key = tuple(id(t) for t in tensors)
+    state = tuple((t.data_ptr(), t._version) for t in tensors)
+    memo = _EQUAL_MEMO.get(key)
+    if memo is not None:
+        refs, old_state, result = memo
+        if old_state == state and all(r() is t for r, t in zip(refs, tensors)):
+            return result
+    result = all(torch.equal(tensors[0], t) for t in tensors[1:])
+    if len(_EQUAL_MEMO) >= 1024:
+        _EQUAL_MEMO.clear()
+    _EQUAL_MEMO[key] = (tuple(weakref.ref(t) for t in tensors), state, result)
+    return result
+
+
 def _scale_fits(scale: torch.Tensor, length: int) -> bool:
     """`_scale_row` (:1281-1287) accepts a scalar or `length` values."""
     return scale.numel() in (1, length)
@@ -919,7 +946,7 @@ def _can_use_video_qkv_shared(attn: torch.nn.Module, x: torch.Tensor, names: tup
     if not all(getattr(lin, "bias", None) is not None for lin in linears):
         return False
     s0 = linears[0].input_scale
-    if not all(torch.equal(s0, lin.input_scale) for lin in linears[1:]):
+    if not _all_equal([lin.input_scale for lin in linears]):
         return False
     if not grouped:
         return True
@@ -1089,10 +1116,9 @@ def _packed_guard_reason(attn: torch.nn.Module, x: torch.Tensor, *, equal_weight
     if not all(getattr(lin, "bias", None) is not None for lin in linears):
         return "bias"
     q, k, v = linears
-    if not (torch.equal(q.input_scale, k.input_scale) and torch.equal(q.input_scale, v.input_scale)):
+    if not _all_equal([q.input_scale, k.input_scale, v.input_scale]):
         return "input_scale"
-    if equal_weight_scales and not (torch.equal(q.weight_scale, k.weight_scale)
-                                    and torch.equal(q.weight_scale, v.weight_scale)):
+    if equal_weight_scales and not _all_equal([q.weight_scale, k.weight_scale, v.weight_scale]):
         return "weight_scale"
     feats = [_features(lin) for lin in linears]
     if not all(fi == x.shape[-1] and fo == x.shape[-1] for fi, fo in feats):

@@ -95,3 +95,26 @@ def test_per_head_cpu_path():
     q, s = L.fused_fp8_quantize_e4m3_per_head_4d(x)
     qr, sr = tr.fp8_per_head(x)
     assert torch.equal(q.view(torch.uint8), qr.view(torch.uint8)) and torch.equal(s, sr)
+
+
+def test_scale_equality_memo_follows_the_tensors():
+    """The Q/K/V guards' torch.equal of the input (and weight) scales is
+    remembered per tuple of tensors and recomputed when a tensor changes in
+    place, is replaced, or another tensor takes its place."""
+    a = torch.tensor([0.5])
+    b = torch.tensor([0.5])
+    c = torch.tensor([0.5])
+    assert L._all_equal([a, b, c])
+    assert L._all_equal([a, b, c])  # remembered
+    c.mul_(2.0)  # in place: version counter moves
+    assert not L._all_equal([a, b, c])
+    c.copy_(torch.tensor([0.5]))
+    assert L._all_equal([a, b, c])
+    c.data = torch.tensor([0.25])  # new storage
+    assert not L._all_equal([a, b, c])
+    d = torch.tensor([0.5])
+    assert L._all_equal([a, b, d])
+    assert not L._all_equal([a, torch.tensor([0.5, 0.5]), d])  # shapes differ: torch.equal is False
+    for trial in range(3):  # fresh tensors each time (ids may be reused after collection)
+        x, y = torch.tensor([float(trial)]), torch.tensor([float(trial) + (trial % 2)])
+        assert L._all_equal([x, y]) == torch.equal(x, y)
