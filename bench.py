@@ -128,6 +128,30 @@ def _graph_time_us(fn, reps: int = 20, inner: int = 25, rounds: int = 3) -> floa
     return best
 
 
+def _settled_time_us(fn, reps: int = 10, settle_s: float = 0.5, batches: int = 5) -> float:
+    """Per-call GPU time of fn on the current stream: calls until the clock
+    has settled after the previous workload (`settle_s`), then the median
+    over `batches` of the mean time of `reps` back-to-back calls (HIP
+    events)."""
+    import torch
+
+    st = torch.cuda.current_stream()
+    t0 = time.time()
+    while time.time() - t0 < settle_s:
+        fn()
+        st.synchronize()
+    per = []
+    for _ in range(batches):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for _ in range(reps):
+            fn()
+        e1.record(st)
+        e1.synchronize()
+        per.append(e0.elapsed_time(e1) * 1000.0 / reps)
+    return statistics.median(per)
+
+
 FLUSH_BYTES = 512 * 1024 * 1024  # twice the MI355X last-level cache (256 MB)
 
 
@@ -302,25 +326,9 @@ def attention_rows(seed: int, reps: int = 10) -> dict:
     g = _gen(seed + 5, "cuda")
     q, k, v = (torch.randn((1, ATT_N, ATT_H, ATT_D), generator=g, device="cuda").to(torch.bfloat16) for _ in range(3))
     flops = 4.0 * ATT_N * ATT_N * ATT_H * ATT_D
-    st = torch.cuda.current_stream()
 
-    def timed(fn, settle_s: float = 0.5, batches: int = 5):
-        # Calls until the clock has settled after the previous parts, then the
-        # median over batches of the mean time of `reps` back-to-back calls.
-        t0 = time.time()
-        while time.time() - t0 < settle_s:
-            fn()
-            st.synchronize()
-        per = []
-        for _ in range(batches):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(st)
-            for _ in range(reps):
-                fn()
-            e1.record(st)
-            e1.synchronize()
-            per.append(e0.elapsed_time(e1) * 1000.0 / reps)
-        return statistics.median(per)
+    def timed(fn):
+        return _settled_time_us(fn, reps)
 
     us = timed(lambda: A.flash_attn_func(q, k, v))
     rows = {"bf16": {"shape": "q,k,v [1,9216,32,128]", "us": round(us, 1),
@@ -364,18 +372,9 @@ def linear_rows(seed: int, reps: int = 10) -> dict:
     from opengenie_amd import ltx_ops as L
 
     rows = {}
-    st = torch.cuda.current_stream()
 
     def timed(fn):
-        for _ in range(3):
-            fn()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(st)
-        for _ in range(reps):
-            fn()
-        e1.record(st)
-        e1.synchronize()
-        return e0.elapsed_time(e1) * 1000.0 / reps
+        return _settled_time_us(fn, reps)
 
     for name, (k, n) in (("ffn_down_16384_to_4096", (16384, 4096)), ("proj_4096_to_4096", (4096, 4096))):
         x, s_in, w, s_w, bias = make_fp8_linear_inputs(seed + n + k, "cuda", M, k, n)
