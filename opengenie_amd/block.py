@@ -173,16 +173,27 @@ def video_self_attention(block: VideoBlock, vx: torch.Tensor, timesteps: torch.T
 
 def video_text_cross_attention(block: VideoBlock, vx: torch.Tensor, context: torch.Tensor,
                                timesteps: torch.Tensor, prompt_timestep: torch.Tensor,
-                               stages: Stages | None = None, *, fuse_norm: bool = False) -> torch.Tensor:
+                               stages: Stages | None = None, *, fuse_norm: bool = False,
+                               fuse_context: bool | None = None) -> torch.Tensor:
     """:2810-2888 (cross_attention_adaln, production flags). rms_norm
     followed by the AdaLN affine of Ada rows 6/7 is AdaZero's composition
     (R(R(R(rms_norm(x)) R(1 + scale)) + shift)); with `fuse_norm` it runs as
-    one AdaZero pass instead of torch's rms_norm and the affine kernel."""
+    one AdaZero pass instead of torch's rms_norm and the affine kernel.
+    `fuse_context` (default: `fuse_norm`) takes the reference's
+    _FUSE_VIDEO_TEXT_CONTEXT_ADALN path (:2839-2850, off in its production):
+    the context affine of the prompt table's rows 0/1 as one AdaLN-affine
+    launch, the same expression as the torch form beside it."""
     a = block.attn2
     b = vx.shape[0]
-    shift_kv, scale_kv = (block.prompt_table[None, None].to(device=vx.device, dtype=vx.dtype)
-                          + prompt_timestep.reshape(b, prompt_timestep.shape[1], 2, -1)).unbind(dim=2)
-    enc = context * (1 + scale_kv) + shift_kv
+    if fuse_context is None:
+        fuse_context = fuse_norm
+    if fuse_context:
+        enc = L.fused_adaln_affine_from_ada(context, block.prompt_table, prompt_timestep, shift_index=0,
+                                            scale_index=1)
+    else:
+        shift_kv, scale_kv = (block.prompt_table[None, None].to(device=vx.device, dtype=vx.dtype)
+                              + prompt_timestep.reshape(b, prompt_timestep.shape[1], 2, -1)).unbind(dim=2)
+        enc = context * (1 + scale_kv) + shift_kv
     if fuse_norm:
         normed = None
         attn_in = L.fused_adazero_from_ada(vx, block.eps, block.table, timesteps, shift_index=6, scale_index=7)
