@@ -190,11 +190,12 @@ int oga_fp8_linear(const void* a, int64_t lda, const void* w, int64_t ldw, const
  * The same FP8 linear (same reference interface) with a caller-owned device
  * workspace of oga_fp8_linear_workspace_bytes(m, n, k) bytes (16-byte
  * aligned). When the 256 x 256 output tiles do not fill a last round of the
- * CUs (e.g. M = 9216, N = 4096: 576 tiles on 256 CUs), the tiles of that
- * round are cut into K-chunks whose float32 partial sums go to the
- * workspace and are added in chunk order (deterministic), so every CU ends
- * with about the same work. A null or smaller workspace (and a size of 0)
- * runs oga_fp8_linear's schedule.
+ * CUs (e.g. M = 9216, N = 4096: 576 tiles on 256 CUs; or M = 256: 16 tiles),
+ * the tiles of that round may be cut into K-chunks whose float32 partial
+ * sums go to the workspace and are added in chunk order (deterministic);
+ * the chunk count weighs the chunks' time against the partials' traffic,
+ * and the size is 0 when no cut pays. A null or smaller workspace (and a
+ * size of 0) runs oga_fp8_linear's schedule.
  */
 int64_t oga_fp8_linear_workspace_bytes(int64_t m, int64_t n, int64_t k);
 
