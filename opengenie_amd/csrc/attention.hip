@@ -17,7 +17,8 @@
 // (b, h); wave w owns queries 32w .. 32w+31. Keys are visited 64 at a time;
 // the K and V tiles of a step (64 x 128 bf16 each) are copied to LDS by DMA
 // (global_load_lds_dwordx4) into a ring of kABufs (3) tile pairs, two steps
-// in flight.
+// in flight. For few keys (<= kShortSteps steps) the same kernel runs with 4
+// waves and two pairs, two workgroups per CU.
 //
 // Per step and wave, with v_mfma_f32_32x32x16_bf16:
 //  * S^T = K Q^T as two 32-key x 32-query blocks (8 MFMAs each over d):
@@ -54,9 +55,15 @@ constexpr int kAW = OGA_ATT_WAVES;         // waves per workgroup, 32 queries ea
 constexpr int kAQ = 32 * kAW;              // queries per workgroup
 constexpr int kAK = 64;                    // keys per step
 constexpr int kABufs = OGA_ATT_BUFS;       // K/V tile pairs in the LDS ring
-constexpr int kADmaI = 16 / kAW;           // DMA instructions per wave per tile
 static_assert(kAW == 4 || kAW == 8, "4 or 8 waves");
 static_assert(kABufs == 2 || kABufs == 3, "2 or 3 tile pairs");
+// Few keys (at most kShortSteps steps, the text cross-attention's 256): the
+// per-workgroup Q loads and O stores are then a large part of the time, so
+// the bf16 kernel runs with 4 waves and two tile pairs (64 KiB of LDS, one
+// wave per SIMD), two workgroups per CU, one's loads and stores under the
+// other's MFMAs; and no key split (its merge costs more than the shorter
+// last round gains).
+constexpr int kAWShort = 4, kABufsShort = 2, kShortSteps = 16;
 constexpr int kATileU4 = kAK * kAD * 2 / 16;  // uint4 per K (or V) tile: 1024 (16 KiB)
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -159,31 +166,34 @@ constexpr bool v_reads_conflict_free() {
 static_assert(v_reads_conflict_free(), "transposing V reads would conflict");
 static_assert(folded_offsets_match(), "folded LDS offsets differ from tile_off");
 
-// DMA of one 64-key tile of K or V (bf16 rows of kAD elements) into LDS:
-// instruction i of wave w fills tile rows 4b .. 4b+3 (b = kADmaI w + i); lane p
-// writes the 16 bytes at row 4b + p/16, physical chunk p%16, i.e. logical
-// chunk (p%16) ^ swz(row%16). `off[i]` is that source's byte offset from the
-// tile's first key row; in the last, partial step rows past the last key
-// re-read the last key.
+// DMA of one 64-key tile of K or V (bf16 rows of kAD elements) into LDS by
+// a workgroup of 16 / DI waves: instruction i of wave w fills tile rows
+// 4b .. 4b+3 (b = DI w + i); lane p writes the 16 bytes at row 4b + p/16,
+// physical chunk p%16, i.e. logical chunk (p%16) ^ swz(row%16). `off[i]` is
+// that source's byte offset from the tile's first key row; in the last,
+// partial step rows past the last key re-read the last key.
+template <int DI>
 struct TileSrc {
-  uint32_t off[kADmaI];
+  uint32_t off[DI];
 };
-OGA_DEVICE TileSrc tile_src(int64_t row_stride, int64_t first_key, int64_t nk, int wv, int lane, bool clamp) {
-  TileSrc t;
+template <int DI>
+OGA_DEVICE TileSrc<DI> tile_src(int64_t row_stride, int64_t first_key, int64_t nk, int wv, int lane, bool clamp) {
+  TileSrc<DI> t;
 #pragma unroll
-  for (int i = 0; i < kADmaI; ++i) {
-    const int row = (wv * kADmaI + i) * 4 + (lane >> 4);
+  for (int i = 0; i < DI; ++i) {
+    const int row = (wv * DI + i) * 4 + (lane >> 4);
     const int chunk = (lane & 15) ^ swz(row & 15);
     const int64_t r = clamp ? min((int64_t)row, nk - 1 - first_key) : (int64_t)row;
     t.off[i] = (uint32_t)(r * row_stride * 2 + chunk * 16);
   }
   return t;
 }
-OGA_DEVICE void tile_dma(const char* tile_base, const TileSrc& t, uint4* dst, int wv) {
+template <int DI>
+OGA_DEVICE void tile_dma(const char* tile_base, const TileSrc<DI>& t, uint4* dst, int wv) {
 #pragma unroll
-  for (int i = 0; i < kADmaI; ++i)
+  for (int i = 0; i < DI; ++i)
     __builtin_amdgcn_global_load_lds((const void*)(tile_base + t.off[i]),
-                                     (lds_void*)(dst + (wv * kADmaI + i) * 64), 16, 0, 0);
+                                     (lds_void*)(dst + (wv * DI + i) * 64), 16, 0, 0);
 }
 
 OGA_DEVICE uint32_t pack2(float a, float b) { return pack_bf16(a, b); }
@@ -228,13 +238,19 @@ OGA_DEVICE float sum_halves(float v) {
 
 
 // LDS: [K0 | V0 | K1 | V1 (| K2 | V2)], 16 KiB each; step st uses tile pair
-// st % kABufs, and the DMA of step st + kABufs - 1 goes out during step st.
+// st % BUFS, and the DMA of step st + BUFS - 1 goes out during step st.
 constexpr int kKBuf = 0, kVBuf = 16384, kParBytes = 32768;
 
-constexpr int kBfBufs = kABufs;  // K/V tile pairs in the bf16 kernel's ring
-static_assert(2 * kBfBufs * kATileU4 * 16 <= 160 * 1024, "LDS budget");
-
-__global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attention(AttnArgs a) {
+// W waves (4 or 8) of 32 queries, BUFS (2 or 3) K/V tile pairs in the ring.
+template <int W, int BUFS>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attention(AttnArgs a) {
+  static_assert(W == 4 || W == 8, "4 or 8 waves");
+  static_assert(BUFS == 2 || BUFS == 3, "2 or 3 tile pairs");
+  constexpr int kBfBufs = BUFS;
+  constexpr int kQB = 32 * W;   // queries per workgroup
+  constexpr int kDI = 16 / W;   // DMA instructions per wave per tile
+  static_assert(2 * kBfBufs * kATileU4 * 16 <= 160 * 1024, "LDS budget");
+  static_assert(W * 8192 <= 2 * kBfBufs * kATileU4 * 16, "the output staging fits the ring");
   __shared__ uint4 smem[2 * kBfBufs * kATileU4];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -255,7 +271,7 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int64_t bh = wg / a.nqb;
   const int h = (int)(bh % a.heads);
   const int64_t b = bh / a.heads;
-  const int64_t q0 = (int64_t)qb * kAQ + wv * 32;
+  const int64_t q0 = (int64_t)qb * kQB + wv * 32;
   const int hl = lane >> 5;  // lane half
   const int ql = lane & 31;
 
@@ -285,8 +301,8 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
   // l_run: this lane's part of the running sum (keys of lane half hl).
   float m_run = -INFINITY, l_run = 0.0f;
 
-  const TileSrc ksrc = tile_src(a.k_sn, 0, a.nk, wv, lane, false);
-  const TileSrc vsrc = tile_src(a.v_sn, 0, a.nk, wv, lane, false);
+  const TileSrc<kDI> ksrc = tile_src<kDI>(a.k_sn, 0, a.nk, wv, lane, false);
+  const TileSrc<kDI> vsrc = tile_src<kDI>(a.v_sn, 0, a.nk, wv, lane, false);
   auto dma_step = [&](int64_t s2, uint4* dK, uint4* dV) {
     const int64_t key0 = s2 * kAK;
     const char* kt = (const char*)(kbase + key0 * a.k_sn);
@@ -295,8 +311,8 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
       tile_dma(kt, ksrc, dK, wv);
       tile_dma(vt, vsrc, dV, wv);
     } else {
-      tile_dma(kt, tile_src(a.k_sn, key0, a.nk, wv, lane, true), dK, wv);
-      tile_dma(vt, tile_src(a.v_sn, key0, a.nk, wv, lane, true), dV, wv);
+      tile_dma(kt, tile_src<kDI>(a.k_sn, key0, a.nk, wv, lane, true), dK, wv);
+      tile_dma(vt, tile_src<kDI>(a.v_sn, key0, a.nk, wv, lane, true), dV, wv);
     }
   };
   // With three pairs the DMA runs two steps ahead; past the last step it
@@ -456,7 +472,7 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
   auto bar_dma = [&](auto par_c, int64_t st) {
     constexpr int PAR = decltype(par_c)::value;
     if (kBfBufs == 3)
-      asm volatile("s_waitcnt vmcnt(%0)" ::"i"(2 * kADmaI) : "memory");
+      asm volatile("s_waitcnt vmcnt(%0)" ::"i"(2 * kDI) : "memory");
     else
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     asm volatile("s_barrier" ::: "memory");
@@ -497,7 +513,7 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
     // A part of a split block (every wave of the workgroup takes this
     // branch, so none waits at the barriers below): O^T rows unnormalized,
     // with m_run and the query's sum over this part's keys.
-    const int64_t row = (int64_t)(blockIdx.x - a.nfull) * kAQ + wv * 32 + ql;
+    const int64_t row = (int64_t)(blockIdx.x - a.nfull) * kQB + wv * 32 + ql;
     float* po = a.part_o + row * kAD;
 #pragma unroll
     for (int dblk = 0; dblk < 4; ++dblk)
@@ -545,7 +561,8 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
 // 64s + 32h .. +31 of it; B = Q^T, the same bytes of query l%32, held in
 // registers. The accumulator layout, the masking and the online softmax are
 // the bf16 kernel's (lane l: query l%32, keys 8g + 4h + r of each 32-key
-// block). O^T = V^T P^T: B = P^T, lane l holding the e4m3 P of its own 32
+// block), except that the running max is exact (rescaled whenever it grows,
+// not lazily). O^T = V^T P^T: B = P^T, lane l holding the e4m3 P of its own 32
 // keys kappa(h, s) = 32(s/16) + 8((s%16)/4) + 4h + s%4 in k-slot s, so P
 // stays in its lane; A = V^T, lane l needing V[kappa(h, s)][d] for d-row
 // 32 dblk + l%32. k_fp8_v_transpose first rewrites V as vt [B, H, D, npad]
@@ -558,6 +575,7 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(2, 2))
 // (8(r%2) + c) ^ ((r/2)%8)) and the V^T tile (128 d-rows x 64 bytes, chunk c
 // of row d at c ^ ((d/4)%4)); three such 16 KiB pairs in a ring.
 constexpr int kF8Tile = kAK * kAD;  // bytes of a K or V^T tile: 8 KiB
+constexpr float kF8Offset = 8.0f;  // P = 2^(s - m + kF8Offset): the largest P is 256
 constexpr int kF8Pair = 2 * kF8Tile;
 constexpr int k8_off(int r, int c) { return (r >> 1) * 256 + (((r & 1) * 8 + c) ^ ((r >> 1) & 7)) * 16; }
 constexpr int vt_off(int d, int c) { return d * 64 + ((c ^ ((d >> 2) & 3)) << 4); }
@@ -734,9 +752,15 @@ __global__ __launch_bounds__(64 * kF8W) __attribute__((amdgpu_waves_per_eu(kF8W 
     vf[3] = lds_b256<KB + 3 * 2048>(vaddr[0], vaddr[1]);
   };
   // Online softmax of step st: masking past the last key, the running max
-  // (O and l rescaled when it grows by more than 2^8), P = 2^(s sl2 - m)
-  // <= 2^8 in float32 into l and as e4m3 (nearest even) into the B operand,
-  // byte 16j + e = P of accumulator e of block j.
+  // (O and l rescaled whenever it grows, as FlashAttention-3 keeps it), and
+  // P = 2^(s sl2 - m + 8) <= 2^8 with FlashAttention-3's FP8 offset of 8:
+  // the key at the maximum has P = 256 exactly, which e4m3 holds (a max
+  // allowed to lag would round that largest P too, an error of up to 2^-4 of
+  // the dominant term), and P down to 2^-6 (2^-14 of the largest) stay in
+  // e4m3's normal range. P goes in float32 into l and as e4m3 (nearest even)
+  // into the B operand, byte 16j + e = P of accumulator e of block j; the
+  // common factor 2^8 cancels in O / l (and in the key-split merge, which
+  // weights O and l alike).
   auto softmax = [&](int64_t st, f32x16(&sacc)[2], i32x8& pf) {
     const int64_t rem64 = a.nk - st * kAK;
     if (rem64 < kAK) {
@@ -753,7 +777,7 @@ __global__ __launch_bounds__(64 * kF8W) __attribute__((amdgpu_waves_per_eu(kF8W 
 #pragma unroll
       for (int e = (j == 0 ? 1 : 0); e < 16; ++e) mx = __builtin_fmaxf(mx, sacc[j][e]);
     const float ms = max_halves(mx) * sl2;
-    if (__any(ms > m_run + 8.0f)) {
+    if (__any(ms > m_run)) {
       const float m_new = __builtin_fmaxf(m_run, ms);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       l_run *= alpha;
@@ -763,7 +787,7 @@ __global__ __launch_bounds__(64 * kF8W) __attribute__((amdgpu_waves_per_eu(kF8W 
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
     }
-    const float nm = -m_run;
+    const float nm = kF8Offset - m_run;
     float ps0 = 0.0f, ps1 = 0.0f;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -990,23 +1014,38 @@ extern "C" int oga_fp8_dequant_per_head(const void* x8, const float* descale, vo
 }
 
 namespace {
-// Workgroups of k_attention resident at once on the current device (CUs x
-// workgroups per CU), cached per device (relaxed atomics: threads filling an
-// entry at once store the same value); 0 if the runtime cannot say.
-int64_t attention_slots(bool fp8 = false) {
-  static std::atomic<int64_t> cache[2][64];
+// The attention kernels: the bf16 kernel for many keys and for few
+// (kShortSteps), and the FP8 kernel.
+enum AttnKernel { kBf16Long = 0, kBf16Short = 1, kFp8 = 2 };
+struct AttnCfg {
+  const void* fn;
+  int threads, qpb;
+};
+AttnCfg attn_cfg(AttnKernel k) {
+  switch (k) {
+    case kBf16Short: return {(const void*)k_attention<kAWShort, kABufsShort>, 64 * kAWShort, 32 * kAWShort};
+    case kFp8: return {(const void*)k_attention_fp8, 64 * kF8W, kF8Q};
+    default: return {(const void*)k_attention<kAW, kABufs>, 64 * kAW, kAQ};
+  }
+}
+AttnKernel bf16_kernel(int64_t nk) { return (nk + kAK - 1) / kAK <= kShortSteps ? kBf16Short : kBf16Long; }
+
+// Workgroups of an attention kernel resident at once on the current device
+// (CUs x workgroups per CU), cached per device (relaxed atomics: threads
+// filling an entry at once store the same value); 0 if the runtime cannot say.
+int64_t attention_slots(AttnKernel kern) {
+  static std::atomic<int64_t> cache[3][64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  int64_t n = cache[fp8][dev].load(std::memory_order_relaxed);
+  int64_t n = cache[kern][dev].load(std::memory_order_relaxed);
   if (n == 0) {
+    const AttnCfg c = attn_cfg(kern);
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fp8 ? k_attention_fp8 : k_attention,
-                                                     fp8 ? 64 * kF8W : 64 * kAW, 0) !=
-            hipSuccess)
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, c.fn, c.threads, 0) != hipSuccess)
       return 0;
     n = (int64_t)cus * per_cu > 0 ? (int64_t)cus * per_cu : -1;
-    cache[fp8][dev].store(n, std::memory_order_relaxed);
+    cache[kern][dev].store(n, std::memory_order_relaxed);
   }
   return n > 0 ? n : 0;
 }
@@ -1018,12 +1057,16 @@ struct AttnPlan {
 // Blocks beyond the last whole round of the CUs are cut into k parts over
 // their key steps (k <= 8 and <= the steps) when that shortens the last
 // round by at least a tenth of a round: rem blocks in k parts take
-// ceil(k rem / slots) rounds of 1/k of a block's time.
+// ceil(k rem / slots) rounds of 1/k of a block's time. Not for kShortSteps
+// steps or fewer: a block's time is then mostly its Q loads and O stores,
+// which every part repeats, and the merge adds a launch (at 256 keys the
+// split ran 75.7 against 66.9 us unsplit).
 AttnPlan attention_plan(int64_t wgs, int64_t nk, int64_t slots) {
   AttnPlan p{wgs, wgs, 0, 1};
   const int64_t rem = slots > 0 ? wgs % slots : 0;
   if (rem == 0) return p;
   const int64_t nsteps = (nk + kAK - 1) / kAK;
+  if (nsteps <= kShortSteps) return p;
   double best = 1.0;
   for (int k = 2; k <= 8 && k <= nsteps; ++k) {
     const double c = (double)((k * rem + slots - 1) / slots) / k;
@@ -1060,25 +1103,32 @@ int attention_run(const void* q, const int64_t q_strides[3], const void* k, cons
   a.o_sb = o_strides[0]; a.o_sn = o_strides[1]; a.o_sh = o_strides[2];
   a.nq = nq; a.nk = nk; a.heads = (int)heads;
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
-  const int64_t nqb = (nq + kAQ - 1) / kAQ;
+  const AttnKernel kern = bf16_kernel(nk);
+  const AttnCfg cfg = attn_cfg(kern);
+  const int64_t nqb = (nq + cfg.qpb - 1) / cfg.qpb;
   const int64_t wgs = nqb * heads * batch;
   if (nqb > INT32_MAX || wgs > UINT32_MAX / 8) return unsupported("too many query blocks");
   a.nqb = (int)nqb;
-  a.qpb = kAQ;
+  a.qpb = cfg.qpb;
   AttnPlan plan{wgs, wgs, 0, 1};
   if (workspace_bytes > 0) {
-    plan = attention_plan(wgs, nk, attention_slots());
-    if (attention_ws_bytes(plan, kAQ) > workspace_bytes) return fail("workspace smaller than oga_attention_workspace_bytes");
+    plan = attention_plan(wgs, nk, attention_slots(kern));
+    if (attention_ws_bytes(plan, cfg.qpb) > workspace_bytes)
+      return fail("workspace smaller than oga_attention_workspace_bytes");
   }
   a.nfull = plan.nfull;
   a.ksplit = plan.ksplit;
   a.part_o = (float*)workspace;
-  a.part_ml = plan.units ? (float*)workspace + plan.units * kAQ * kAD : nullptr;
+  a.part_ml = plan.units ? (float*)workspace + plan.units * cfg.qpb * kAD : nullptr;
   a.xcd_remap = plan.nfull % 8 == 0;
-  hipLaunchKernelGGL(k_attention, dim3((unsigned)(plan.nfull + plan.units)), dim3(64 * kAW), 0,
-                     (hipStream_t)stream, a);
+  if (kern == kBf16Short)
+    hipLaunchKernelGGL((k_attention<kAWShort, kABufsShort>), dim3((unsigned)(plan.nfull + plan.units)),
+                       dim3(cfg.threads), 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL((k_attention<kAW, kABufs>), dim3((unsigned)(plan.nfull + plan.units)), dim3(cfg.threads), 0,
+                       (hipStream_t)stream, a);
   if (plan.units) {
-    const int64_t rows = (wgs - plan.nfull) * kAQ;
+    const int64_t rows = (wgs - plan.nfull) * cfg.qpb;
     hipLaunchKernelGGL(k_attention_combine, dim3((unsigned)((rows * (kAD / 8) + 255) / 256)), dim3(256), 0,
                        (hipStream_t)stream, a, rows);
   }
@@ -1132,7 +1182,7 @@ int attention_fp8_run(const void* q, const int64_t q_strides[3], const void* k, 
   if (nqb > INT32_MAX || wgs > UINT32_MAX / 8) return unsupported("too many query blocks");
   a.nqb = (int)nqb;
   a.qpb = kF8Q;
-  AttnPlan plan = attention_plan(wgs, nk, attention_slots(true));
+  AttnPlan plan = attention_plan(wgs, nk, attention_slots(kFp8));
   if (vtb + attention_ws_bytes(plan, kF8Q) > workspace_bytes) plan = AttnPlan{wgs, wgs, 0, 1};
   a.nfull = plan.nfull;
   a.ksplit = plan.ksplit;
@@ -1165,9 +1215,11 @@ extern "C" int oga_attention(const void* q, const int64_t q_strides[3], const vo
 extern "C" int64_t oga_attention_workspace_bytes(int64_t batch, int64_t nq, int64_t nk, int64_t heads,
                                                  int64_t head_dim) {
   if (batch <= 0 || nq <= 0 || nk <= 0 || heads <= 0 || head_dim != kAD) return 0;
-  const int64_t nqb = (nq + kAQ - 1) / kAQ;
+  const AttnKernel kern = bf16_kernel(nk);
+  const int qpb = attn_cfg(kern).qpb;
+  const int64_t nqb = (nq + qpb - 1) / qpb;
   if (nqb > INT32_MAX || heads > INT32_MAX || nqb * heads > (int64_t)(UINT32_MAX / 8) / batch) return 0;
-  return attention_ws_bytes(attention_plan(nqb * heads * batch, nk, attention_slots()), kAQ);
+  return attention_ws_bytes(attention_plan(nqb * heads * batch, nk, attention_slots(kern)), qpb);
 }
 
 extern "C" int oga_attention_ws(const void* q, const int64_t q_strides[3], const void* k, const int64_t k_strides[3],
@@ -1184,7 +1236,7 @@ extern "C" int64_t oga_attention_fp8_workspace_bytes(int64_t batch, int64_t nq, 
   const int64_t nqb = (nq + kF8Q - 1) / kF8Q;
   if (nqb > INT32_MAX || heads > 65535 || batch > 65535) return 0;
   return vt_bytes(batch, heads, nk) +
-         attention_ws_bytes(attention_plan(nqb * heads * batch, nk, attention_slots(true)), kF8Q);
+         attention_ws_bytes(attention_plan(nqb * heads * batch, nk, attention_slots(kFp8)), kF8Q);
 }
 
 extern "C" int oga_attention_fp8_ws(const void* q8, const int64_t q_strides[3], const void* k8,

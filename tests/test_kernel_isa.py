@@ -86,11 +86,20 @@ def test_barrier_check_sees_a_missing_wait():
 @pytest.mark.skipif(not os.path.exists("/opt/rocm/bin/hipcc") and not os.environ.get("HIPCC"),
                     reason="hipcc not present")
 def test_attention_barriers_wait_for_lds_dma():
-    body = _kernel_body(_device_asm(os.path.join(CSRC, "attention.hip")), "k_attention")
-    n_barriers = sum(1 for ins in body if ins == "s_barrier")
-    assert n_barriers >= 2
-    assert any("load_lds" in ins for ins in body)
-    assert barrier_violations(body, max_vmcnt=4) == []
+    """Both instances of the bf16 kernel: 8 waves with three tile pairs (the
+    wait may leave the next step's 4 DMA instructions in flight) and 4 waves
+    with two pairs (nothing may stay in flight: the next DMA goes into the
+    pair the step after reads)."""
+    asm = _device_asm(os.path.join(CSRC, "attention.hip"))
+    seen = set()
+    for mangled, max_vmcnt in (("k_attentionILi8ELi3EE", 4), ("k_attentionILi4ELi2EE", 0)):
+        body = _kernel_body(asm, mangled)
+        seen.add(mangled)
+        n_barriers = sum(1 for ins in body if ins == "s_barrier")
+        assert n_barriers >= 2, mangled
+        assert any("load_lds" in ins for ins in body), mangled
+        assert barrier_violations(body, max_vmcnt=max_vmcnt) == [], mangled
+    assert len(seen) == 2
 
 
 @pytest.mark.skipif(not os.path.exists("/opt/rocm/bin/hipcc") and not os.environ.get("HIPCC"),
