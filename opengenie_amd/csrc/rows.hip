@@ -432,22 +432,16 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
   // A wave past the batch's V waves takes no rows but joins the fill.
   const int64_t t_first = v < V ? v : a.tokens;
 
-  // The first row's loads, then the constant loads (table rows and, when
-  // shared, the timestep row). Every one is unconditional (a wave without
+  // The constant loads (table rows and, when shared, the timestep row),
+  // then the first row's loads. Every one is unconditional (a wave without
   // rows loads row tokens - 1 and stores nothing; a thread past the column
   // groups repeats group gi % G and writes the same values): a branch around
   // a load would make the compiler wait for every outstanding load at its
-  // merge. The rows go first so that they are in flight as early as
-  // possible; the fill then waits for them too (loads complete in order),
-  // which costs nothing since the wave needs its row next anyway.
-  const uint16_t* const xb = a.x + b * a.tokens * C + lane * 8;
-  uint16_t* const yb = a.out + b * a.tokens * C + lane * 8;
-  uint4 xv[CH];
-  {
-    const int64_t tl = t_first < a.tokens ? t_first : a.tokens - 1;
-#pragma unroll
-    for (int j = 0; j < CH; ++j) xv[j] = *(const uint4*)(xb + tl * C + j * 512);
-  }
+  // merge. Loads complete in order, so with the constants first the fill and
+  // its barrier wait for them alone and run while the row is still in
+  // flight (rows first made the fill wait for the row too: 6.47 against
+  // 6.41 us at 1x2304x4096, 13.71 against 13.44 us with per-token
+  // timesteps).
   Raw8<TD> tr0[GPT], tr1[GPT];
   Raw8<D0> u0[GPT];
   Raw8<D1> u1[GPT];
@@ -462,6 +456,14 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
       u0[q] = raw8_load<D0>(a.s0.ts, a.s0.ts_off + b * a.s0.ts_sb + gi * 8);
       u1[q] = raw8_load<D1>(a.s1.ts, a.s1.ts_off + b * a.s1.ts_sb + gi * 8);
     }
+  }
+  const uint16_t* const xb = a.x + b * a.tokens * C + lane * 8;
+  uint16_t* const yb = a.out + b * a.tokens * C + lane * 8;
+  uint4 xv[CH];
+  {
+    const int64_t tl = t_first < a.tokens ? t_first : a.tokens - 1;
+#pragma unroll
+    for (int j = 0; j < CH; ++j) xv[j] = *(const uint4*)(xb + tl * C + j * 512);
   }
   // Constants to LDS.
 #pragma unroll
