@@ -954,17 +954,36 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
 
 // Sum of the K-chunk partials of the split tiles, in chunk order, then the
 // epilogue of k_fp8_gemm_ring: out = R(R(sum * sa * sb) + R(bias)). One
-// thread per 4 accumulators of the GEMM: float4 index f of a tile's chunk is
-// (wave, (i * 4 + j) * 4 + q, lane), output row wm*128 + 32j + lane%32,
-// columns wn*128 + 32i + 8q + 4(lane/32) + 0..3; consecutive threads read
-// consecutive float4s of every chunk.
+// workgroup per (split tile, wave quarter): the quarter's 4096 float4s of a
+// chunk are the accumulators of one wave of the GEMM, float4 f = (block b =
+// (i * 4 + j) * 4 + q, lane) holding row 32j + lane%32, columns 32i + 8q +
+// 4(lane/32) + 0..3 of the quarter's 128 x 128 outputs. Thread t sums float4s
+// t, t + 256, ... of every chunk (whole 4 KiB per wave and load), rounds
+// R(sum * s) to bf16 and stages it in LDS in row order; after the barrier each
+// thread reads 16-byte pieces of rows, adds R(bias) and stores them, so every
+// wave's store covers four whole 256-byte row pieces.
+constexpr int kReduceRow = 264;  // bytes per staged row of 128 bf16 (+8: the 32 rows of a write hit 64 banks)
+constexpr bool reduce_writes_conflict_free() {
+  // a half-wave (32 lanes, one lane%32 each: rows 32j + 0..31 at one column
+  // pair) writes 8 bytes per lane: 64 distinct banks
+  for (int half = 0; half < 2; ++half) {
+    unsigned long long banks = 0;
+    for (int fr = 0; fr < 32; ++fr) {
+      const int bk = ((fr * kReduceRow + half * 8) >> 2) & 63;
+      if ((banks >> bk) & 3ull) return false;
+      banks |= 3ull << bk;
+    }
+  }
+  return true;
+}
+static_assert(reduce_writes_conflict_free(), "reduce staging writes would conflict");
 __global__ __launch_bounds__(256) void k_fp8_splitk_reduce(GemmArgs g) {
   constexpr int kPerTile = kWaves * 64 * 64;  // float4s per tile chunk
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int x = (int)(gid / kPerTile), f = (int)(gid % kPerTile);
-  const int wv = f >> 12, b = (f >> 6) & 63, lane = f & 63;
-  const int wm = wv >> 1, wn = wv & 1, fr = lane & 31, fh = lane >> 5;
-  const int i = b >> 4, j = (b >> 2) & 3, q = b & 3;
+  constexpr int kPerWave = 64 * 64;            // float4s of one wave's accumulators
+  __shared__ __attribute__((aligned(16))) uint8_t stage[128 * kReduceRow];
+  const int x = blockIdx.x >> 2, wv = blockIdx.x & 3;
+  const int wm = wv >> 1, wn = wv & 1;
+  const int tid = threadIdx.x;
   const int t = g.nfull + x;
   const int per_group = kGroupM * g.tiles_n;
   const int grp = t / per_group;
@@ -972,24 +991,57 @@ __global__ __launch_bounds__(256) void k_fp8_splitk_reduce(GemmArgs g) {
   const int gsize = min(g.tiles_m - first_m, kGroupM);
   const int n0 = ((t % per_group) / gsize) * GN;
   const int gi = n0 / g.group_n;  // the tile's group (uniform per workgroup)
-  const int row = (first_m + (t % per_group) % gsize) * GM + wm * 128 + 32 * j + fr;
-  const int col = n0 - gi * g.group_n + wn * 128 + 32 * i + 8 * q + 4 * fh;  // inside the group
-  const f32x4* const p = (const f32x4*)g.ws + (int64_t)x * g.split * kPerTile + f;
-  f32x4 sum = p[0];
-  for (int c = 1; c < g.split; ++c) sum += p[(int64_t)c * kPerTile];
-  if (row >= g.m || col >= g.group_n) return;
+  const int row0 = (first_m + (t % per_group) % gsize) * GM + wm * 128;
+  const int col0 = n0 - gi * g.group_n + wn * 128;  // inside the group
   const float sc = g.sa[0] * pick(g.sbg, gi)[0];
-  const uint16_t* const bias = (const uint16_t*)pick(g.biasg, gi);
-  float o[4];
+  const f32x4* const p = (const f32x4*)g.ws + (int64_t)x * g.split * kPerTile + wv * kPerWave;
+  f32x4 sum[16];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float bb = bias ? __uint_as_float(((uint32_t)bias[col + e]) << 16) : -0.0f;
-    o[e] = rbf(sum[e] * sc) + bb;
+  for (int k = 0; k < 16; ++k) sum[k] = p[tid + 256 * k];
+  for (int c = 1; c < g.split; ++c) {
+    f32x4 v[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = p[(int64_t)c * kPerTile + tid + 256 * k];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) sum[k] += v[k];
   }
-  uint2 pk;
-  pk.x = pack_bf16(o[0], o[1]);
-  pk.y = pack_bf16(o[2], o[3]);
-  *(uint2*)(pick(g.outg, gi) + (int64_t)row * g.ldo + col) = pk;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int f = tid + 256 * k;
+    const int b = f >> 6, lane = f & 63;
+    const int i = b >> 4, j = (b >> 2) & 3, q = b & 3;
+    const int r = 32 * j + (lane & 31);
+    const int cc = 32 * i + 8 * q + 4 * (lane >> 5);
+    uint2 pk;
+    pk.x = pack_bf16(rbf(sum[k][0] * sc), rbf(sum[k][1] * sc));
+    pk.y = pack_bf16(rbf(sum[k][2] * sc), rbf(sum[k][3] * sc));
+    *(uint2*)(stage + r * kReduceRow + cc * 2) = pk;
+  }
+  __syncthreads();
+  const uint16_t* const bias = (const uint16_t*)pick(g.biasg, gi);
+  uint16_t* const out = pick(g.outg, gi);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int idx = tid + 256 * k;
+    const int r = idx >> 4, c8 = idx & 15;
+    const int row = row0 + r, col = col0 + 8 * c8;
+    if (row >= g.m || col >= g.group_n) continue;
+    const uint2 lo = *(const uint2*)(stage + r * kReduceRow + c8 * 16);
+    const uint2 hi = *(const uint2*)(stage + r * kReduceRow + c8 * 16 + 8);
+    const uint32_t w[4] = {lo.x, lo.y, hi.x, hi.y};
+    uint4 bw = {0u, 0u, 0u, 0u};
+    if (bias) bw = *(const uint4*)(bias + col);
+    const uint32_t bb[4] = {bw.x, bw.y, bw.z, bw.w};
+    uint32_t y[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      // bf16 pairs: the low half is the lower column; no bias adds -0
+      const float b0 = bias ? __uint_as_float(bb[e] << 16) : -0.0f;
+      const float b1 = bias ? __uint_as_float(bb[e] & 0xFFFF0000u) : -0.0f;
+      y[e] = pack_bf16(__uint_as_float(w[e] << 16) + b0, __uint_as_float(w[e] & 0xFFFF0000u) + b1);
+    }
+    *(uint4*)(out + (int64_t)row * g.ldo + col) = make_uint4(y[0], y[1], y[2], y[3]);
+  }
 }
 
 }  // namespace oga
@@ -1080,8 +1132,7 @@ int launch_ring(GemmArgs& g, void* workspace, int64_t workspace_bytes, hipStream
     grid = g.units < cus ? g.units : cus;
     g.xcd_remap = (g.units % 8) == 0 && (grid % 8) == 0;
     hipLaunchKernelGGL(k_fp8_gemm_ring<true>, dim3((unsigned)grid), dim3(64 * kWaves), 0, stream, g);
-    hipLaunchKernelGGL(k_fp8_splitk_reduce, dim3((unsigned)((nt - p.nfull) * kWaves * 64 * 64 / 256)), dim3(256), 0,
-                       stream, g);
+    hipLaunchKernelGGL(k_fp8_splitk_reduce, dim3((unsigned)((nt - p.nfull) * kWaves)), dim3(256), 0, stream, g);
   }
   return launch_status();
 }
