@@ -155,6 +155,18 @@ int oga_video_rmsnorm_rope(const void* x, const void* weight, int weight_dtype, 
                            const int64_t sin_strides[4], void* out, int64_t batch, int64_t tokens,
                            int64_t cols, int64_t heads, float eps, void* stream);
 
+/*
+ * The attention module's q/k RMSNorm where no RoPE follows: the text
+ * cross-attention's `attn_module.q_norm(q)`, `attn_module.k_norm(k)`
+ * (triton_ltx_ops.py:1866-1867, the PytorchPreAttention path taken with
+ * pe = None), i.e. torch.nn.functional.rms_norm over the last dimension.
+ * x, out: (rows, cols) bf16 contiguous, cols in {2048, 4096}; weight (cols,)
+ * bf16 or f32, or NULL for none. out = R(x * inv * w) (w = 1 without a
+ * weight), inv = 1/sqrt(mean(x^2) + eps), rounded once.
+ */
+int oga_rmsnorm(const void* x, const void* weight, int weight_dtype, void* out, int64_t rows, int64_t cols,
+                float eps, void* stream);
+
 /* `fused_video_qk_bias_rmsnorm_rope` (triton_ltx_ops.py:508-587): q and k
  * first become R(q + R(q_bias)), R(k + R(k_bias)). */
 int oga_video_qk_bias_rmsnorm_rope(const void* q, const void* k, const void* q_bias, const void* k_bias,

@@ -49,6 +49,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                          _i64, _i64, _f32, _p]),
     "oga_video_rmsnorm_rope": (_i32, [_p, _p, _i32, _p, _p, _i32, _i64p, _i64p, _p, _i64, _i64, _i64, _i64, _f32,
                                       _p]),
+    "oga_rmsnorm": (_i32, [_p, _p, _i32, _p, _i64, _i64, _f32, _p]),
     "oga_video_qk_bias_rmsnorm_rope": (_i32, [_p, _p, _p, _p, _i32, _p, _p, _i32, _p, _p, _i32, _i64p, _i64p, _p,
                                               _p, _i64, _i64, _i64, _i64, _f32, _p]),
     "oga_video_qkv_rmsnorm_rope_pack": (_i32, [_p, _p, _p, _p, _p, _i32, _p, _p, _i32, _i64p, _i64p, _p, _i64,

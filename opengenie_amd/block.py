@@ -182,7 +182,9 @@ def video_text_cross_attention(block: VideoBlock, vx: torch.Tensor, context: tor
     `fuse_context` (default: `fuse_norm`) takes the reference's
     _FUSE_VIDEO_TEXT_CONTEXT_ADALN path (:2839-2850, off in its production):
     the context affine of the prompt table's rows 0/1 as one AdaLN-affine
-    launch, the same expression as the torch form beside it."""
+    launch, the same expression as the torch form beside it. With `fuse_norm`
+    the q/k RMSNorms (the module's q_norm/k_norm with no RoPE after them,
+    :1866-1867) run as `qk_rmsnorm` launches instead of torch's rms_norm."""
     a = block.attn2
     b = vx.shape[0]
     if fuse_context is None:
@@ -200,15 +202,19 @@ def video_text_cross_attention(block: VideoBlock, vx: torch.Tensor, context: tor
     else:
         normed = _rms_norm(vx, block.eps)
         attn_in = L.fused_adaln_affine_from_ada(normed, block.table, timesteps, shift_index=6, scale_index=7)
-    q = _rms_norm(L.fp8_linear_forward(a.to_q, attn_in), block.eps, a.q_norm_weight)
-    k = _rms_norm(L.fp8_linear_forward(a.to_k, enc), block.eps, a.k_norm_weight)
+    qk_norm = L.qk_rmsnorm if fuse_norm else (lambda x, w, eps: _rms_norm(x, eps, w))
+    qp = L.fp8_linear_forward(a.to_q, attn_in)
+    kp = L.fp8_linear_forward(a.to_k, enc)
+    q = qk_norm(qp, a.q_norm_weight, block.eps)
+    k = qk_norm(kp, a.k_norm_weight, block.eps)
     v = L.fp8_linear_forward(a.to_v, enc)
     o = attention_video(q, k, v, a.heads)
     ca = L.fp8_linear_forward(a.to_out, o)
     out = L.fused_residual_gate_from_ada(vx, ca, block.table, timesteps, gate_index=8, count_video_ada=False)
     if stages is not None:
-        for name, val in (("ca.x", vx), ("ca.enc", enc), ("ca.normed", normed), ("ca.in", attn_in), ("ca.q", q),
-                          ("ca.k", k), ("ca.v", v), ("ca.attn", o), ("ca.proj", ca), ("ca.out", out)):
+        for name, val in (("ca.x", vx), ("ca.enc", enc), ("ca.normed", normed), ("ca.in", attn_in), ("ca.qp", qp),
+                          ("ca.kp", kp), ("ca.q", q), ("ca.k", k), ("ca.v", v), ("ca.attn", o), ("ca.proj", ca),
+                          ("ca.out", out)):
             stages[name] = val
     return out
 

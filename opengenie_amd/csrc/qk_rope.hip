@@ -117,7 +117,9 @@ OGA_DEVICE uint4 rope8(const uint4& nv, const float* cs, const float* sn, bool s
 
 // Grid (blocks_per_batch, batch); a 4-wave workgroup stages the norm weights
 // (and biases) in LDS as float, then each wave strides over token rows.
-template <int CH, int NT, bool BIAS, bool PACK, int CDT, bool VEC>
+// ROPE false: the plain RMSNorm n = R(x * inv * w) (w = 1 without a weight),
+// with no cos/sin and no partner exchange.
+template <int CH, int NT, bool BIAS, bool PACK, int CDT, bool VEC, bool ROPE = true>
 __global__ __launch_bounds__(256) void k_rmsnorm_rope(RopeArgs a) {
   constexpr int C = CH * 512;
   __shared__ float W0[C];
@@ -131,7 +133,12 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rope(RopeArgs a) {
 #pragma unroll 1
   for (int c0 = tid * 8; c0 < C; c0 += 256 * 8) {
     float v[8];
-    load8(a.w0, a.w_dt, c0, 1, true, v);
+    if (ROPE || a.w0) {
+      load8(a.w0, a.w_dt, c0, 1, true, v);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = 1.0f;
+    }
     lds_put8(W0, c0, v);
     if (NT == 2) {
       load8(a.w1, a.w_dt, c0, 1, true, v);
@@ -176,7 +183,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rope(RopeArgs a) {
     const int64_t cbase = b * a.c_sb + t * a.c_st + hd0;
     const int64_t sbase = b * a.s_sb + t * a.s_st + hd0;
     Raw8<CDT> cr[VEC ? CH : 1], sr[VEC ? CH : 1];
-    if (VEC) {
+    if (ROPE && VEC) {
 #pragma unroll
       for (int j = 0; j < CH; ++j) {
         const int64_t head = j * 4 + (lane >> 4);
@@ -189,6 +196,12 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rope(RopeArgs a) {
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       const int c0 = j * 512 + lane * 8;
+      if constexpr (!ROPE) {
+        st_nt16(a.o0 + r * a.out_stride + c0, norm8(x0[j], W0, c0, inv0));
+        if (NT == 2) st_nt16(a.o1 + r * a.out_stride + c0, norm8(x1[j], W1, c0, inv1));
+        __builtin_amdgcn_sched_barrier(0);
+        continue;
+      }
       const int64_t head = j * 4 + (lane >> 4);
       float cs[8], sn[8];
       if (VEC) {
@@ -307,6 +320,34 @@ extern "C" int oga_video_rmsnorm_rope(const void* x, const void* weight, int wei
   if (!aligned(out, 16)) return fail("output must be 16-byte aligned");
   a.o0 = (uint16_t*)out;
   return launch_rope<1, false, false>(a, batch, (hipStream_t)stream);
+}
+
+extern "C" int oga_rmsnorm(const void* x, const void* weight, int weight_dtype, void* out, int64_t rows,
+                           int64_t cols, float eps, void* stream) {
+  RopeArgs a{};
+  if (cols != 2048 && cols != 4096) return unsupported("cols must be 2048 or 4096");
+  if (rows < 0) return fail("bad shape");
+  if (!x || !out) return fail("null pointer");
+  if (weight && !dt_ok(weight_dtype)) return fail("weight dtype must be bf16 or f32");
+  if (!aligned(x, 16) || !aligned(out, 16)) return fail("x and out must be 16-byte aligned");
+  if (weight && !aligned(weight, 8 * dt_size(weight_dtype))) return fail("weight must be aligned to 8 elements");
+  if (rows == 0) return OGA_OK;
+  a.x0 = (const uint16_t*)x;
+  a.w0 = weight;
+  a.w_dt = weight_dtype;
+  a.o0 = (uint16_t*)out;
+  a.tokens = rows;
+  a.cols = (int)cols;
+  a.out_stride = cols;
+  a.eps = eps;
+  const dim3 grid = balanced_row_grid(1, rows);
+  if (cols == 4096)
+    hipLaunchKernelGGL((k_rmsnorm_rope<8, 1, false, false, OGA_DT_BF16, false, false>), grid, dim3(256), 0,
+                       (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL((k_rmsnorm_rope<4, 1, false, false, OGA_DT_BF16, false, false>), grid, dim3(256), 0,
+                       (hipStream_t)stream, a);
+  return launch_status();
 }
 
 extern "C" int oga_video_qk_bias_rmsnorm_rope(const void* q, const void* k, const void* q_bias, const void* k_bias,

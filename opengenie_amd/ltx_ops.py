@@ -39,6 +39,7 @@ __all__ = [
     "fused_video_qkv_rmsnorm_rope_pack",
     "fused_video_qk_rmsnorm_rope_separate",
     "fused_video_qk_bias_rmsnorm_rope",
+    "qk_rmsnorm",
     "fused_residual_gate_bf16",
     "fused_head_gate_mul_bf16",
     "fused_residual_gate_from_ada",
@@ -749,6 +750,28 @@ def fused_video_qk_bias_rmsnorm_rope(q, k, q_bias, k_bias, q_weight, k_weight, e
               _dt(qw), _ptr(cos), _ptr(sin), _dt(cos), cst, sst, _ptr(q_out), _ptr(k_out), q.shape[0], q.shape[1],
               q.shape[2], cos.shape[1], float(eps), _stream(q))
     return q_out, k_out
+
+
+def qk_rmsnorm(x: torch.Tensor, weight: torch.Tensor | None, eps: float) -> torch.Tensor:
+    """The attention module's q/k RMSNorm where no RoPE follows (the text
+    cross-attention, pe = None: `attn_module.q_norm(q)` / `k_norm(k)`,
+    :1866-1867): torch.nn.functional.rms_norm over the last dimension, one
+    rounding of x * inv * w. Runs the RMSNorm pass of the preattention kernel
+    without its rotation for bf16 x with 2048 or 4096 columns; otherwise the
+    torch expression."""
+    cols = x.shape[-1] if x.dim() else 0
+    ok = (x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous() and cols in (2048, 4096)
+          and (weight is None or (weight.shape == (cols,) and weight.is_cuda
+                                  and weight.dtype in (torch.bfloat16, torch.float32))))
+    if not ok:
+        _fallback("qk_rmsnorm", x)
+        return torch.nn.functional.rms_norm(x, (cols,), weight=weight, eps=eps)
+    w = None if weight is None else weight.contiguous()
+    out = torch.empty_like(x)
+    _hip("qk_rmsnorm")
+    _lib.call("oga_rmsnorm", _ptr(x), _ptr(w), _dt(w) if w is not None else _lib.DT_BF16, _ptr(out),
+              x.numel() // cols, cols, float(eps), _stream(x))
+    return out
 
 
 def fused_video_qkv_rmsnorm_rope_pack(q, k, v, q_weight, k_weight, eps, cos, sin) -> torch.Tensor | None:

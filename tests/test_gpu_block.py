@@ -109,6 +109,7 @@ def test_block_steps_match_oracle(gated, fuse_gelu):
     # or the context affine (with the fusions, where the query side is AdaZero)
     assert calls.get("fused_adaln_affine_from_ada", 0) == 1, calls
     assert calls.get("fused_adazero_from_ada", 0) == (3 if gated else 2), calls
+    assert calls.get("qk_rmsnorm", 0) == (2 if gated else 0), calls
     tab, tsT = to_T(blk.table), to_T(ts)
     a1, a2 = blk.attn1, blk.attn2
 
@@ -139,6 +140,14 @@ def test_block_steps_match_oracle(gated, fuse_gelu):
         assert (bf16_ulp_distance(np32(st["ca.normed"]), nref.v) <= 1).all()
         ref = O.adaln_affine_from_ada(to_T(st["ca.normed"]), tab, tsT, 6, 7)
     assert_same_bits(np32(st["ca.in"]), ref.v, "ca.in")
+    _check_linear(st["ca.qp"], _lin_ref(a2.to_q, to_T(st["ca.in"])), "ca.qp")
+    _check_linear(st["ca.kp"], _lin_ref(a2.to_k, to_T(st["ca.enc"])), "ca.kp")
+    for nm, w in (("q", a2.q_norm_weight), ("k", a2.k_norm_weight)):
+        nref = O.rms_norm(to_T(st[f"ca.{nm}p"]), EPS, to_T(w))
+        if gated:  # qk_rmsnorm: bit for bit
+            assert_same_bits(np32(st[f"ca.{nm}"]), nref.v, f"ca.{nm}")
+        else:  # torch's rms_norm on the GPU: within one bf16 step
+            assert (bf16_ulp_distance(np32(st[f"ca.{nm}"]), nref.v) <= 1).all(), f"ca.{nm}"
     _check_attn(st["ca.attn"], _attn_ref(st["ca.q"], st["ca.k"], st["ca.v"]), st["ca.v"], "ca.attn")
     _check_linear(st["ca.proj"], _lin_ref(a2.to_out, to_T(st["ca.attn"])), "ca.proj")
     ref = O.residual_gate_from_ada(to_T(st["ca.x"]), to_T(st["ca.proj"]), tab, tsT, 8)

@@ -469,6 +469,47 @@ def test_video_qk_rmsnorm_rope_separate_and_pack_and_bias():
     assert_same_bits(out_np(bk), rbk.v, "bias k")
 
 
+# ------------------------------------------------------------ q/k RMSNorm without RoPE
+@pytest.mark.parametrize("rows,cols,w_dtype", [
+    (37, 4096, torch.bfloat16), (1, 4096, torch.float32), (256, 4096, None), (300, 2048, torch.bfloat16),
+    # more rows than the grid has waves: several rows per wave
+    (20000, 2048, torch.bfloat16)])
+def test_qk_rmsnorm(rows, cols, w_dtype):
+    from opengenie_amd import ltx_ops as L
+
+    x = randn((1, rows, cols), 990 + rows, std=2.0)
+    w = None if w_dtype is None else randn((cols,), 991, dtype=w_dtype, std=0.05, mean=1.0)
+    got = L.qk_rmsnorm(g(x), None if w is None else g(w), 1e-6)
+    assert got.shape == x.shape and got.dtype == torch.bfloat16
+    ref = O.rms_norm(to_T(x), 1e-6, None if w is None else to_T(w))
+    assert_same_bits(out_np(got), ref.v, f"qk_rmsnorm {rows}x{cols}")
+    _ran("qk_rmsnorm")
+
+
+def test_qk_rmsnorm_special_values():
+    """Each element is its own R(x * inv * w), as in torch's rms_norm: signed
+    zeros keep their sign next to negative values, a row with an infinity or
+    a NaN goes as torch's does, and an all-zero row takes inv = 1/sqrt(eps)."""
+    from opengenie_amd import ltx_ops as L
+
+    cols = 4096
+    x = randn((8, cols), 995)
+    x[0, ::2] = -0.0
+    x[0, 1::2] = -x[0, 1::2].abs()
+    x[1, 5] = float("inf")
+    x[2, 77] = float("nan")
+    x[3] = 0.0
+    x[3, ::3] = -0.0
+    x[4] = (x[4].float() * 1e-30).to(torch.bfloat16)  # squares below float32's range
+    x[5, 0] = float("-inf")
+    w = randn((cols,), 996, std=0.05, mean=1.0)
+    w[64:80] = -w[64:80]
+    got = L.qk_rmsnorm(g(x), g(w), 1e-6)
+    ref = O.rms_norm(to_T(x), 1e-6, to_T(w))
+    assert_same_bits(out_np(got), ref.v, "qk_rmsnorm special values")
+    assert np.signbit(out_np(got)[0, ::2]).any()
+
+
 # ------------------------------------------------------------ FP8 linear
 def _fp8_weights(n, k, seed):
     wf = randn((n, k), seed, dtype=torch.float32, std=0.02)
