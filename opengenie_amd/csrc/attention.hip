@@ -561,8 +561,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 // 64s + 32h .. +31 of it; B = Q^T, the same bytes of query l%32, held in
 // registers. The accumulator layout, the masking and the online softmax are
 // the bf16 kernel's (lane l: query l%32, keys 8g + 4h + r of each 32-key
-// block), except that the running max is exact (rescaled whenever it grows,
-// not lazily). O^T = V^T P^T: B = P^T, lane l holding the e4m3 P of its own 32
+// block), except that the running max lags by at most 0.8 (not 8), which
+// keeps every P of the offset form below e4m3's 448. O^T = V^T P^T: B = P^T,
+// lane l holding the e4m3 P of its own 32
 // keys kappa(h, s) = 32(s/16) + 8((s%16)/4) + 4h + s%4 in k-slot s, so P
 // stays in its lane; A = V^T, lane l needing V[kappa(h, s)][d] for d-row
 // 32 dblk + l%32. k_fp8_v_transpose first rewrites V as vt [B, H, D, npad]
@@ -575,7 +576,11 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 // (8(r%2) + c) ^ ((r/2)%8)) and the V^T tile (128 d-rows x 64 bytes, chunk c
 // of row d at c ^ ((d/4)%4)); three such 16 KiB pairs in a ring.
 constexpr int kF8Tile = kAK * kAD;  // bytes of a K or V^T tile: 8 KiB
-constexpr float kF8Offset = 8.0f;  // P = 2^(s - m + kF8Offset): the largest P is 256
+constexpr float kF8Offset = 8.0f;  // P = 2^(s - m + kF8Offset): a row's largest P is >= 256
+// How far a row's scores may pass the running max before O and l are
+// rescaled: 2^(8 + 0.8) = 445.7 stays below e4m3's largest finite 448.
+constexpr float kF8Lag = 0.8f;
+static_assert(kF8Offset + kF8Lag < 8.807f, "P must stay below 448 = 2^8.807");
 constexpr int kF8Pair = 2 * kF8Tile;
 constexpr int k8_off(int r, int c) { return (r >> 1) * 256 + (((r & 1) * 8 + c) ^ ((r >> 1) & 7)) * 16; }
 constexpr int vt_off(int d, int c) { return d * 64 + ((c ^ ((d >> 2) & 3)) << 4); }
@@ -751,16 +756,18 @@ __global__ __launch_bounds__(64 * kF8W) __attribute__((amdgpu_waves_per_eu(kF8W 
     vf[2] = lds_b256<KB + 2 * 2048>(vaddr[0], vaddr[1]);
     vf[3] = lds_b256<KB + 3 * 2048>(vaddr[0], vaddr[1]);
   };
-  // Online softmax of step st: masking past the last key, the running max
-  // (O and l rescaled whenever it grows, as FlashAttention-3 keeps it), and
-  // P = 2^(s sl2 - m + 8) <= 2^8 with FlashAttention-3's FP8 offset of 8:
-  // the key at the maximum has P = 256 exactly, which e4m3 holds (a max
-  // allowed to lag would round that largest P too, an error of up to 2^-4 of
-  // the dominant term), and P down to 2^-6 (2^-14 of the largest) stay in
-  // e4m3's normal range. P goes in float32 into l and as e4m3 (nearest even)
-  // into the B operand, byte 16j + e = P of accumulator e of block j; the
-  // common factor 2^8 cancels in O / l (and in the key-split merge, which
-  // weights O and l alike).
+  // Online softmax of step st: masking past the last key, the running max m
+  // and P = 2^(s sl2 - m + 8) with FlashAttention-3's FP8 offset of 8. The
+  // max lags by at most kF8Lag: O and l are rescaled only when some query's
+  // scores pass m + kF8Lag, so every P <= 2^(8 + kF8Lag) < 448 stays finite
+  // in e4m3, the largest P of a row is >= 256 (m never exceeds the row's
+  // true max), and P down to 2^-6 stay in e4m3's normal range, where nearest
+  // even errs by at most 2^-4 of P. (Without the offset a lagging max leaves
+  // the largest P as small as 1 and pushes the small ones into e4m3's
+  // subnormals.) P goes in float32 into l and as e4m3 into the B operand,
+  // byte 16j + e = P of accumulator e of block j; the common factor 2^8
+  // cancels in O / l (and in the key-split merge, which weights O and l
+  // alike).
   auto softmax = [&](int64_t st, f32x16(&sacc)[2], i32x8& pf) {
     const int64_t rem64 = a.nk - st * kAK;
     if (rem64 < kAK) {
@@ -777,7 +784,7 @@ __global__ __launch_bounds__(64 * kF8W) __attribute__((amdgpu_waves_per_eu(kF8W 
 #pragma unroll
       for (int e = (j == 0 ? 1 : 0); e < 16; ++e) mx = __builtin_fmaxf(mx, sacc[j][e]);
     const float ms = max_halves(mx) * sl2;
-    if (__any(ms > m_run)) {
+    if (__any(ms > m_run + kF8Lag)) {
       const float m_new = __builtin_fmaxf(m_run, ms);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       l_run *= alpha;

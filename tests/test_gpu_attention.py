@@ -211,11 +211,13 @@ def _fp8_exact(t8: torch.Tensor, ds: torch.Tensor) -> np.ndarray:
 def _fp8_rounding_bound(qe: np.ndarray, ke: np.ndarray, ve: np.ndarray) -> np.ndarray:
     """Per-element bound, from the rounding model, of what rounding P to e4m3
     (nearest even) does to the output, for [B, N, H, D] float64 inputs. The
-    kernel keeps the running max exact with FlashAttention-3's FP8 offset, so
-    every P = 2^(s - m + 8) <= 256 and the largest is 256 (exact in e4m3).
+    kernel's running max m lags a row's true max by at most 0.8 (base 2),
+    with FlashAttention-3's FP8 offset, so every P = 2^(s - m + 8) is below
+    2^8.8 < 448 (finite in e4m3) and a row's largest P is at least 256.
     Rounding moves a P in e4m3's normal range by at most 2^-4 P and one below
-    2^-6 (spacing 2^-9) by at most 2^-10, i.e. 2^-18 in units of the largest
-    P; so, with p_j = exp(s_j - max) and l = sum_j p_j (float32, unrounded):
+    2^-6 (spacing 2^-9) by at most 2^-10, i.e. 2^-18 in units of 256 or of
+    the largest P; so, with p_j = exp(s_j - max) and l = sum_j p_j (float32,
+    unrounded):
         |out - ref| <= (2^-4 sum_j p_j |v_j| + 2^-18 sum_j |v_j|) / l.
     A key split keeps the bound: each part's P are relative to its own max,
     which is at most the global one."""
