@@ -93,11 +93,13 @@ def make_fp8_linear_inputs(seed: int, device: str, m: int = M, k: int = K, n: in
     return x, s_in, w, s_w, bias
 
 
-def _graph_time_us(fn, reps: int = 20, inner: int = 25, rounds: int = 3) -> float:
+def _graph_time_us(fn, reps: int = 20, inner: int = 25, rounds: int = 3, settle_s: float = 0.3) -> float:
     """Mean per-call GPU time of fn: `inner` calls captured in one HIP graph,
-    the graph replayed `reps` times between two events on the capture stream;
-    the best of `rounds` such measurements (the first one after a change of
-    workload runs on a clock that is still settling)."""
+    replayed for `settle_s` seconds first (the clock after a change of
+    workload takes that long to settle), then `reps` times between two
+    events on the capture stream; the best of `rounds` such measurements."""
+    import time
+
     import torch
 
     s = torch.cuda.Stream()
@@ -113,6 +115,10 @@ def _graph_time_us(fn, reps: int = 20, inner: int = 25, rounds: int = 3) -> floa
             fn()
     graph.replay()
     torch.cuda.synchronize()
+    t0 = time.time()
+    while time.time() - t0 < settle_s:
+        graph.replay()
+        torch.cuda.synchronize()
     st = torch.cuda.current_stream()
     best = float("inf")
     for _ in range(rounds):
@@ -214,14 +220,15 @@ def fused_op_rows(seed: int) -> dict:
     table = (torch.randn((6, C), generator=g, device=dev) * 0.02).to(torch.bfloat16)
     ts = (torch.randn((1, 1, 6 * C), generator=g, device=dev) * 0.5).to(torch.bfloat16).expand(1, 2304, 6 * C)
     fn = lambda: L.fused_adazero_from_ada(x, 1e-6, table, ts, shift_index=0, scale_index=1)  # noqa: E731
-    rec("adazero_from_ada", 2 * 2304 * C * 2 + 2 * C * 2 * 2, _graph_time_us(fn), "x(1,2304,4096) ts broadcast", fn)
+    rec("adazero_from_ada", 2 * 2304 * C * 2 + 2 * C * 2 * 2, _graph_time_us(fn, reps=5, inner=100),
+        "x(1,2304,4096) ts broadcast", fn)
     del x, table, ts
 
     # FP8 input quantizer at 9216 x 4096.
     xq = torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
     sq = torch.tensor(0.05, device=dev)
     fn = lambda: L.fused_fp8_quantize_e4m3(xq, sq)  # noqa: E731
-    rec("fp8_quantize_e4m3", M * K * 3, _graph_time_us(fn), "x(9216,4096)", fn)
+    rec("fp8_quantize_e4m3", M * K * 3, _graph_time_us(fn, reps=5, inner=100), "x(9216,4096)", fn)
 
     # GELU-tanh quantizer on the FFN hidden (9216, 16384): the down-projection's input.
     xh = (torch.randn((M, 4 * K), generator=g, device=dev) * 2.0).to(torch.bfloat16)
@@ -432,7 +439,8 @@ def copy_reference(graph: bool = True, reps: int = 10) -> dict:
         a = torch.empty(n, device="cuda", dtype=torch.bfloat16).normal_()
         b = torch.empty_like(a)
         if graph:
-            us = _graph_time_us(lambda: b.copy_(a), reps=10, inner=10)
+            small = n * 4 < 200_000_000  # 100 calls per graph for the small copy, as for the small ops
+            us = _graph_time_us(lambda: b.copy_(a), reps=5 if small else 10, inner=100 if small else 10)
         else:
             st = torch.cuda.current_stream()
             b.copy_(a)

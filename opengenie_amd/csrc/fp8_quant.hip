@@ -240,10 +240,31 @@ __global__ __launch_bounds__(256) void k_head_scale_quant(const uint16_t* x, con
   const int h = blockIdx.y;
   const int64_t b = blockIdx.z;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  // The chunk's x slices are loaded first, so that they are in flight with
+  // the partials below (a slice past the last token re-reads the last one
+  // and is not stored: no branch around a load).
+  constexpr int NI = kQuantTokens / TPP;
+  const int sub = threadIdx.x % LPT, tk = threadIdx.x / LPT;
+  const int64_t t0 = (int64_t)blockIdx.x * kQuantTokens;
+  const int64_t t1 = min(t0 + kQuantTokens, tokens);
+  uint4 xv[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int64_t t = min(t0 + tk + i * TPP, t1 - 1);
+    xv[i] = *(const uint4*)(x + ((b * tokens + t) * heads + h) * D + sub * 8);
+  }
   // Partials are magnitudes as float32 bit patterns: their integer maximum
   // is the amax, NaN if any element of the head was NaN.
+  // Four loads per thread and pass, all in flight with the x slices (an
+  // index past the last partial re-reads it, which leaves the maximum).
   uint32_t m = 0;
-  for (int c = threadIdx.x; c < nchunk; c += 256) m = max(m, __float_as_uint(partial[(b * heads + h) * nchunk + c]));
+  const float* const ph = partial + (b * heads + h) * nchunk;
+  for (int c0 = threadIdx.x; c0 < nchunk; c0 += 1024) {
+    uint32_t v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = __float_as_uint(ph[min(c0 + 256 * k, nchunk - 1)]);
+    m = max(m, max(max(v[0], v[1]), max(v[2], v[3])));
+  }
   m = umax_dpp(umax_dpp(umax_dpp(umax_dpp(m, 0), 1), 2), 3);
   m = max(m, (uint32_t)__builtin_amdgcn_ds_swizzle((int)m, 0x401F));
   m = max((uint32_t)__builtin_amdgcn_readlane((int)m, 0), (uint32_t)__builtin_amdgcn_readlane((int)m, 32));
@@ -275,18 +296,19 @@ __global__ __launch_bounds__(256) void k_head_scale_quant(const uint16_t* x, con
     qv = fmaf(fmaf(-s, qv, n), r, qv);
     return __builtin_amdgcn_div_fixupf(qv, s, n);
   };
-  const int sub = threadIdx.x % LPT, tk = threadIdx.x / LPT;
-  const int64_t t0 = (int64_t)blockIdx.x * kQuantTokens;
-  const int64_t t1 = min(t0 + kQuantTokens, tokens);
-  for (int64_t t = t0 + tk; t < t1; t += TPP) {
-    const int64_t e0 = ((b * tokens + t) * heads + h) * D + sub * 8;
-    float f[8];
-    unpack8(*(const uint4*)(x + e0), f);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) f[i] = clamp448(div(f[i]));
-    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-    const u32x2 o = {e4m3x4(f[0], f[1], f[2], f[3]), e4m3x4(f[4], f[5], f[6], f[7])};
-    __builtin_nontemporal_store(o, (u32x2*)(q + e0));
+  for (int i = 0; i < NI; ++i) {
+    const int64_t t = t0 + tk + i * TPP;
+    if (t < t1) {
+      const int64_t e0 = ((b * tokens + t) * heads + h) * D + sub * 8;
+      float f[8];
+      unpack8(xv[i], f);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) f[k] = clamp448(div(f[k]));
+      typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+      const u32x2 o = {e4m3x4(f[0], f[1], f[2], f[3]), e4m3x4(f[4], f[5], f[6], f[7])};
+      __builtin_nontemporal_store(o, (u32x2*)(q + e0));
+    }
   }
 }
 
