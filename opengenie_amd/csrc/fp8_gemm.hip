@@ -994,6 +994,12 @@ __global__ __launch_bounds__(256) void k_fp8_splitk_reduce(GemmArgs g) {
   const int row0 = (first_m + (t % per_group) % gsize) * GM + wm * 128;
   const int col0 = n0 - gi * g.group_n + wn * 128;  // inside the group
   const float sc = g.sa[0] * pick(g.sbg, gi)[0];
+  // R(bias) of the 8 columns this thread stores (the same in every pass
+  // below), loaded once, first (without a bias, -0.0, which an add leaves
+  // every value as it is).
+  const uint16_t* const bias = (const uint16_t*)pick(g.biasg, gi);
+  const int c8 = tid & 15;
+  const uint4 bw = *(const uint4*)(bias ? bias + min(col0 + 8 * c8, g.group_n - 8) : kNegZeroRow + 8 * c8);
   const f32x4* const p = (const f32x4*)g.ws + (int64_t)x * g.split * kPerTile + wv * kPerWave;
   f32x4 sum[16];
 #pragma unroll
@@ -1018,28 +1024,21 @@ __global__ __launch_bounds__(256) void k_fp8_splitk_reduce(GemmArgs g) {
     *(uint2*)(stage + r * kReduceRow + cc * 2) = pk;
   }
   __syncthreads();
-  const uint16_t* const bias = (const uint16_t*)pick(g.biasg, gi);
   uint16_t* const out = pick(g.outg, gi);
+  const uint32_t bb[4] = {bw.x, bw.y, bw.z, bw.w};
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
-    const int idx = tid + 256 * k;
-    const int r = idx >> 4, c8 = idx & 15;
+    const int r = (tid + 256 * k) >> 4;
     const int row = row0 + r, col = col0 + 8 * c8;
     if (row >= g.m || col >= g.group_n) continue;
     const uint2 lo = *(const uint2*)(stage + r * kReduceRow + c8 * 16);
     const uint2 hi = *(const uint2*)(stage + r * kReduceRow + c8 * 16 + 8);
     const uint32_t w[4] = {lo.x, lo.y, hi.x, hi.y};
-    uint4 bw = {0u, 0u, 0u, 0u};
-    if (bias) bw = *(const uint4*)(bias + col);
-    const uint32_t bb[4] = {bw.x, bw.y, bw.z, bw.w};
     uint32_t y[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      // bf16 pairs: the low half is the lower column; no bias adds -0
-      const float b0 = bias ? __uint_as_float(bb[e] << 16) : -0.0f;
-      const float b1 = bias ? __uint_as_float(bb[e] & 0xFFFF0000u) : -0.0f;
-      y[e] = pack_bf16(__uint_as_float(w[e] << 16) + b0, __uint_as_float(w[e] & 0xFFFF0000u) + b1);
-    }
+    for (int e = 0; e < 4; ++e)  // bf16 pairs: the low half is the lower column
+      y[e] = pack_bf16(__uint_as_float(w[e] << 16) + __uint_as_float(bb[e] << 16),
+                       __uint_as_float(w[e] & 0xFFFF0000u) + __uint_as_float(bb[e] & 0xFFFF0000u));
     *(uint4*)(out + (int64_t)row * g.ldo + col) = make_uint4(y[0], y[1], y[2], y[3]);
   }
 }
