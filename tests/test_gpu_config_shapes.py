@@ -19,6 +19,10 @@ Shapes:
   Q/K RMSNorm+RoPE   (1, 9216, 4096) with the (16, 18, 32) grid table
   per-head FP8       (1, 9216, 32, 128)
   FP8 quantizer      (9216, 4096) with 0.1 % outliers x50, amax/448 scale
+  FP8 linear         9216 x 4096 -> 16384 (nine whole rounds), 16384 -> 4096
+                     and 4096 -> 4096 (split-K tails), grouped Q/K/V 4096 ->
+                     3 x 4096: sampled rows against the oracle, the bias
+                     epilogue on every element
 """
 
 from __future__ import annotations
@@ -240,3 +244,86 @@ def test_fp8_quantize_config_shape(zero_dim):
     got = q.view(torch.uint8).cpu().numpy()
     assert np.array_equal(nan_canon(got), nan_canon(ref))
     assert (np.abs(x.float().numpy()) > 40).sum() > 9216 * C // 5000  # the outliers are there
+
+
+# ------------------------------------------------------------ FP8 linear at 9216 tokens
+def _linear_rows_check(got_rows: np.ndarray, ref_rows: np.ndarray) -> None:
+    """The FP8 linear's bar against the float64-accumulated oracle (as the
+    small-shape tests): rtol 1e-2 with an outlier allowance of 1e-5 at most
+    two bf16 steps (the MFMA's own accumulation rounding next to a power of
+    two), and fewer than 1 % of outputs more than one step away."""
+    from tests.helpers import bf16_ulp_distance
+
+    close = np.isclose(got_rows, ref_rows, rtol=1e-2, atol=1e-3 * float(np.abs(ref_rows).max()))
+    assert (~close).mean() < 1e-5, int((~close).sum())
+    assert (bf16_ulp_distance(got_rows[~close], ref_rows[~close]) <= 2).all()
+    assert (bf16_ulp_distance(got_rows, ref_rows) > 1).mean() < 1e-2
+
+
+@pytest.mark.parametrize("n,k", [(16384, 4096), (4096, 16384), (4096, 4096)],
+                         ids=["up_4096_to_16384", "down_16384_to_4096", "proj_4096_to_4096"])
+def test_fp8_linear_config_shapes(n, k):
+    """The FP8 linear at 9216 tokens on the schedules the benchmark times:
+    4096 -> 16384 is 2304 tiles, nine whole rounds of the persistent kernel;
+    16384 -> 4096 and 4096 -> 4096 are two whole rounds, then the split-K
+    tail (4 and 2 K-chunks) and its reduce. Config 2's data: x ~N(0,1) with
+    0.1 % of the entries x50, per-tensor amax/448 scales, W from N(0,0.02),
+    bf16 bias ~N(0,0.01). Every 127th row (and the last) against the oracle
+    at the GEMM bar; every element of the biased output equal to
+    R(out_nobias + R(bias)) from the unbiased call on the same schedule."""
+    from opengenie_amd import _lib
+    from opengenie_amd.ltx_ops import fp8_scaled_mm
+
+    m = 9216
+    lib = _lib.load()
+    split = int(lib.oga_fp8_linear_workspace_bytes(m, n, k)) > 0
+    assert split == (n == 4096)  # the N = 4096 shapes leave a partial last round
+    gg = gen(20260601 + n + k)
+    xf = torch.randn((m, k), generator=gg)
+    idx = torch.randperm(m * k, generator=gg)[: m * k // 1000]
+    xf.view(-1)[idx] *= 50.0
+    x = xf.to(torch.bfloat16)
+    sa = (x.float().abs().amax() / 448.0).reshape(())
+    a = torch.clamp(x.float() / sa, -448, 448).to(torch.float8_e4m3fn)
+    wf = torch.randn((n, k), generator=gg) * 0.02
+    sb = (wf.abs().amax() / 448.0).reshape(())
+    w = torch.clamp(wf / sb, -448, 448).to(torch.float8_e4m3fn)
+    bias = (torch.randn((n,), generator=gg) * 0.01).to(torch.bfloat16)
+    ga, gw, gsa, gsb, gb = g(a), g(w), g(sa), g(sb), g(bias)
+    out = fp8_scaled_mm(ga, gw, gsa, gsb, gb)
+    out0 = fp8_scaled_mm(ga, gw, gsa, gsb, None)
+    _ran("fp8_scaled_mm")
+    want = (out0.float() + gb.float()).to(torch.bfloat16)  # R(out_nobias + R(bias)), bias already bf16
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    rows = np.unique(np.concatenate([np.arange(0, m, 127), [m - 1]]))
+    a_codes = a.view(torch.uint8).numpy()
+    ref = O.fp8_linear(a_codes[rows], w.view(torch.uint8).numpy(), float(sa), float(sb), to_T(bias))
+    got = out_np(out)[rows]
+    _linear_rows_check(got, ref)
+
+
+def test_fp8_grouped_qkv_config_shape():
+    """The grouped Q/K/V projection at 9216 tokens (one launch over the 1728
+    tiles of the three 4096 -> 4096 linears, 6.75 rounds of the CUs, no split)
+    with each linear's own weight scale and bias: every 127th row of q, k and
+    v against the oracle at the GEMM bar."""
+    from opengenie_amd import ltx_ops as L
+    from opengenie_amd.block import random_video_block
+
+    blk = random_video_block(C, 32, seed=41, gated=False)
+    a = blk.attn1
+    x = (torch.randn((1, 9216, C), generator=gen(20260611))).to(torch.bfloat16)
+    qkv = L.fp8_qkv_from_grouped_mm(a, g(x))
+    assert qkv is not None
+    _ran("fp8_grouped_linear")
+    rows = np.unique(np.concatenate([np.arange(0, 9216, 127), [9215]]))
+    for lin, got_t in zip((a.to_q, a.to_k, a.to_v), qkv):
+        # the input codes as torch computes them on the GPU (x times the
+        # float32 reciprocal of the 0-dim scale; torch's CPU division differs
+        # in about 2 % of the codes)
+        s_in = float(lin.input_scale.float().cpu())
+        xq = O.fp8_quantize_e4m3(to_T(x), s_in, True, device="cuda").reshape(9216, C)
+        ref = O.fp8_linear(xq[rows], lin.weight.cpu().view(torch.uint8).numpy(), s_in,
+                           float(lin.weight_scale.float().cpu()), to_T(lin.bias.cpu()))
+        got = out_np(got_t).reshape(9216, -1)[rows]
+        _linear_rows_check(got, ref)
