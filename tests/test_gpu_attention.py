@@ -357,3 +357,34 @@ def test_fp8_attention_config_shape_against_bf16():
     ref = O.attention(*[np.ascontiguousarray(x.transpose(0, 2, 1, 3)) for x in (qe, ke, ve)]).transpose(0, 2, 1, 3)
     got = out.float().cpu().numpy()[:, rows][:, :, heads]
     _check_fp8(got, ref, _fp8_rounding_bound(qe, ke, ve), "fp8 config 5 sampled rows")
+
+
+def test_attention_config_shape():
+    """Config 5 on the bf16 kernel: q, k, v (1, 9216, 32, 128) ~N(0,1), the
+    schedule the benchmark times (1152 blocks of 256 queries: 4.5 rounds of
+    the CUs, the last round's blocks cut in key parts and merged). Every
+    31st query row of four heads, among them the two last (whose blocks
+    fall in the key-split round), against float64 attention at the bf16
+    bar above."""
+    from opengenie_amd import _lib
+    from opengenie_amd.attention import flash_attn_func
+
+    n, h = 9216, 32
+    lib = _lib.load()
+    assert int(lib.oga_attention_workspace_bytes(1, n, n, h, 128)) > 0  # the key split is planned
+    q, k, v = (randn((1, n, h, 128), 960 + i) for i in range(3))
+    out = flash_attn_func(q.to(DEV), k.to(DEV), v.to(DEV))
+    torch.cuda.synchronize()
+    _ran("flash_attn_func")
+    rows = np.unique(np.concatenate([np.arange(0, n, 31), [n - 1]]))
+    qn, kn, vn = (np32(t).astype(np.float64) for t in (q, k, v))
+    got = out.float().cpu().numpy().astype(np.float64)
+    for head in (0, 13, 30, 31):
+        s = qn[0, rows, head] @ kn[0, :, head].T * 128 ** -0.5
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        ref = (p @ vn[0, :, head]) / p.sum(axis=1, keepdims=True)
+        err = np.abs(got[0, rows, head] - ref)
+        worst = float((err / (2e-3 + 2e-2 * np.abs(ref))).max())
+        rms_rel = float(np.sqrt((err ** 2).mean()) / np.sqrt((ref ** 2).mean()))
+        print(f"attention 1x9216x32x128 head {head}: worst/bound {worst:.3f} rms_rel {rms_rel:.3e}")
+        assert worst <= 1.0 and rms_rel < 4e-3, (head, worst, rms_rel)
