@@ -63,6 +63,8 @@ def _fp8_kernel_ok(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, descales) 
             return False
     if q.shape[0] != k.shape[0] or k.shape != v.shape or q.shape[2] != k.shape[2] or k.shape[1] < 1:
         return False
+    if not 0 <= k.stride(1) <= 1 << 26 or k.shape[1] > 1 << 25:  # the kernel's 32-bit DMA offsets
+        return False
     b, h = q.shape[0], q.shape[2]
     return b <= 65535 and h <= 65535 and all(d.is_cuda and d.numel() == b * h for d in descales)
 

@@ -704,7 +704,11 @@ __global__ __launch_bounds__(64 * kF8W) __attribute__((amdgpu_waves_per_eu(kF8W 
   const int krow = 2 * kL + (kv >> 3);
   const uint32_t koff_c = (uint32_t)((kv & 7) * 16);
   const int vd_row = 16 * wd + (lane >> 2);
-  const int64_t vt_src = vd_row * a.vt_npad + (((lane & 3) ^ ((vd_row >> 2) & 3)) * 16);
+  // Per-lane byte offsets from the step's first key (32 bits: the host keeps
+  // 64 key rows of K and 128 d-rows of V^T below 2^32 bytes), added to a
+  // wave-uniform base, so a step's DMA addresses cost no 64-bit vector math.
+  const uint32_t vt_src = (uint32_t)(vd_row * a.vt_npad) + (uint32_t)(((lane & 3) ^ ((vd_row >> 2) & 3)) * 16);
+  const uint32_t k_src = (uint32_t)(krow * a.k_sn) + koff_c;
   // LDS destinations (wave-uniform): the wave's 1 KiB of the pair's K and
   // V^T tiles, or, for a wave past the eighth, its own 2 KiB after the ring.
   const bool tile_wave = wv < kF8DmaW;
@@ -712,10 +716,12 @@ __global__ __launch_bounds__(64 * kF8W) __attribute__((amdgpu_waves_per_eu(kF8W 
   const int v_dst = tile_wave ? kF8Tile / 16 + wv * 64 : kF8DummyOff / 16 + (wv - kF8DmaW) * 128 + 64;
   auto dma_step = [&](int64_t s2, uint4* dst) {
     const int64_t key0 = s2 * kAK;
-    const int64_t r = min((int64_t)krow, a.nk - 1 - key0);
     uint4* const kd = tile_wave ? dst + k_dst : smem + k_dst;
     uint4* const vdp = tile_wave ? dst + v_dst : smem + v_dst;
-    __builtin_amdgcn_global_load_lds((const void*)(kbase + (key0 + r) * a.k_sn + koff_c), (lds_void*)kd, 16, 0, 0);
+    // Rows past the last key (the last, partial step) re-read the last key.
+    const int last = (int)min((int64_t)(kAK - 1), a.nk - 1 - key0);
+    const uint32_t ko = krow <= last ? k_src : (uint32_t)(last * a.k_sn) + koff_c;
+    __builtin_amdgcn_global_load_lds((const void*)(kbase + key0 * a.k_sn + ko), (lds_void*)kd, 16, 0, 0);
     __builtin_amdgcn_global_load_lds((const void*)(vtbase + key0 + vt_src), (lds_void*)vdp, 16, 0, 0);
   };
   dma_step(st_begin, smem);
@@ -1162,6 +1168,10 @@ int attention_fp8_run(const void* q, const int64_t q_strides[3], const void* k, 
   if (batch == 0 || nq == 0 || heads == 0) return OGA_OK;
   if (nk == 0) return unsupported("no keys");
   if (heads > 65535 || batch > 65535) return unsupported("batch and heads must be below 65536");
+  // The DMA's per-lane offsets are 32-bit: 64 key rows of K and 128 d-rows
+  // of the rewritten V^T (nk padded to 64) stay below 2^32 bytes.
+  if (k_strides[1] < 0 || k_strides[1] > (int64_t(1) << 26)) return unsupported("key token stride out of range");
+  if (nk > (int64_t(1) << 25)) return unsupported("more than 2^25 keys");
   for (const int64_t* st : {q_strides, k_strides, v_strides})
     for (int i = 0; i < 3; ++i)
       if (st[i] % 16) return fail("e4m3 strides must be multiples of 16 elements");
