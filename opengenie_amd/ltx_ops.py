@@ -760,13 +760,15 @@ def qk_rmsnorm(x: torch.Tensor, weight: torch.Tensor | None, eps: float) -> torc
     without its rotation for bf16 x with 2048 or 4096 columns; otherwise the
     torch expression."""
     cols = x.shape[-1] if x.dim() else 0
+    w = None if weight is None else weight.contiguous()
     ok = (x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous() and cols in (2048, 4096)
-          and (weight is None or (weight.shape == (cols,) and weight.is_cuda
-                                  and weight.dtype in (torch.bfloat16, torch.float32))))
+          and x.data_ptr() % 16 == 0
+          and (w is None or (w.shape == (cols,) and w.device == x.device
+                             and w.dtype in (torch.bfloat16, torch.float32)
+                             and w.data_ptr() % (8 * w.element_size()) == 0)))
     if not ok:
         _fallback("qk_rmsnorm", x)
         return torch.nn.functional.rms_norm(x, (cols,), weight=weight, eps=eps)
-    w = None if weight is None else weight.contiguous()
     out = torch.empty_like(x)
     _hip("qk_rmsnorm")
     _lib.call("oga_rmsnorm", _ptr(x), _ptr(w), _dt(w) if w is not None else _lib.DT_BF16, _ptr(out),
