@@ -295,19 +295,22 @@ def block_rows(seed: int, reps: int = 5, ctx_tokens: int = 256) -> dict:
     sin = torch.randn((1, 32, M, 64), generator=g, device="cuda").clamp(-1, 1).to(torch.bfloat16)
     st = torch.cuda.current_stream()
     rows = {}
-    for fuse in (False, True):
+    for key in ("production_flags", "mi355x_fusions", "mi355x_fusions_ada_quant"):
         # production flags; then the MI355X-side fusions (grouped Q/K/V,
         # rms_norm + AdaLN as one AdaZero, GELU in the down-projection's
-        # quantizer)
+        # quantizer); then also each AdaZero that feeds an FP8 linear writing
+        # that linear's e4m3 input
+        fuse = key != "production_flags"
+        aq = key == "mi355x_fusions_ada_quant"
         parts = {"self_attention": [], "text_cross_attention": [], "feed_forward": [], "block": []}
         for rep in range(reps + 2):
             ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
             ev[0].record(st)
-            x1 = B.video_self_attention(blk, vx, ts, cos, sin, qkv_grouped=fuse)
+            x1 = B.video_self_attention(blk, vx, ts, cos, sin, qkv_grouped=fuse, fuse_ada_quant=aq)
             ev[1].record(st)
-            x2 = B.video_text_cross_attention(blk, x1, ctx, ts, pts, fuse_norm=fuse)
+            x2 = B.video_text_cross_attention(blk, x1, ctx, ts, pts, fuse_norm=fuse, fuse_ada_quant=aq)
             ev[2].record(st)
-            B.video_feed_forward(blk, x2, ts, fuse_gelu_quant=fuse)
+            B.video_feed_forward(blk, x2, ts, fuse_gelu_quant=fuse, fuse_ada_quant=aq)
             ev[3].record(st)
             ev[3].synchronize()
             if rep < 2:
@@ -315,7 +318,6 @@ def block_rows(seed: int, reps: int = 5, ctx_tokens: int = 256) -> dict:
             for i, k in enumerate(("self_attention", "text_cross_attention", "feed_forward")):
                 parts[k].append(ev[i].elapsed_time(ev[i + 1]) * 1000.0)
             parts["block"].append(ev[0].elapsed_time(ev[3]) * 1000.0)
-        key = "mi355x_fusions" if fuse else "production_flags"
         rows[key] = {k: round(statistics.median(v), 1) for k, v in parts.items()}
     rows["shape"] = f"vx (1,{M},4096), text context (1,{ctx_tokens},4096), 32 heads, FFN 16384; us per call"
     return rows

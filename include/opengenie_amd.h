@@ -48,6 +48,24 @@ int oga_adazero_from_ada(const void* x, void* y, int64_t batch, int64_t tokens, 
                          int shift_index, int scale_index, float eps, void* stream);
 
 /*
+ * AdaZero from the Ada table straight into e4m3 codes: the composition of
+ * `fused_adazero_from_ada` (triton_ltx_ops.py:40-91) and the input
+ * quantizer of the FP8Linear that consumes its output (triton_ltx_ops.py:
+ * 1691-1709 -> `fused_fp8_quantize_e4m3` :144-161). No single counterpart
+ * in the reference; the codes equal quantizing oga_adazero_from_ada's bf16
+ * output with oga_fp8_quantize_e4m3, and the bf16 rows never reach memory.
+ * Arguments as oga_adazero_from_ada; q: (batch*tokens, cols) bytes;
+ * input_scale: one float32 on the device (scale_zero_dim != 0 for a 0-dim
+ * scale tensor, whose reciprocal and products round to bf16 as torch's).
+ * Needs 16-byte table and timestep rows.
+ */
+int oga_adazero_from_ada_fp8(const void* x, void* q, int64_t batch, int64_t tokens, int64_t cols,
+                             const void* table, int table_dtype, int64_t tab_s0, int64_t tab_s1,
+                             const void* timestep, int ts_dtype, const int64_t ts_strides[4],
+                             int shift_index, int scale_index, float eps, const float* input_scale,
+                             int scale_zero_dim, void* stream);
+
+/*
  * AdaZero with materialised scale/shift: `fused_adazero`
  * (triton_ltx_ops.py:8-37; guard :1626-1637).
  * x, y viewed (batch, tokens, cols); scale/shift are that shape after torch

@@ -30,6 +30,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "oga_last_error": (ctypes.c_char_p, []),
     "oga_adazero_from_ada": (_i32, [_p, _p, _i64, _i64, _i64, _p, _i32, _i64, _i64, _p, _i32, _i64p, _i32, _i32,
                                     _f32, _p]),
+    "oga_adazero_from_ada_fp8": (_i32, [_p, _p, _i64, _i64, _i64, _p, _i32, _i64, _i64, _p, _i32, _i64p, _i32,
+                                        _i32, _f32, _p, _i32, _p]),
     "oga_adazero": (_i32, [_p, _p, _i64, _i64, _i64, _p, _i32, _i64p, _p, _i32, _i64p, _f32, _p]),
     "oga_adaln_affine_from_ada": (_i32, [_p, _p, _i64, _i64, _i64, _p, _i32, _i64, _i64, _p, _i32, _i64p, _i32,
                                          _i32, _p]),

@@ -138,14 +138,24 @@ def _rms_norm(x: torch.Tensor, eps: float, weight: torch.Tensor | None = None) -
 
 
 def video_self_attention(block: VideoBlock, vx: torch.Tensor, timesteps: torch.Tensor, cos: torch.Tensor,
-                         sin: torch.Tensor, stages: Stages | None = None, *, qkv_grouped: bool = False) -> torch.Tensor:
+                         sin: torch.Tensor, stages: Stages | None = None, *, qkv_grouped: bool = False,
+                         fuse_ada_quant: bool = False) -> torch.Tensor:
     """:3006-3083 with `_attention_without_out_bias` (:2561-2648). With
     `qkv_grouped` the three projections run as one grouped FP8 GEMM
     (`fp8_qkv_from_grouped_mm`, :890-925; off in the reference's
-    production), otherwise as three FP8 linears."""
+    production), otherwise as three FP8 linears. With `fuse_ada_quant` as
+    well, and no head gates (their logits read the bf16 AdaZero rows), the
+    AdaZero pass writes the grouped GEMM's e4m3 input itself."""
     a = block.attn1
-    norm_vx = L.fused_adazero_from_ada(vx, block.eps, block.table, timesteps, shift_index=0, scale_index=1)
-    qkv = L.fp8_qkv_from_grouped_mm(a, norm_vx) if qkv_grouped else None
+    norm_vx = norm_q8 = qkv = None
+    if fuse_ada_quant and qkv_grouped and a.to_gate_logits is None:
+        norm_q8 = L.fused_adazero_from_ada_fp8(vx, block.eps, block.table, timesteps, a.to_q.input_scale,
+                                               shift_index=0, scale_index=1)
+        qkv = L.fp8_qkv_from_quantized_e4m3(a, norm_q8, out_dtype=vx.dtype)
+    if qkv is None:
+        norm_q8 = None
+        norm_vx = L.fused_adazero_from_ada(vx, block.eps, block.table, timesteps, shift_index=0, scale_index=1)
+        qkv = L.fp8_qkv_from_grouped_mm(a, norm_vx) if qkv_grouped else None
     if qkv is not None:
         q, k, v = qkv
     else:
@@ -164,7 +174,7 @@ def video_self_attention(block: VideoBlock, vx: torch.Tensor, timesteps: torch.T
         raise RuntimeError("to_out is not an FP8 linear")
     out = L.fused_residual_gate_bias_from_ada(vx, proj, a.to_out.bias, block.table, timesteps, gate_index=2)
     if stages is not None:
-        for name, val in (("msa.x", vx), ("msa.norm", norm_vx), ("msa.q", q), ("msa.k", k), ("msa.v", v),
+        for name, val in (("msa.x", vx), ("msa.norm", norm_vx), ("msa.norm_q8", norm_q8), ("msa.q", q), ("msa.k", k), ("msa.v", v),
                           ("msa.qr", qr), ("msa.kr", kr), ("msa.attn", o), ("msa.gates", gates),
                           ("msa.gated", og), ("msa.proj", proj), ("msa.out", out)):
             stages[name] = val
@@ -174,7 +184,7 @@ def video_self_attention(block: VideoBlock, vx: torch.Tensor, timesteps: torch.T
 def video_text_cross_attention(block: VideoBlock, vx: torch.Tensor, context: torch.Tensor,
                                timesteps: torch.Tensor, prompt_timestep: torch.Tensor,
                                stages: Stages | None = None, *, fuse_norm: bool = False,
-                               fuse_context: bool | None = None) -> torch.Tensor:
+                               fuse_context: bool | None = None, fuse_ada_quant: bool = False) -> torch.Tensor:
     """:2810-2888 (cross_attention_adaln, production flags). rms_norm
     followed by the AdaLN affine of Ada rows 6/7 is AdaZero's composition
     (R(R(R(rms_norm(x)) R(1 + scale)) + shift)); with `fuse_norm` it runs as
@@ -184,7 +194,9 @@ def video_text_cross_attention(block: VideoBlock, vx: torch.Tensor, context: tor
     the context affine of the prompt table's rows 0/1 as one AdaLN-affine
     launch, the same expression as the torch form beside it. With `fuse_norm`
     the q/k RMSNorms (the module's q_norm/k_norm with no RoPE after them,
-    :1866-1867) run as `qk_rmsnorm` launches instead of torch's rms_norm."""
+    :1866-1867) run as `qk_rmsnorm` launches instead of torch's rms_norm.
+    `fuse_ada_quant` (with `fuse_norm`) has that AdaZero pass write the
+    q-projection's e4m3 input directly."""
     a = block.attn2
     b = vx.shape[0]
     if fuse_context is None:
@@ -196,14 +208,22 @@ def video_text_cross_attention(block: VideoBlock, vx: torch.Tensor, context: tor
         shift_kv, scale_kv = (block.prompt_table[None, None].to(device=vx.device, dtype=vx.dtype)
                               + prompt_timestep.reshape(b, prompt_timestep.shape[1], 2, -1)).unbind(dim=2)
         enc = context * (1 + scale_kv) + shift_kv
-    if fuse_norm:
+    attn_in_q8 = None
+    if fuse_norm and fuse_ada_quant:
+        normed = attn_in = None
+        attn_in_q8 = L.fused_adazero_from_ada_fp8(vx, block.eps, block.table, timesteps, a.to_q.input_scale,
+                                                  shift_index=6, scale_index=7)
+    elif fuse_norm:
         normed = None
         attn_in = L.fused_adazero_from_ada(vx, block.eps, block.table, timesteps, shift_index=6, scale_index=7)
     else:
         normed = _rms_norm(vx, block.eps)
         attn_in = L.fused_adaln_affine_from_ada(normed, block.table, timesteps, shift_index=6, scale_index=7)
     qk_norm = L.qk_rmsnorm if fuse_norm else (lambda x, w, eps: _rms_norm(x, eps, w))
-    qp = L.fp8_linear_forward(a.to_q, attn_in)
+    if attn_in_q8 is not None:
+        qp = L.fp8_linear_from_quantized_e4m3(a.to_q, attn_in_q8, out_dtype=vx.dtype)
+    else:
+        qp = L.fp8_linear_forward(a.to_q, attn_in)
     kp = L.fp8_linear_forward(a.to_k, enc)
     q = qk_norm(qp, a.q_norm_weight, block.eps)
     k = qk_norm(kp, a.k_norm_weight, block.eps)
@@ -212,7 +232,8 @@ def video_text_cross_attention(block: VideoBlock, vx: torch.Tensor, context: tor
     ca = L.fp8_linear_forward(a.to_out, o)
     out = L.fused_residual_gate_from_ada(vx, ca, block.table, timesteps, gate_index=8, count_video_ada=False)
     if stages is not None:
-        for name, val in (("ca.x", vx), ("ca.enc", enc), ("ca.normed", normed), ("ca.in", attn_in), ("ca.qp", qp),
+        for name, val in (("ca.x", vx), ("ca.enc", enc), ("ca.normed", normed), ("ca.in", attn_in),
+                          ("ca.in_q8", attn_in_q8), ("ca.qp", qp),
                           ("ca.kp", kp), ("ca.q", q), ("ca.k", k), ("ca.v", v), ("ca.attn", o), ("ca.proj", ca),
                           ("ca.out", out)):
             stages[name] = val
@@ -220,13 +241,22 @@ def video_text_cross_attention(block: VideoBlock, vx: torch.Tensor, context: tor
 
 
 def video_feed_forward(block: VideoBlock, vx: torch.Tensor, timesteps: torch.Tensor, *,
-                       fuse_gelu_quant: bool = False, stages: Stages | None = None) -> torch.Tensor:
+                       fuse_gelu_quant: bool = False, fuse_ada_quant: bool = False,
+                       stages: Stages | None = None) -> torch.Tensor:
     """:3224-3258. With `fuse_gelu_quant` the GELU-tanh runs inside the
     down-projection's input quantizer (`fused_gelu_tanh_fp8_quantize_e4m3`,
     :164-182, off in the reference's production); otherwise torch's GELU
-    (tanh) in bf16, then the down-projection's own quantizer."""
-    y = L.fused_adazero_from_ada(vx, block.eps, block.table, timesteps, shift_index=3, scale_index=4)
-    h = L.fp8_linear_forward(block.ff_up, y)
+    (tanh) in bf16, then the down-projection's own quantizer. With
+    `fuse_ada_quant` the AdaZero pass writes the up-projection's e4m3 input."""
+    if fuse_ada_quant:
+        y = None
+        yq = L.fused_adazero_from_ada_fp8(vx, block.eps, block.table, timesteps, block.ff_up.input_scale,
+                                          shift_index=3, scale_index=4)
+        h = L.fp8_linear_from_quantized_e4m3(block.ff_up, yq, out_dtype=vx.dtype)
+    else:
+        yq = None
+        y = L.fused_adazero_from_ada(vx, block.eps, block.table, timesteps, shift_index=3, scale_index=4)
+        h = L.fp8_linear_forward(block.ff_up, y)
     if fuse_gelu_quant:
         g = None
         qg = L.fused_gelu_tanh_fp8_quantize_e4m3(h, block.ff_down.input_scale)
@@ -236,7 +266,7 @@ def video_feed_forward(block: VideoBlock, vx: torch.Tensor, timesteps: torch.Ten
         d = L.fp8_linear_forward(block.ff_down, g)
     out = L.fused_residual_gate_from_ada(vx, d, block.table, timesteps, gate_index=5)
     if stages is not None:
-        for name, val in (("ff.x", vx), ("ff.norm", y), ("ff.h", h), ("ff.gelu", g), ("ff.down", d),
+        for name, val in (("ff.x", vx), ("ff.norm", y), ("ff.norm_q8", yq), ("ff.h", h), ("ff.gelu", g), ("ff.down", d),
                           ("ff.out", out)):
             stages[name] = val
     return out
@@ -245,11 +275,16 @@ def video_feed_forward(block: VideoBlock, vx: torch.Tensor, timesteps: torch.Ten
 def video_block_forward(block: VideoBlock, vx: torch.Tensor, context: torch.Tensor, timesteps: torch.Tensor,
                         prompt_timestep: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, *,
                         fuse_gelu_quant: bool = False, qkv_grouped: bool = False, fuse_norm: bool = False,
-                        stages: Stages | None = None) -> torch.Tensor:
+                        fuse_ada_quant: bool = False, stages: Stages | None = None) -> torch.Tensor:
     """The video branches of one block: self-attention, text cross-attention,
     feed-forward (:2989-3298 without the audio and audio-video branches).
     vx (B, N, C) bf16; context (B, T, C) bf16; timesteps (B, N, 9C) or a
-    stride-0 token axis; prompt_timestep (B, T, 2C); cos/sin [B or 1, H, N, 64]."""
-    vx = video_self_attention(block, vx, timesteps, cos, sin, stages, qkv_grouped=qkv_grouped)
-    vx = video_text_cross_attention(block, vx, context, timesteps, prompt_timestep, stages, fuse_norm=fuse_norm)
-    return video_feed_forward(block, vx, timesteps, fuse_gelu_quant=fuse_gelu_quant, stages=stages)
+    stride-0 token axis; prompt_timestep (B, T, 2C); cos/sin [B or 1, H, N, 64].
+    `fuse_ada_quant` has each AdaZero pass that feeds an FP8 linear write that
+    linear's e4m3 input instead of bf16 rows (`fused_adazero_from_ada_fp8`)."""
+    vx = video_self_attention(block, vx, timesteps, cos, sin, stages, qkv_grouped=qkv_grouped,
+                              fuse_ada_quant=fuse_ada_quant)
+    vx = video_text_cross_attention(block, vx, context, timesteps, prompt_timestep, stages, fuse_norm=fuse_norm,
+                                    fuse_ada_quant=fuse_ada_quant)
+    return video_feed_forward(block, vx, timesteps, fuse_gelu_quant=fuse_gelu_quant, fuse_ada_quant=fuse_ada_quant,
+                              stages=stages)

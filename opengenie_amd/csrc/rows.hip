@@ -85,6 +85,11 @@ struct RowArgs {
   int cols;
   float eps;
   AdaSrc s0, s1;
+  // AdaZero with e4m3 output (out then holds one byte per element): the
+  // input quantizer of the FP8 linear that follows, with its scale.
+  int q8;
+  const float* qscale;
+  int q_zero_dim;
 };
 
 template <int OP>
@@ -412,7 +417,11 @@ constexpr int kAdaWaves = OGA_ADA_WAVES;
 constexpr int kAdaSchedGroup = OGA_ADA_SCHED_GROUP;
 enum { TAB_NONE = 0, TAB_BF16 = 1, TAB_F32 = 2 };
 
-template <int CH, bool UNIFORM, int D0, int D1, int TAB>
+// Q8: each finished bf16 row goes straight into the FP8 linear's input
+// quantizer, e4m3(clamp(R(y) * r, +-448)) with r as k_fp8_quant takes it
+// (the float32 reciprocal of the scale, rounded to bf16 for a 0-dim scale,
+// and the product rounded to bf16 then), so only the codes reach memory.
+template <int CH, bool UNIFORM, int D0, int D1, int TAB, bool Q8 = false>
 __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int64_t waves_per_batch) {
   constexpr int C = CH * 512;
   constexpr int G = C / 8;  // groups of 8 columns
@@ -459,6 +468,12 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
   }
   const uint16_t* const xb = a.x + b * a.tokens * C + lane * 8;
   uint16_t* const yb = a.out + b * a.tokens * C + lane * 8;
+  uint8_t* const qb = (uint8_t*)a.out + b * a.tokens * C + lane * 8;
+  float qr = 0.0f;
+  if constexpr (Q8) {
+    qr = 1.0f / a.qscale[0];
+    if (a.q_zero_dim) qr = rbf(qr);
+  }
   uint4 xv[CH];
   {
     const int64_t tl = t_first < a.tokens ? t_first : a.tokens - 1;
@@ -594,7 +609,24 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
         }
         ow[i / 2] = pack_bf16(pa + v0[i], pb + v0[i + 1]);
       }
-      st_nt16(yb + t * C + j * 512, make_uint4(ow[0], ow[1], ow[2], ow[3]));
+      if constexpr (Q8) {
+        float qv[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float lo = bf16_lo(ow[i]) * qr, hi = bf16_hi(ow[i]) * qr;
+          if (a.q_zero_dim) {
+            lo = rbf(lo);
+            hi = rbf(hi);
+          }
+          qv[2 * i] = clamp448(lo);
+          qv[2 * i + 1] = clamp448(hi);
+        }
+        typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 o = {e4m3x4(qv[0], qv[1], qv[2], qv[3]), e4m3x4(qv[4], qv[5], qv[6], qv[7])};
+        __builtin_nontemporal_store(o, (u32x2*)(qb + t * C + j * 512));
+      } else {
+        st_nt16(yb + t * C + j * 512, make_uint4(ow[0], ow[1], ow[2], ow[3]));
+      }
     }
   };
   if (t_first < a.tokens) {
@@ -751,7 +783,14 @@ static void launch_row_v(RowArgs& a, int64_t batch, bool vec, hipStream_t st) {
     int64_t vpb = 0, rpw = 0;
     adazero_rows_grid(batch, a.tokens, grid, vpb, rpw);
     const dim3 block(64 * kAdaWaves);
-    if (!a.s0.tab)
+    if (a.q8) {
+      if (!a.s0.tab)
+        hipLaunchKernelGGL((k_adazero_rows<CH, UNIFORM, D0, D1, TAB_NONE, true>), grid, block, 0, st, a, vpb);
+      else if (a.s0.tab_dt == OGA_DT_BF16)
+        hipLaunchKernelGGL((k_adazero_rows<CH, UNIFORM, D0, D1, TAB_BF16, true>), grid, block, 0, st, a, vpb);
+      else
+        hipLaunchKernelGGL((k_adazero_rows<CH, UNIFORM, D0, D1, TAB_F32, true>), grid, block, 0, st, a, vpb);
+    } else if (!a.s0.tab)
       hipLaunchKernelGGL((k_adazero_rows<CH, UNIFORM, D0, D1, TAB_NONE>), grid, block, 0, st, a, vpb);
     else if (a.s0.tab_dt == OGA_DT_BF16)
       hipLaunchKernelGGL((k_adazero_rows<CH, UNIFORM, D0, D1, TAB_BF16>), grid, block, 0, st, a, vpb);
@@ -795,6 +834,7 @@ static int run_row(RowArgs& a, int64_t batch, hipStream_t st) {
   bool vec = a.s0.ts_vec && (!two || a.s1.ts_vec);
   if (OP == OP_ADAZERO && a.s0.tab)  // k_adazero_rows reads table rows 16 bytes at a time
     vec = vec && a.s0.tab_vec && a.s1.tab_vec && a.s0.tab_dt == a.s1.tab_dt;
+  if (a.q8 && !vec) return unsupported("e4m3 output needs 16-byte table and timestep rows");
   return a.cols == 4096 ? launch_row_ch<8, OP>(a, batch, uniform, vec, st)
                         : launch_row_ch<4, OP>(a, batch, uniform, vec, st);
 }
@@ -831,6 +871,24 @@ extern "C" int oga_adazero_from_ada(const void* x, void* y, int64_t batch, int64
   int rc = row_common(a, x, nullptr, y, batch, tokens, cols);
   if (rc) return rc;
   a.eps = eps;
+  if ((rc = make_ada_src(a.s0, table, table_dtype, tab_s0, tab_s1, timestep, ts_dtype, ts_strides, shift_index, INT64_MAX))) return rc;
+  if ((rc = make_ada_src(a.s1, table, table_dtype, tab_s0, tab_s1, timestep, ts_dtype, ts_strides, scale_index, INT64_MAX))) return rc;
+  return run_row<OP_ADAZERO>(a, batch, (hipStream_t)stream);
+}
+
+extern "C" int oga_adazero_from_ada_fp8(const void* x, void* q, int64_t batch, int64_t tokens, int64_t cols,
+                                        const void* table, int table_dtype, int64_t tab_s0, int64_t tab_s1,
+                                        const void* timestep, int ts_dtype, const int64_t ts_strides[4],
+                                        int shift_index, int scale_index, float eps, const float* input_scale,
+                                        int scale_zero_dim, void* stream) {
+  RowArgs a{};
+  int rc = row_common(a, x, nullptr, q, batch, tokens, cols);
+  if (rc) return rc;
+  if (!input_scale) return fail("null input scale");
+  a.eps = eps;
+  a.q8 = 1;
+  a.qscale = input_scale;
+  a.q_zero_dim = scale_zero_dim ? 1 : 0;
   if ((rc = make_ada_src(a.s0, table, table_dtype, tab_s0, tab_s1, timestep, ts_dtype, ts_strides, shift_index, INT64_MAX))) return rc;
   if ((rc = make_ada_src(a.s1, table, table_dtype, tab_s0, tab_s1, timestep, ts_dtype, ts_strides, scale_index, INT64_MAX))) return rc;
   return run_row<OP_ADAZERO>(a, batch, (hipStream_t)stream);

@@ -29,6 +29,7 @@ from . import _lib
 __all__ = [
     "fused_adazero",
     "fused_adazero_from_ada",
+    "fused_adazero_from_ada_fp8",
     "fused_adaln_affine_from_ada",
     "fused_fp8_quantize_e4m3",
     "fused_gelu_tanh_fp8_quantize_e4m3",
@@ -50,6 +51,7 @@ __all__ = [
     "fp8_scaled_mm",
     "fp8_qkv_from_shared_quantized_input",
     "fp8_qkv_from_grouped_mm",
+    "fp8_qkv_from_quantized_e4m3",
     "fp8_qk_from_grouped_mm",
     "fp8_qkv_from_packed_linear",
     "fp8_qkv_from_packed_requant",
@@ -436,6 +438,54 @@ def fused_adazero_from_ada(
               _dt(scale_shift_table), scale_shift_table.stride(0), scale_shift_table.stride(1), _ptr(ts_view),
               _dt(timestep), st, si, ci, float(eps), _stream(x))
     return y
+
+
+def _ada_rows_vec8(t: torch.Tensor, offset: int, *strides_: int) -> bool:
+    """16-byte row reads of an Ada source (the C library's own check): unit
+    column stride, 8-element aligned base, offset and outer strides."""
+    if strides_[-1] != 1:
+        return False
+    es = t.element_size()
+    g = 8 * es
+    return t.data_ptr() % g == 0 and all((v * es) % g == 0 for v in (offset, *strides_[:-1]))
+
+
+def fused_adazero_from_ada_fp8(
+    x: torch.Tensor,
+    eps: float,
+    scale_shift_table: torch.Tensor,
+    timestep: torch.Tensor,
+    input_scale: torch.Tensor,
+    *,
+    shift_index: int,
+    scale_index: int,
+    counter: str = "video",
+) -> torch.Tensor:
+    """AdaZero from the Ada table (:40-91) handed to the FP8Linear that reads
+    it (:1691-1709): the e4m3 codes of `fused_fp8_quantize_e4m3` (:144-161)
+    applied to `fused_adazero_from_ada`'s output, from one HIP pass that never
+    writes the bf16 rows. No single counterpart in the reference."""
+    ok = (_can_use_ada_from_table(x, scale_shift_table, timestep) and _can_use_fused_fp8_quantize(x, input_scale)
+          and input_scale.device == x.device and scale_shift_table.device == x.device
+          and timestep.device == x.device)
+    if ok:
+        ts_view, st, (si, ci) = _ada_args(x, scale_shift_table, timestep, shift_index, scale_index)
+        tab_s = scale_shift_table.stride()
+        ok = all(_ada_rows_vec8(scale_shift_table, i * tab_s[0], tab_s[1]) for i in (si, ci)) and all(
+            _ada_rows_vec8(ts_view, i * ts_view.stride(2), ts_view.stride(0), ts_view.stride(1), ts_view.stride(3))
+            for i in (si, ci))
+    if not ok:
+        _fallback("fused_adazero_from_ada_fp8", x, scale_shift_table, timestep, input_scale)
+        y = fused_adazero_from_ada(x, eps, scale_shift_table, timestep, shift_index=shift_index,
+                                   scale_index=scale_index, counter=counter)
+        return fused_fp8_quantize_e4m3(y, input_scale)
+    _increment_ada_counter(counter)
+    q = torch.empty(x.shape, device=x.device, dtype=_FP8)
+    _hip("fused_adazero_from_ada_fp8")
+    _lib.call("oga_adazero_from_ada_fp8", _ptr(x), _ptr(q), x.shape[0], x.shape[1], x.shape[2],
+              _ptr(scale_shift_table), _dt(scale_shift_table), tab_s[0], tab_s[1], _ptr(ts_view), _dt(timestep), st,
+              si, ci, float(eps), _ptr(input_scale), int(input_scale.dim() == 0), _stream(x))
+    return q
 
 
 def fused_adaln_affine_from_ada(
@@ -963,6 +1013,12 @@ def _can_use_video_qkv_shared(attn: torch.nn.Module, x: torch.Tensor, names: tup
     square 4096 linears and weight scales `_scale_row` accepts."""
     if not x.is_cuda or not x.is_contiguous() or x.dtype not in (torch.bfloat16, torch.float16):
         return False
+    return _video_qkv_linears_ok(attn, x, names, grouped)
+
+
+def _video_qkv_linears_ok(attn: torch.nn.Module, x: torch.Tensor, names: tuple[str, ...], grouped: bool) -> bool:
+    """The shape and linear checks of `_can_use_video_qkv_shared` for an input
+    x of any dtype (bf16 activations or their e4m3 codes)."""
     if x.ndim != 3 or x.shape[0] != 1 or x.shape[1] < 1 or x.shape[-1] != 4096:
         return False
     linears = [getattr(attn, n, None) for n in names]
@@ -1065,6 +1121,17 @@ def fp8_qkv_from_grouped_mm(attn: torch.nn.Module, x: torch.Tensor):
         return None
     qinput = fused_fp8_quantize_e4m3(x.contiguous(), attn.to_q.input_scale)
     return _fp8_grouped_linear((attn.to_q, attn.to_k, attn.to_v), qinput, x.dtype)
+
+
+def fp8_qkv_from_quantized_e4m3(attn: torch.nn.Module, qinput: torch.Tensor, *, out_dtype: torch.dtype):
+    """The grouped Q/K/V projection of `fp8_qkv_from_grouped_mm` (:890-925)
+    on an input already quantized with to_q's input scale (as
+    `fused_adazero_from_ada_fp8` leaves it); None when the guard fails."""
+    if qinput.dtype != _FP8 or not qinput.is_cuda or not qinput.is_contiguous():
+        return None
+    if not _video_qkv_linears_ok(attn, qinput, ("to_q", "to_k", "to_v"), grouped=True):
+        return None
+    return _fp8_grouped_linear((attn.to_q, attn.to_k, attn.to_v), qinput, out_dtype)
 
 
 def fp8_qk_from_grouped_mm(attn: torch.nn.Module, x: torch.Tensor):

@@ -53,7 +53,19 @@ def _g(*ts):
 
 
 def _lin_ref(lin, x: T, bias=True):
+    return _lin_ref_codes(lin, O.fp8_quantize_e4m3(x, float(lin.input_scale), True, device="cuda"), bias)
+
+
+def _check_codes(got: torch.Tensor, x: T, lin, what):
+    """e4m3 codes written by the fused AdaZero pass: bit for bit those of the
+    linear's own input quantizer applied to the oracle's AdaZero rows."""
     codes = O.fp8_quantize_e4m3(x, float(lin.input_scale), True, device="cuda")
+    g = got.view(torch.uint8).cpu().numpy().reshape(codes.shape)
+    assert np.array_equal(g, codes), (what, int((g != codes).sum()))
+    return codes
+
+
+def _lin_ref_codes(lin, codes, bias=True):
     w = lin.weight.view(torch.uint8).cpu().numpy()
     return O.fp8_linear(codes, w, float(lin.input_scale), float(lin.weight_scale),
                         to_T(lin.bias) if bias else None)
@@ -84,39 +96,46 @@ def _check_attn(got, ref, v, what):
     assert float((err / (2e-3 * vrms + 2e-2 * np.abs(ref))).max()) <= 1.0, what
 
 
-@pytest.mark.parametrize("gated,fuse_gelu", [(False, False), (True, True)])
-def test_block_steps_match_oracle(gated, fuse_gelu):
+@pytest.mark.parametrize("gated,fused,ada_quant", [(False, False, False), (True, True, False), (False, True, True)])
+def test_block_steps_match_oracle(gated, fused, ada_quant):
     """Every step of the slice against the oracle on that step's GPU inputs
-    (the second case with all the MI355X-side fusions: grouped Q/K/V, the
+    (the second case with the MI355X-side fusions: grouped Q/K/V, the
     cross-attention's rms_norm + AdaLN as one AdaZero, GELU in the
-    down-projection's quantizer)."""
+    down-projection's quantizer; the third, without head gates, also with
+    each AdaZero that feeds an FP8 linear writing that linear's e4m3 input)."""
     from opengenie_amd import ltx_ops as L
     from opengenie_amd.block import Stages, random_video_block, video_block_forward
 
-    blk = random_video_block(C, HEADS, seed=11 + gated, gated=gated)
-    vx, context, ts, pts, cos, sin = _g(*_inputs(300 + 7 * gated))
+    blk = random_video_block(C, HEADS, seed=11 + gated + 2 * ada_quant, gated=gated)
+    vx, context, ts, pts, cos, sin = _g(*_inputs(300 + 7 * gated + 13 * ada_quant))
     st = Stages()
-    out = video_block_forward(blk, vx, context, ts, pts, cos, sin, fuse_gelu_quant=fuse_gelu, qkv_grouped=gated,
-                              fuse_norm=gated, stages=st)
+    out = video_block_forward(blk, vx, context, ts, pts, cos, sin, fuse_gelu_quant=fused, qkv_grouped=fused,
+                              fuse_norm=fused, fuse_ada_quant=ada_quant, stages=st)
     torch.cuda.synchronize()
     assert out.shape == vx.shape and out.dtype == torch.bfloat16
     calls = L.collect_hip_calls()
-    for op in ("fused_adazero_from_ada", "fp8_scaled_mm", "fused_video_qk_rmsnorm_rope", "flash_attn_func",
+    for op in ("fp8_scaled_mm", "fused_video_qk_rmsnorm_rope", "flash_attn_func",
                "fused_residual_gate_bias_from_ada", "fused_residual_gate_from_ada"):
         assert calls.get(op, 0) > 0, (op, calls)
-    assert (calls.get("fp8_grouped_linear", 0) > 0) == gated, calls
+    assert (calls.get("fp8_grouped_linear", 0) > 0) == fused, calls
     # one AdaLN-affine launch either way: the query affine (production flags)
     # or the context affine (with the fusions, where the query side is AdaZero)
     assert calls.get("fused_adaln_affine_from_ada", 0) == 1, calls
-    assert calls.get("fused_adazero_from_ada", 0) == (3 if gated else 2), calls
-    assert calls.get("qk_rmsnorm", 0) == (2 if gated else 0), calls
+    assert calls.get("fused_adazero_from_ada", 0) == (0 if ada_quant else 3 if fused else 2), calls
+    assert calls.get("fused_adazero_from_ada_fp8", 0) == (3 if ada_quant else 0), calls
+    assert calls.get("qk_rmsnorm", 0) == (2 if fused else 0), calls
     tab, tsT = to_T(blk.table), to_T(ts)
     a1, a2 = blk.attn1, blk.attn2
 
     # self-attention
-    assert_same_bits(np32(st["msa.norm"]), O.adazero_from_ada(to_T(st["msa.x"]), EPS, tab, tsT, 0, 1).v, "msa.norm")
+    nref = O.adazero_from_ada(to_T(st["msa.x"]), EPS, tab, tsT, 0, 1)
+    if ada_quant:
+        codes = _check_codes(st["msa.norm_q8"], nref, a1.to_q, "msa.norm_q8")
+    else:
+        assert_same_bits(np32(st["msa.norm"]), nref.v, "msa.norm")
     for nm, lin in (("q", a1.to_q), ("k", a1.to_k), ("v", a1.to_v)):
-        _check_linear(st[f"msa.{nm}"], _lin_ref(lin, to_T(st["msa.norm"])), f"msa.{nm}")
+        ref = _lin_ref_codes(lin, codes) if ada_quant else _lin_ref(lin, to_T(st["msa.norm"]))
+        _check_linear(st[f"msa.{nm}"], ref, f"msa.{nm}")
     rq, rk = O.video_qk_rmsnorm_rope(to_T(st["msa.q"]), to_T(st["msa.k"]), to_T(a1.q_norm_weight),
                                      to_T(a1.k_norm_weight), EPS, to_T(cos), to_T(sin))
     assert_same_bits(np32(st["msa.qr"]), rq.v, "msa.qr")
@@ -133,18 +152,22 @@ def test_block_steps_match_oracle(gated, fuse_gelu):
     # (torch's expression, or the AdaLN-affine kernel with the fusions)
     ref = O.adaln_affine_from_ada(to_T(context), to_T(blk.prompt_table), to_T(pts), 0, 1)
     assert_same_bits(np32(st["ca.enc"]), ref.v, "ca.enc")
-    if gated:  # rms_norm + AdaLN(6, 7) as one AdaZero pass
+    if fused:  # rms_norm + AdaLN(6, 7) as one AdaZero pass
         ref = O.adazero_from_ada(to_T(st["ca.x"]), EPS, tab, tsT, 6, 7)
     else:
         nref = O.rms_norm(to_T(st["ca.x"]), EPS)
         assert (bf16_ulp_distance(np32(st["ca.normed"]), nref.v) <= 1).all()
         ref = O.adaln_affine_from_ada(to_T(st["ca.normed"]), tab, tsT, 6, 7)
-    assert_same_bits(np32(st["ca.in"]), ref.v, "ca.in")
-    _check_linear(st["ca.qp"], _lin_ref(a2.to_q, to_T(st["ca.in"])), "ca.qp")
+    if ada_quant:
+        codes = _check_codes(st["ca.in_q8"], ref, a2.to_q, "ca.in_q8")
+        _check_linear(st["ca.qp"], _lin_ref_codes(a2.to_q, codes), "ca.qp")
+    else:
+        assert_same_bits(np32(st["ca.in"]), ref.v, "ca.in")
+        _check_linear(st["ca.qp"], _lin_ref(a2.to_q, to_T(st["ca.in"])), "ca.qp")
     _check_linear(st["ca.kp"], _lin_ref(a2.to_k, to_T(st["ca.enc"])), "ca.kp")
     for nm, w in (("q", a2.q_norm_weight), ("k", a2.k_norm_weight)):
         nref = O.rms_norm(to_T(st[f"ca.{nm}p"]), EPS, to_T(w))
-        if gated:  # qk_rmsnorm: bit for bit
+        if fused:  # qk_rmsnorm: bit for bit
             assert_same_bits(np32(st[f"ca.{nm}"]), nref.v, f"ca.{nm}")
         else:  # torch's rms_norm on the GPU: within one bf16 step
             assert (bf16_ulp_distance(np32(st[f"ca.{nm}"]), nref.v) <= 1).all(), f"ca.{nm}"
@@ -154,9 +177,14 @@ def test_block_steps_match_oracle(gated, fuse_gelu):
     assert_same_bits(np32(st["ca.out"]), ref.v, "ca.out")
 
     # feed-forward
-    assert_same_bits(np32(st["ff.norm"]), O.adazero_from_ada(to_T(st["ff.x"]), EPS, tab, tsT, 3, 4).v, "ff.norm")
-    _check_linear(st["ff.h"], _lin_ref(blk.ff_up, to_T(st["ff.norm"])), "ff.h")
-    if not fuse_gelu:
+    nref = O.adazero_from_ada(to_T(st["ff.x"]), EPS, tab, tsT, 3, 4)
+    if ada_quant:
+        codes = _check_codes(st["ff.norm_q8"], nref, blk.ff_up, "ff.norm_q8")
+        _check_linear(st["ff.h"], _lin_ref_codes(blk.ff_up, codes), "ff.h")
+    else:
+        assert_same_bits(np32(st["ff.norm"]), nref.v, "ff.norm")
+        _check_linear(st["ff.h"], _lin_ref(blk.ff_up, to_T(st["ff.norm"])), "ff.h")
+    if not fused:
         _check_linear(st["ff.down"], _lin_ref(blk.ff_down, to_T(st["ff.gelu"])), "ff.down")
     else:
         # GELU inside the quantizer: tanh's last float32 bit may move a code

@@ -116,6 +116,28 @@ def test_adazero_from_ada(rows, cols, params, tdt, sdt, bc, batch):
     assert_same_bits(out_np(out), bf16_round(ref.v), "adazero_from_ada")
 
 
+@pytest.mark.parametrize("scale,zero_dim", [(8.0 / 448, True), (0.01, False), (0.5 / 448, True)])
+@pytest.mark.parametrize("rows,cols,params,tdt,sdt,bc,batch",
+                         ADA_CASES + [(2304, 4096, 9, torch.bfloat16, torch.bfloat16, True, 1)])
+def test_adazero_from_ada_fp8(rows, cols, params, tdt, sdt, bc, batch, scale, zero_dim):
+    """AdaZero straight into the FP8 linear's e4m3 input: bit for bit the
+    oracle's quantizer (GPU torch semantics) applied to the oracle's AdaZero
+    rows; 0.5/448 saturates the tails at +-448."""
+    from opengenie_amd.ltx_ops import fused_adazero_from_ada_fp8
+
+    x, table, ts, xg, tg, sg = _ada(700 + rows, rows, cols, params, tdt, sdt, bc, batch)
+    s = torch.tensor(scale, dtype=torch.float32) if zero_dim else torch.tensor([scale], dtype=torch.float32)
+    out = fused_adazero_from_ada_fp8(xg, 1e-6, tg, sg, g(s), shift_index=3, scale_index=4)
+    _ran("fused_adazero_from_ada_fp8")
+    assert out.dtype == torch.float8_e4m3fn and out.shape == x.shape
+    ref = O.adazero_from_ada(to_T(x), 1e-6, to_T(table), to_T(ts), 3, 4)
+    codes = O.fp8_quantize_e4m3(O.bf(bf16_round(ref.v)), float(s.reshape(())), zero_dim, device="cuda")
+    got = out.view(torch.uint8).cpu().numpy()
+    assert np.array_equal(got, codes.reshape(got.shape)), int((got != codes.reshape(got.shape)).sum())
+    if scale < 0.005:
+        assert (np.abs(np32(out.float())) == 448).any()
+
+
 @pytest.mark.parametrize("rows,cols,params,tdt,sdt,bc,batch", ADA_CASES)
 def test_adaln_affine_from_ada(rows, cols, params, tdt, sdt, bc, batch):
     from opengenie_amd.ltx_ops import fused_adaln_affine_from_ada
