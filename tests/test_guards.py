@@ -44,6 +44,32 @@ def test_cpu_fallbacks_equal_reference_expressions():
                        tr.fp8_quantize_e4m3(x, s).view(torch.uint8))
 
 
+def test_adazero_fp8_cpu_path_is_the_composition():
+    """fused_adazero_from_ada_fp8 on CPU tensors: the torch AdaZero expression
+    followed by the FP8Linear input quantizer, code for code."""
+    x = randn((1, 9, 2048), 11)
+    table = randn((6, 2048), 12, dtype=torch.float32)
+    ts = randn((1, 9, 6 * 2048), 13)
+    s = torch.tensor(4.0 / 448)
+    L.reset_hip_calls()
+    q = L.fused_adazero_from_ada_fp8(x, 1e-6, table, ts, s, shift_index=3, scale_index=4)
+    ref = tr.fp8_quantize_e4m3(tr.adazero_from_ada(x, 1e-6, table, ts, 3, 4), s)
+    assert q.dtype == torch.float8_e4m3fn and torch.equal(q.view(torch.uint8), ref.view(torch.uint8))
+    assert L.collect_hip_calls() == {}
+
+
+def test_qkv_from_codes_guard():
+    """fp8_qkv_from_quantized_e4m3 takes only contiguous e4m3 GPU codes of a
+    (1, N, 4096) input; anything else returns None, as the grouped guard does."""
+    from opengenie_amd.block import random_video_block
+
+    blk = random_video_block(4096, 32, device="cpu", seed=5)
+    codes = torch.zeros((1, 4, 4096), dtype=torch.float8_e4m3fn)
+    assert L.fp8_qkv_from_quantized_e4m3(blk.attn1, codes, out_dtype=torch.bfloat16) is None
+    assert L.fp8_qkv_from_quantized_e4m3(blk.attn1, codes.view(torch.uint8).to(torch.bfloat16),
+                                         out_dtype=torch.bfloat16) is None
+
+
 def test_residual_mode_selection():
     x, y, gate = randn((1, 3, 2048), 1), randn((1, 3, 2048), 2), randn((1, 3, 2048), 3)
     try:
