@@ -417,11 +417,13 @@ constexpr int kAdaWaves = OGA_ADA_WAVES;
 constexpr int kAdaSchedGroup = OGA_ADA_SCHED_GROUP;
 enum { TAB_NONE = 0, TAB_BF16 = 1, TAB_F32 = 2 };
 
-// Q8: each finished bf16 row goes straight into the FP8 linear's input
-// quantizer, e4m3(clamp(R(y) * r, +-448)) with r as k_fp8_quant takes it
-// (the float32 reciprocal of the scale, rounded to bf16 for a 0-dim scale,
-// and the product rounded to bf16 then), so only the codes reach memory.
-template <int CH, bool UNIFORM, int D0, int D1, int TAB, bool Q8 = false>
+// Q8 (Q8_F32, Q8_BF16): each finished bf16 row goes straight into the FP8
+// linear's input quantizer, e4m3(clamp(R(y) * r, +-448)) with r as
+// k_fp8_quant takes it (the float32 reciprocal of the scale; for a 0-dim
+// scale, Q8_BF16, r and the product are rounded to bf16), so only the codes
+// reach memory. The scale's kind is a template flag, not a per-value select.
+enum { Q8_NONE = 0, Q8_F32 = 1, Q8_BF16 = 2 };
+template <int CH, bool UNIFORM, int D0, int D1, int TAB, int Q8 = Q8_NONE>
 __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int64_t waves_per_batch) {
   constexpr int C = CH * 512;
   constexpr int G = C / 8;  // groups of 8 columns
@@ -470,9 +472,9 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
   uint16_t* const yb = a.out + b * a.tokens * C + lane * 8;
   uint8_t* const qb = (uint8_t*)a.out + b * a.tokens * C + lane * 8;
   float qr = 0.0f;
-  if constexpr (Q8) {
+  if constexpr (Q8 != Q8_NONE) {
     qr = 1.0f / a.qscale[0];
-    if (a.q_zero_dim) qr = rbf(qr);
+    if constexpr (Q8 == Q8_BF16) qr = rbf(qr);
   }
   uint4 xv[CH];
   {
@@ -609,12 +611,12 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
         }
         ow[i / 2] = pack_bf16(pa + v0[i], pb + v0[i + 1]);
       }
-      if constexpr (Q8) {
+      if constexpr (Q8 != Q8_NONE) {
         float qv[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           float lo = bf16_lo(ow[i]) * qr, hi = bf16_hi(ow[i]) * qr;
-          if (a.q_zero_dim) {
+          if constexpr (Q8 == Q8_BF16) {
             lo = rbf(lo);
             hi = rbf(hi);
           }
@@ -768,6 +770,16 @@ static void make_direct_src(AdaSrc& s, const void* p, int dt, const int64_t* st3
   s.ts_vec = vec8_ok(p, dt, 0, s.ts_sb, s.ts_st, s.ts_sc);
 }
 
+template <int CH, bool UNIFORM, int D0, int D1, int Q8>
+static void launch_adazero_q8(RowArgs& a, dim3 grid, dim3 block, int64_t vpb, hipStream_t st) {
+  if (!a.s0.tab)
+    hipLaunchKernelGGL((k_adazero_rows<CH, UNIFORM, D0, D1, TAB_NONE, Q8>), grid, block, 0, st, a, vpb);
+  else if (a.s0.tab_dt == OGA_DT_BF16)
+    hipLaunchKernelGGL((k_adazero_rows<CH, UNIFORM, D0, D1, TAB_BF16, Q8>), grid, block, 0, st, a, vpb);
+  else
+    hipLaunchKernelGGL((k_adazero_rows<CH, UNIFORM, D0, D1, TAB_F32, Q8>), grid, block, 0, st, a, vpb);
+}
+
 template <int CH, int OP, bool UNIFORM, int D0, int D1>
 static void launch_row_v(RowArgs& a, int64_t batch, bool vec, hipStream_t st) {
   if constexpr (OP != OP_ADAZERO) {
@@ -784,12 +796,10 @@ static void launch_row_v(RowArgs& a, int64_t batch, bool vec, hipStream_t st) {
     adazero_rows_grid(batch, a.tokens, grid, vpb, rpw);
     const dim3 block(64 * kAdaWaves);
     if (a.q8) {
-      if (!a.s0.tab)
-        hipLaunchKernelGGL((k_adazero_rows<CH, UNIFORM, D0, D1, TAB_NONE, true>), grid, block, 0, st, a, vpb);
-      else if (a.s0.tab_dt == OGA_DT_BF16)
-        hipLaunchKernelGGL((k_adazero_rows<CH, UNIFORM, D0, D1, TAB_BF16, true>), grid, block, 0, st, a, vpb);
+      if (a.q_zero_dim)
+        launch_adazero_q8<CH, UNIFORM, D0, D1, Q8_BF16>(a, grid, block, vpb, st);
       else
-        hipLaunchKernelGGL((k_adazero_rows<CH, UNIFORM, D0, D1, TAB_F32, true>), grid, block, 0, st, a, vpb);
+        launch_adazero_q8<CH, UNIFORM, D0, D1, Q8_F32>(a, grid, block, vpb, st);
     } else if (!a.s0.tab)
       hipLaunchKernelGGL((k_adazero_rows<CH, UNIFORM, D0, D1, TAB_NONE>), grid, block, 0, st, a, vpb);
     else if (a.s0.tab_dt == OGA_DT_BF16)
