@@ -138,6 +138,41 @@ def test_adazero_from_ada_fp8(rows, cols, params, tdt, sdt, bc, batch, scale, ze
         assert (np.abs(np32(out.float())) == 448).any()
 
 
+def test_adazero_from_ada_special_values():
+    """Rows with a NaN, an infinity, both infinities, all zeros, signed zeros
+    and a mean square beyond float32 (1e30: inv = 0), and Ada columns with a
+    NaN scale and infinite shifts: the bf16 AdaZero bit for bit (NaN == NaN)
+    and its e4m3 codes, with saturation, NaN codes compared sign-free."""
+    from opengenie_amd.ltx_ops import fused_adazero_from_ada, fused_adazero_from_ada_fp8
+
+    cols, params = 4096, 6
+    x = randn((1, 8, cols), 771)
+    x[0, 1, 17] = float("nan")
+    x[0, 2, 300] = float("inf")
+    x[0, 3, 5], x[0, 3, 6] = float("inf"), float("-inf")
+    x[0, 4] = 0.0
+    x[0, 5, ::2] = -0.0
+    x[0, 5, 1::2] = 0.0
+    x[0, 6] = x[0, 6] * 1e30
+    table = randn((params, cols), 772, std=0.02)
+    table[4, 9] = float("nan")             # scale row: NaN column
+    table[3, 10] = float("inf")            # shift row: +inf and -inf columns
+    table[3, 11] = float("-inf")
+    ts = randn((1, 1, params * cols), 773, std=0.5).expand(1, 8, params * cols)
+    xg, tg, sg = g(x), g(table), g(ts)
+    ref = O.adazero_from_ada(to_T(x), 1e-6, to_T(table), to_T(ts), 3, 4)
+    out = fused_adazero_from_ada(xg, 1e-6, tg, sg, shift_index=3, scale_index=4)
+    _ran("fused_adazero_from_ada")
+    assert_same_bits(out_np(out), bf16_round(ref.v), "adazero special values")
+    for scale in (0.5 / 448, 8.0 / 448):
+        sc = torch.tensor(scale, dtype=torch.float32)
+        q = fused_adazero_from_ada_fp8(xg, 1e-6, tg, sg, g(sc), shift_index=3, scale_index=4)
+        _ran("fused_adazero_from_ada_fp8")
+        codes = O.fp8_quantize_e4m3(O.bf(bf16_round(ref.v)), scale, True, device="cuda")
+        got = q.view(torch.uint8).cpu().numpy()
+        assert np.array_equal(nan_canon(got), nan_canon(codes.reshape(got.shape))), scale
+
+
 @pytest.mark.parametrize("rows,cols,params,tdt,sdt,bc,batch", ADA_CASES)
 def test_adaln_affine_from_ada(rows, cols, params, tdt, sdt, bc, batch):
     from opengenie_amd.ltx_ops import fused_adaln_affine_from_ada
