@@ -173,6 +173,48 @@ def test_adazero_from_ada_special_values():
         assert np.array_equal(nan_canon(got), nan_canon(codes.reshape(got.shape))), scale
 
 
+@pytest.mark.parametrize("tdt", [torch.bfloat16, torch.float32])
+def test_ada_elementwise_special_values(tdt):
+    """AdaLN affine, gate multiply, residual gate and residual gate + bias on
+    NaN, +-inf, signed zeros and bf16-overflowing products in x, y, the
+    table, the timestep rows and the bias: bit for bit (NaN == NaN)."""
+    from opengenie_amd.ltx_ops import (fused_adaln_affine_from_ada, fused_mul_from_ada,
+                                       fused_residual_gate_bias_from_ada, fused_residual_gate_from_ada)
+
+    cols, params, rows = 2048, 9, 12
+    x = randn((1, rows, cols), 781)
+    y = randn((1, rows, cols), 782)
+    x[0, 0, :8] = torch.tensor([float("nan"), float("inf"), float("-inf"), 0.0, -0.0, 3e38, -3e38, 1e-38])
+    y[0, 1, :8] = torch.tensor([float("inf"), float("nan"), -0.0, 0.0, 3e38, float("-inf"), 1e38, -1e38])
+    x[0, 2] = -0.0
+    y[0, 2] = 0.0
+    table = randn((params, cols), 783, dtype=tdt, std=0.02)
+    table[:, 20] = float("nan")
+    table[:, 21] = float("inf")
+    table[:, 22] = float("-inf")
+    table[:, 23] = -1.0
+    ts = randn((1, rows, params * cols), 784, std=0.5)
+    tsv = ts.view(1, rows, params, cols)
+    tsv[0, 3, :, 30] = float("inf")
+    tsv[0, 4, :, 31] = float("nan")
+    tsv[0, 5, :, 32] = 1e38
+    bias = randn((cols,), 785, std=0.01)
+    bias[40], bias[41] = float("inf"), float("nan")
+    xg, yg, tg, sg, bg = g(x), g(y), g(table), g(ts), g(bias)
+    T_ = (to_T(x), to_T(y), to_T(table), to_T(ts))
+    cases = (
+        (fused_adaln_affine_from_ada(xg, tg, sg, shift_index=6, scale_index=7),
+         O.adaln_affine_from_ada(T_[0], T_[2], T_[3], 6, 7), "adaln_affine"),
+        (fused_mul_from_ada(xg, tg, sg, gate_index=8), O.mul_from_ada(T_[0], T_[2], T_[3], 8), "mul"),
+        (fused_residual_gate_from_ada(xg, yg, tg, sg, gate_index=5),
+         O.residual_gate_from_ada(T_[0], T_[1], T_[2], T_[3], 5), "residual_gate"),
+        (fused_residual_gate_bias_from_ada(xg, yg, bg, tg, sg, gate_index=2),
+         O.residual_gate_bias_from_ada(T_[0], T_[1], to_T(bias), T_[2], T_[3], 2), "residual_gate_bias"),
+    )
+    for out, ref, what in cases:
+        assert_same_bits(out_np(out), bf16_round(ref.v), what)
+
+
 @pytest.mark.parametrize("rows,cols,params,tdt,sdt,bc,batch", ADA_CASES)
 def test_adaln_affine_from_ada(rows, cols, params, tdt, sdt, bc, batch):
     from opengenie_amd.ltx_ops import fused_adaln_affine_from_ada
