@@ -533,6 +533,32 @@ def test_video_qk_rmsnorm_rope(tokens, cos_dtype, w_dtype):
     assert_same_bits(out_np(ok), bf16_round(rk.v), "k")
 
 
+@pytest.mark.parametrize("cos_dtype", [torch.bfloat16, torch.float32])
+def test_video_qk_rmsnorm_rope_special_values(cos_dtype):
+    """Q/K RMSNorm + RoPE on tokens with a NaN, an infinity, all zeros, signed
+    zeros and a mean square beyond float32, NaN/inf norm weights, and NaN/inf
+    cos/sin entries: bit for bit (NaN == NaN)."""
+    from opengenie_amd.ltx_ops import fused_video_qk_rmsnorm_rope
+
+    q, k, qw, kw, cos, sin = _rope(990, 8, cos_dtype)
+    q[0, 1, 70] = float("nan")
+    k[0, 2, 4000] = float("inf")
+    q[0, 3] = 0.0
+    k[0, 3, ::2] = -0.0
+    k[0, 3, 1::2] = 0.0
+    q[0, 4] = q[0, 4] * 1e30
+    k[0, 5, 7], k[0, 5, 71] = float("inf"), float("-inf")
+    qw[200] = float("nan")
+    kw[300] = float("inf")
+    cos[0, 5, 6, 10] = float("nan")
+    sin[0, 7, 7, 20] = float("inf")
+    oq, ok = fused_video_qk_rmsnorm_rope(g(q), g(k), g(qw), g(kw), 1e-6, g(cos), g(sin))
+    _ran("fused_video_qk_rmsnorm_rope")
+    rq, rk = O.video_qk_rmsnorm_rope(to_T(q), to_T(k), to_T(qw), to_T(kw), 1e-6, to_T(cos), to_T(sin))
+    assert_same_bits(out_np(oq), bf16_round(rq.v), "q")
+    assert_same_bits(out_np(ok), bf16_round(rk.v), "k")
+
+
 def test_video_qk_rmsnorm_rope_strided_cos():
     """cos/sin as non-contiguous views (head and token strides permuted)."""
     from opengenie_amd.ltx_ops import fused_video_qk_rmsnorm_rope
