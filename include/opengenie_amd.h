@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-enum { OGA_DT_BF16 = 0, OGA_DT_F32 = 1 };
+enum { OGA_DT_BF16 = 0, OGA_DT_F32 = 1, OGA_DT_F16 = 2 };
 enum { OGA_OK = 0, OGA_EINVAL = -1, OGA_EUNSUPPORTED = -2 };
 
 /* Library identification and the last argument-error message (per thread). */
@@ -121,35 +121,40 @@ int oga_head_gate_mul_bf16(const void* x, const void* gates, int64_t g_s0, int64
                            int64_t rows, int64_t heads, int64_t dim_head, void* stream);
 
 /*
- * `fused_fp8_quantize_e4m3` (triton_ltx_ops.py:144-161; torch path :146-148):
- * q = e4m3fn(clamp(x * (1/scale), -448, 448)) for n contiguous bf16 inputs.
- * scale is a device float32 with one element. scale_is_0dim selects torch's
- * dtype rule for a 0-dim scale tensor (both operands taken to bf16 before the
- * multiply, the product rounded to bf16) versus a (1,)-shaped one (float32
- * product). q holds n e4m3fn codes.
+ * `fused_fp8_quantize_e4m3` (triton_ltx_ops.py:144-161; torch path :146-148;
+ * guard :1021-1022): q = e4m3fn(clamp(x * (1/scale), -448, 448)) for n
+ * contiguous inputs of dtype x_dtype (OGA_DT_BF16 or OGA_DT_F16, the two the
+ * reference's guard takes; x 16-byte aligned). scale is a device float32
+ * with one element. scale_is_0dim selects torch's dtype rule for a 0-dim
+ * scale tensor (the reciprocal taken to x's dtype before the multiply, the
+ * product rounded to x's dtype) versus a (1,)-shaped one (float32 product).
+ * q holds n e4m3fn codes.
  */
-int oga_fp8_quantize_e4m3(const void* x, const float* scale, int scale_is_0dim, void* q, int64_t n,
+int oga_fp8_quantize_e4m3(const void* x, int x_dtype, const float* scale, int scale_is_0dim, void* q, int64_t n,
                           void* stream);
 
 /* `fused_gelu_tanh_fp8_quantize_e4m3` (triton_ltx_ops.py:164-182; torch
- * path :165-169): the quantizer above applied to R(gelu_tanh(x)), with the
- * GELU evaluated in float32 exactly as torch's GPU kernel evaluates
- * gelu(approximate='tanh') (the device tanhf), so the codes equal torch's.
- * Each call first writes R(gelu) of all 65536 bf16 inputs into a 128 KiB
- * table in a file-scope device array of the library (the same values every
- * time), then quantizes by looking the elements up in it. */
-int oga_gelu_tanh_fp8_quantize_e4m3(const void* x, const float* scale, int scale_is_0dim, void* q,
+ * path :165-169): the quantizer above applied to gelu_tanh(x) rounded to
+ * x's dtype, with the GELU evaluated in float32 exactly as torch's GPU kernel
+ * evaluates gelu(approximate='tanh') (the device tanhf), so the codes equal
+ * torch's. The results for all 65536 inputs of x's dtype are a 128 KiB table
+ * in a file-scope device array of the library, one per dtype and GPU, built
+ * by the first call on that GPU (on the caller's stream; calls on other
+ * streams wait for it through an event until it has completed) and only read
+ * afterwards; the elements are quantized by looking them up in it. */
+int oga_gelu_tanh_fp8_quantize_e4m3(const void* x, int x_dtype, const float* scale, int scale_is_0dim, void* q,
                                     int64_t n, void* stream);
 
 /*
  * `fused_fp8_quantize_e4m3_per_head_4d` (triton_ltx_ops.py:265-317; torch
- * path :976-980). x [B, N, H, D] bf16 contiguous, D in {64, 128}, H*D a
- * multiple of 512. scale_out [B, H] float32 = max(amax|x|, 1e-12) / 448;
- * q [B, N, H, D] e4m3fn = e4m3(clamp(x / scale, +-448)). `workspace` holds
+ * path :976-980; guard :1489-1499). x [B, N, H, D] contiguous, bf16 or fp16
+ * (x_dtype), D in {64, 128}, H*D in {1024, 2048, 4096}. scale_out [B, H]
+ * float32 = max(amax|x|, 1e-12) / 448; q [B, N, H, D] e4m3fn =
+ * e4m3(clamp(x / scale, +-448)). `workspace` holds
  * oga_fp8_per_head_workspace_bytes(...) bytes of caller-owned device memory.
  */
 int64_t oga_fp8_per_head_workspace_bytes(int64_t batch, int64_t tokens, int64_t heads, int64_t head_dim);
-int oga_fp8_quantize_per_head(const void* x, void* q, float* scale_out, void* workspace, int64_t batch,
+int oga_fp8_quantize_per_head(const void* x, int x_dtype, void* q, float* scale_out, void* workspace, int64_t batch,
                               int64_t tokens, int64_t heads, int64_t head_dim, void* stream);
 
 /*
@@ -331,8 +336,8 @@ int oga_selftest_convert(const float* in, uint16_t* bf16_out, uint8_t* e4m3_out,
  * oga_fp8_quantize_per_head.
  */
 int64_t oga_fp8_per_head_noalloc_max_bytes(void);
-int oga_fp8_quantize_per_head_noalloc(const void* x, void* q, float* scale_out, int64_t batch, int64_t tokens,
-                                      int64_t heads, int64_t head_dim, void* stream);
+int oga_fp8_quantize_per_head_noalloc(const void* x, int x_dtype, void* q, float* scale_out, int64_t batch,
+                                      int64_t tokens, int64_t heads, int64_t head_dim, void* stream);
 
 /*
  * Schedule query of the token-row kernels: how many token rows of one batch

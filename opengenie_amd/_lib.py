@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(HERE, "libopengenie_amd.so")
 
 DT_BF16 = 0
 DT_F32 = 1
+DT_F16 = 2
 ROWS_ADAZERO = 0
 ROWS_ELEMENTWISE = 1
 
@@ -43,10 +44,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "oga_residual_gate_bf16": (_i32, [_p, _p, _p, _i64p, _p, _i64, _i64, _i64, _p]),
     "oga_bias_add_bf16": (_i32, [_p, _p, _i32, _p, _i64, _i64, _p]),
     "oga_head_gate_mul_bf16": (_i32, [_p, _p, _i64, _i64, _p, _i64, _i64, _i64, _p]),
-    "oga_fp8_quantize_e4m3": (_i32, [_p, _p, _i32, _p, _i64, _p]),
-    "oga_gelu_tanh_fp8_quantize_e4m3": (_i32, [_p, _p, _i32, _p, _i64, _p]),
+    "oga_fp8_quantize_e4m3": (_i32, [_p, _i32, _p, _i32, _p, _i64, _p]),
+    "oga_gelu_tanh_fp8_quantize_e4m3": (_i32, [_p, _i32, _p, _i32, _p, _i64, _p]),
     "oga_fp8_per_head_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
-    "oga_fp8_quantize_per_head": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _p]),
+    "oga_fp8_quantize_per_head": (_i32, [_p, _i32, _p, _p, _p, _i64, _i64, _i64, _i64, _p]),
     "oga_video_qk_rmsnorm_rope": (_i32, [_p, _p, _p, _p, _i32, _p, _p, _i32, _i64p, _i64p, _p, _p, _i64, _i64,
                                          _i64, _i64, _f32, _p]),
     "oga_video_rmsnorm_rope": (_i32, [_p, _p, _i32, _p, _p, _i32, _i64p, _i64p, _p, _i64, _i64, _i64, _i64, _f32,
@@ -72,7 +73,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "oga_selftest_convert": (_i32, [_p, _p, _p, _i64, _p]),
     "oga_rows_per_wave": (_i64, [_i32, _i64, _i64, _i64]),
     "oga_fp8_per_head_noalloc_max_bytes": (_i64, []),
-    "oga_fp8_quantize_per_head_noalloc": (_i32, [_p, _p, _p, _i64, _i64, _i64, _i64, _p]),
+    "oga_fp8_quantize_per_head_noalloc": (_i32, [_p, _i32, _p, _p, _i64, _i64, _i64, _i64, _p]),
 }
 
 _lock = threading.Lock()

@@ -126,7 +126,9 @@ def flash_attn_func(
         if t.dtype == _FP8:
             if ds is None:
                 raise ValueError("float8_e4m3fn attention inputs need their descale")
-            if t.is_cuda and t.ndim == 4 and t.shape[-1] % 16 == 0:
+            # the kernel reads 16-byte pieces of the contiguous codes
+            if t.is_cuda and t.ndim == 4 and t.shape[-1] % 16 == 0 and (not t.is_contiguous()
+                                                                       or t.data_ptr() % 16 == 0):
                 _hip("fp8_dequant_per_head")
                 t = _dequant(t, ds)
             else:

@@ -148,7 +148,10 @@ def video_self_attention(block: VideoBlock, vx: torch.Tensor, timesteps: torch.T
     AdaZero pass writes the grouped GEMM's e4m3 input itself."""
     a = block.attn1
     norm_vx = norm_q8 = qkv = None
-    if fuse_ada_quant and qkv_grouped and a.to_gate_logits is None:
+    # The grouped projection's guard is checked before the e4m3 AdaZero pass,
+    # so a failing guard costs no second AdaZero pass.
+    if (fuse_ada_quant and qkv_grouped and a.to_gate_logits is None and vx.is_cuda
+            and L._video_qkv_linears_ok(a, vx, ("to_q", "to_k", "to_v"), grouped=True)):
         norm_q8 = L.fused_adazero_from_ada_fp8(vx, block.eps, block.table, timesteps, a.to_q.input_scale,
                                                shift_index=0, scale_index=1)
         qkv = L.fp8_qkv_from_quantized_e4m3(a, norm_q8, out_dtype=vx.dtype)

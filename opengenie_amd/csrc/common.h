@@ -67,6 +67,43 @@ OGA_DEVICE uint4 pack8(const float* f) {
   return u;
 }
 
+// ---------------------------------------------------------------- fp16 bits
+OGA_DEVICE float f16_bits(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+OGA_DEVICE float f16_lo(uint32_t w) { return f16_bits(w & 0xFFFFu); }
+OGA_DEVICE float f16_hi(uint32_t w) { return f16_bits(w >> 16); }
+// Round a float to the nearest fp16 (ties to even, overflow to infinity,
+// v_cvt_f16_f32) and return it as float. The empty asm keeps v a float32
+// value in a register: without it the compiler folds a product rounded to
+// fp16 into v_fma_mix_f16(a, b, +0), whose +0 addend turns a -0 product
+// into +0.
+OGA_DEVICE float rhf(float v) {
+  asm("" : "+v"(v));
+  return (float)(_Float16)v;
+}
+
+// The 16-bit activation dtypes (XDT = OGA_DT_BF16 or OGA_DT_F16): a value of
+// x's dtype from its bits, rounding to x's dtype, and 8 elements of a
+// 16-byte vector as floats.
+template <int XDT>
+OGA_DEVICE float x16_bits(uint32_t b) {
+  return XDT == OGA_DT_F16 ? f16_bits(b) : __uint_as_float(b << 16);
+}
+template <int XDT>
+OGA_DEVICE float rx16(float v) {
+  return XDT == OGA_DT_F16 ? rhf(v) : rbf(v);
+}
+template <int XDT>
+OGA_DEVICE void unpack8x(const uint4& u, float* f) {
+  if (XDT == OGA_DT_F16) {
+    f[0] = f16_lo(u.x); f[1] = f16_hi(u.x);
+    f[2] = f16_lo(u.y); f[3] = f16_hi(u.y);
+    f[4] = f16_lo(u.z); f[5] = f16_hi(u.z);
+    f[6] = f16_lo(u.w); f[7] = f16_hi(u.w);
+  } else {
+    unpack8(u, f);
+  }
+}
+
 // 16-byte store of a streamed output: non-temporal, so it does not evict
 // the inputs still being read from the caches.
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));

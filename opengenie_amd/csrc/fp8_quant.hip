@@ -1,4 +1,4 @@
-// bf16 -> float8_e4m3fn activation quantizers.
+// bf16 / fp16 -> float8_e4m3fn activation quantizers.
 //
 // Reference: ltx_serve/triton_ltx_ops.py :144-161 (per tensor; torch path
 // :146-148), :164-182 (GELU-tanh then quantize; torch :165-169), :265-317
@@ -6,12 +6,14 @@
 //
 // Per-tensor: q = e4m3(clamp(x * r, +-448)), r = 1/scale (IEEE division).
 // torch's dtype rule decides the rounding of x * r: with a 0-dim scale the
-// common dtype is bf16, so the float32 operand r is first converted to bf16
-// and the product is rounded to bf16; with a (1,) scale the product stays
-// float32. Every thread converts 16 elements: two 128-bit loads, one 128-bit
+// common dtype is x's (bf16 or fp16), so the float32 operand r is first
+// converted to x's dtype and the product is rounded to it; with a (1,) scale
+// the product stays float32. Every kernel takes x's dtype as the template
+// parameter XDT (OGA_DT_BF16 or OGA_DT_F16). Every thread converts 16 elements: two 128-bit loads, one 128-bit
 // store. The e4m3 rounding is the hardware v_cvt_pk_fp8_f32 (nearest even),
 // applied after the clamp so saturation never engages.
 #include <atomic>
+#include <mutex>
 
 #include "common.h"
 #include "host.h"
@@ -30,31 +32,31 @@ namespace oga {
 constexpr int kGeluNone = 0, kGeluExact = 1;
 constexpr float kGeluBeta = (float)(M_SQRT2 * M_2_SQRTPI * 0.5);
 constexpr float kGeluKappa = 0.044715f;
-template <int GELU>
+template <int GELU, int XDT>
 OGA_DEVICE float pre(float x) {
   if (GELU == kGeluNone) return x;
   const float x3 = (x * x) * x;
   const float inner = kGeluBeta * fmaf(kGeluKappa, x3, x);
-  return rbf((0.5f * x) * (1.0f + tanhf(inner)));
+  return rx16<XDT>((0.5f * x) * (1.0f + tanhf(inner)));
 }
 
-template <int GELU>
+template <int GELU, int XDT>
 __global__ __launch_bounds__(256) void k_fp8_quant(const uint16_t* x, const float* scale, int zero_dim, uint8_t* q,
                                                    int64_t n) {
   const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 16;
   if (i0 >= n) return;
   float r = 1.0f / scale[0];
-  if (zero_dim) r = rbf(r);
+  if (zero_dim) r = rx16<XDT>(r);
   if (i0 + 16 <= n) {
     const uint4 u0 = *(const uint4*)(x + i0);
     const uint4 u1 = *(const uint4*)(x + i0 + 8);
     float f[16];
-    unpack8(u0, f);
-    unpack8(u1, f + 8);
+    unpack8x<XDT>(u0, f);
+    unpack8x<XDT>(u1, f + 8);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      float v = pre<GELU>(f[i]) * r;
-      if (zero_dim) v = rbf(v);
+      float v = pre<GELU, XDT>(f[i]) * r;
+      if (zero_dim) v = rx16<XDT>(v);
       f[i] = clamp448(v);
     }
     uint4 o;
@@ -65,8 +67,8 @@ __global__ __launch_bounds__(256) void k_fp8_quant(const uint16_t* x, const floa
     st_nt16(q + i0, o);
   } else {
     for (int64_t i = i0; i < n; ++i) {
-      float v = pre<GELU>(__uint_as_float(((uint32_t)x[i]) << 16)) * r;
-      if (zero_dim) v = rbf(v);
+      float v = pre<GELU, XDT>(x16_bits<XDT>(x[i])) * r;
+      if (zero_dim) v = rx16<XDT>(v);
       v = clamp448(v);
       q[i] = (uint8_t)(e4m3x4(v, 0.0f, 0.0f, 0.0f) & 0xFF);
     }
@@ -74,17 +76,20 @@ __global__ __launch_bounds__(256) void k_fp8_quant(const uint16_t* x, const floa
 }
 
 // ------------------------------------------------------------ GELU table
-// The GELU quantizer reads R(gelu(x)) from a table: a bf16 input has 65536
-// patterns, so k_gelu_table evaluates the formula of pre<kGeluExact> once
-// per pattern (128 KiB of bf16 results, written on every call; every call
-// writes the same values) and the streaming kernel looks each element up in
-// an LDS copy of it, which makes the pass HBM-bound instead of bound by
-// tanhf's VALU work. The table lives in a file-scope device array per GPU;
-// its address comes from hipGetSymbolAddress.
-static __device__ __align__(256) uint16_t gelu_table[65536];
+// The GELU quantizer reads gelu(x) rounded to x's dtype from a table: a
+// 16-bit input has 65536 patterns, so k_gelu_table evaluates the formula of
+// pre<kGeluExact, XDT> once per pattern (128 KiB of results) and the
+// streaming kernel looks each element up in an LDS copy of it, which makes
+// the pass HBM-bound instead of bound by tanhf's VALU work. The tables (one
+// per dtype) live in file-scope device arrays per GPU, built by the first
+// call on a GPU and only read after that (oga_gelu_tanh_fp8_quantize_e4m3).
+static __device__ __align__(256) uint16_t gelu_table_bf16[65536];
+static __device__ __align__(256) uint16_t gelu_table_f16[65536];
+template <int XDT>
 __global__ __launch_bounds__(256) void k_gelu_table(uint16_t* table) {
   const uint32_t i = blockIdx.x * 256 + threadIdx.x;  // grid: 256 x 256
-  table[i] = (uint16_t)(__float_as_uint(pre<kGeluExact>(__uint_as_float(i << 16))) >> 16);
+  const float g = pre<kGeluExact, XDT>(x16_bits<XDT>(i));
+  table[i] = XDT == OGA_DT_F16 ? __builtin_bit_cast(uint16_t, (_Float16)g) : (uint16_t)(__float_as_uint(g) >> 16);
 }
 
 // q = e4m3(clamp(table[x] * r)) with the rounding rule of k_fp8_quant. One
@@ -92,6 +97,7 @@ __global__ __launch_bounds__(256) void k_gelu_table(uint16_t* table) {
 // tensor in steps of gridDim.x * 1024 lanes * 32 elements; per step a lane
 // converts two 16-element groups with all four 16-byte loads in flight.
 constexpr int kGeluLanes = 1024;
+template <int XDT>
 __global__ __launch_bounds__(kGeluLanes) void k_gelu_quant(const uint16_t* x, const float* scale, int zero_dim,
                                                            uint8_t* q, int64_t n, const uint16_t* table) {
   __shared__ uint4 tab[65536 * 2 / 16];
@@ -99,10 +105,10 @@ __global__ __launch_bounds__(kGeluLanes) void k_gelu_quant(const uint16_t* x, co
   __syncthreads();
   const uint16_t* const t16 = (const uint16_t*)tab;
   float r = 1.0f / scale[0];
-  if (zero_dim) r = rbf(r);
-  auto code = [&](uint32_t xb) {  // one element, x as bf16 bits
-    float v = __uint_as_float((uint32_t)t16[xb] << 16) * r;
-    if (zero_dim) v = rbf(v);
+  if (zero_dim) r = rx16<XDT>(r);
+  auto code = [&](uint32_t xb) {  // one element, x as its 16 bits
+    float v = x16_bits<XDT>(t16[xb]) * r;
+    if (zero_dim) v = rx16<XDT>(v);
     return clamp448(v);
   };
   auto conv16 = [&](const uint4& u0, const uint4& u1, int64_t i0) {
@@ -147,10 +153,11 @@ __global__ __launch_bounds__(kGeluLanes) void k_gelu_quant(const uint16_t* x, co
 
 // ------------------------------------------------------------ per head
 // The amax of |x| is taken on bit patterns: with the sign bit cleared, a
-// bf16 (or float32) pattern orders as its magnitude, and every NaN pattern
-// lies above infinity, so the maximum is NaN when any element is NaN, as
-// torch's amax gives. Two bf16 magnitudes are kept per dword and combined
-// with one packed 16-bit max.
+// bf16, fp16 (or float32) pattern orders as its magnitude, and every NaN
+// pattern lies above infinity, so the maximum is NaN when any element is
+// NaN, as torch's amax gives. Two 16-bit magnitudes are kept per dword and
+// combined with one packed 16-bit max; the float32 conversion of the
+// largest keeps the order.
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 OGA_DEVICE u16x2 abs_bits2(uint32_t w) { return __builtin_bit_cast(u16x2, w & 0x7FFF7FFFu); }
 OGA_DEVICE uint32_t umax_dpp(uint32_t v, int ctrl) {
@@ -169,7 +176,7 @@ OGA_DEVICE uint32_t umax_dpp(uint32_t v, int ctrl) {
 // TPB/4 token rows; lane l of vector step j sees head (j*512 + 8l) / D.
 // partial[b, h, chunk] = max |x| over the block as a float32 bit pattern
 // (a head's partials are contiguous for the reduction in pass 2).
-template <int CH, int D, int TPB>
+template <int CH, int D, int TPB, int XDT>
 __global__ __launch_bounds__(256) void k_head_amax(const uint16_t* x, float* partial, int64_t tokens, int nchunk) {
   constexpr int H = CH * 512 / D;
   constexpr int LPH = D / 8;  // lanes per head inside one vector step
@@ -210,7 +217,8 @@ __global__ __launch_bounds__(256) void k_head_amax(const uint16_t* x, float* par
   // Reduce over the lanes of one head: 16 lanes (D=128) or 8 lanes (D=64).
 #pragma unroll
   for (int j = 0; j < CH; ++j) {
-    uint32_t v = max((uint32_t)m[j].x, (uint32_t)m[j].y) << 16;  // float32 pattern of the bf16 magnitude
+    // float32 pattern of the largest magnitude
+    uint32_t v = __float_as_uint(x16_bits<XDT>(max((uint32_t)m[j].x, (uint32_t)m[j].y)));
     v = umax_dpp(v, 0);
     v = umax_dpp(v, 1);
     v = umax_dpp(v, 2);
@@ -231,7 +239,7 @@ __global__ __launch_bounds__(256) void k_head_amax(const uint16_t* x, float* par
 // (16 bytes each), so every load is a whole 2*D-byte slice and every store
 // a whole D-byte slice.
 constexpr int kQuantTokens = 64;
-template <int D>
+template <int D, int XDT>
 __global__ __launch_bounds__(256) void k_head_scale_quant(const uint16_t* x, const float* partial, float* scale_out,
                                                           uint8_t* q, int64_t tokens, int heads, int nchunk) {
   constexpr int LPT = D / 8;      // lanes per token slice
@@ -302,7 +310,7 @@ __global__ __launch_bounds__(256) void k_head_scale_quant(const uint16_t* x, con
     if (t < t1) {
       const int64_t e0 = ((b * tokens + t) * heads + h) * D + sub * 8;
       float f[8];
-      unpack8(xv[i], f);
+      unpack8x<XDT>(xv[i], f);
 #pragma unroll
       for (int k = 0; k < 8; ++k) f[k] = clamp448(div(f[k]));
       typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
@@ -325,62 +333,148 @@ constexpr int kHeadTokensPerBlock = 16;
 
 static int64_t head_chunks(int64_t tokens) { return (tokens + kHeadTokensPerBlock - 1) / kHeadTokensPerBlock; }
 
-template <int CH, int D>
+template <int CH, int D, int XDT>
 static void launch_head_amax(const uint16_t* x, float* partial, int64_t batch, int64_t tokens, hipStream_t st) {
   const int nchunk = (int)head_chunks(tokens);
-  hipLaunchKernelGGL((k_head_amax<CH, D, kHeadTokensPerBlock>), dim3((unsigned)nchunk, (unsigned)batch), dim3(256), 0,
-                     st, x, partial, tokens, nchunk);
+  hipLaunchKernelGGL((k_head_amax<CH, D, kHeadTokensPerBlock, XDT>), dim3((unsigned)nchunk, (unsigned)batch),
+                     dim3(256), 0, st, x, partial, tokens, nchunk);
 }
+
+template <int XDT>
+static void launch_per_head(const uint16_t* xs, uint8_t* q, float* scale_out, float* partial, int64_t batch,
+                            int64_t tokens, int64_t heads, int64_t head_dim, hipStream_t st) {
+  const int ch = (int)(heads * head_dim / 512);
+  if (head_dim == 128) {
+    if (ch == 8) launch_head_amax<8, 128, XDT>(xs, partial, batch, tokens, st);
+    else if (ch == 4) launch_head_amax<4, 128, XDT>(xs, partial, batch, tokens, st);
+    else launch_head_amax<2, 128, XDT>(xs, partial, batch, tokens, st);
+  } else {
+    if (ch == 8) launch_head_amax<8, 64, XDT>(xs, partial, batch, tokens, st);
+    else if (ch == 4) launch_head_amax<4, 64, XDT>(xs, partial, batch, tokens, st);
+    else launch_head_amax<2, 64, XDT>(xs, partial, batch, tokens, st);
+  }
+  const dim3 qgrid((unsigned)((tokens + kQuantTokens - 1) / kQuantTokens), (unsigned)heads, (unsigned)batch);
+  if (head_dim == 128)
+    hipLaunchKernelGGL((k_head_scale_quant<128, XDT>), qgrid, dim3(256), 0, st, xs, partial, scale_out, q, tokens,
+                       (int)heads, (int)head_chunks(tokens));
+  else
+    hipLaunchKernelGGL((k_head_scale_quant<64, XDT>), qgrid, dim3(256), 0, st, xs, partial, scale_out, q, tokens,
+                       (int)heads, (int)head_chunks(tokens));
+}
+
+static bool x16_dt_ok(int dt) { return dt == OGA_DT_BF16 || dt == OGA_DT_F16; }
 
 }  // namespace oga
 
 using namespace oga;
 
-extern "C" int oga_fp8_quantize_e4m3(const void* x, const float* scale, int scale_is_0dim, void* q, int64_t n,
-                                     void* stream) {
+extern "C" int oga_fp8_quantize_e4m3(const void* x, int x_dtype, const float* scale, int scale_is_0dim, void* q,
+                                     int64_t n, void* stream) {
   if (!x || !scale || !q) return fail("null pointer");
+  if (!x16_dt_ok(x_dtype)) return unsupported("x dtype must be bf16 or fp16");
   if (n < 0) return fail("bad size");
   if (n == 0) return OGA_OK;
   if (!aligned(x, 16) || !aligned(q, 16)) return fail("x/q must be 16-byte aligned");
   const int64_t threads = (n + 15) / 16;
-  hipLaunchKernelGGL(k_fp8_quant<kGeluNone>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
-                     (const uint16_t*)x, scale, scale_is_0dim ? 1 : 0, (uint8_t*)q, n);
+  const dim3 grid((unsigned)((threads + 255) / 256));
+  if (x_dtype == OGA_DT_F16)
+    hipLaunchKernelGGL((k_fp8_quant<kGeluNone, OGA_DT_F16>), grid, dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t*)x, scale, scale_is_0dim ? 1 : 0, (uint8_t*)q, n);
+  else
+    hipLaunchKernelGGL((k_fp8_quant<kGeluNone, OGA_DT_BF16>), grid, dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t*)x, scale, scale_is_0dim ? 1 : 0, (uint8_t*)q, n);
   return launch_status();
 }
 
-// Per-GPU address of the GELU table (hipGetSymbolAddress, once per device).
-static std::atomic<void*> g_gelu_table[64];
-static int gelu_table_ptr(uint16_t** out) {
+// The GELU tables of a GPU: built once, by the first call on that GPU, on
+// the caller's stream. Until the build is known to have completed, a call
+// on any stream waits for it through an event recorded behind it (no host
+// synchronisation); from then on calls only read the table. A call made
+// while its stream is being captured into a graph, before the table is
+// complete, puts the build into the graph instead (the graph then builds
+// the table, with the same values, each time it runs).
+namespace {
+constexpr int kMaxGeluDevices = 64;
+enum { kTableNone = 0, kTablePending = 1, kTableReady = 2 };
+struct GeluTable {
+  std::mutex mu;
+  std::atomic<int> state{kTableNone};
+  void* ptr = nullptr;
+  hipEvent_t built = nullptr;
+};
+GeluTable g_gelu[2][kMaxGeluDevices];  // [bf16, fp16][device]
+}  // namespace
+
+static int gelu_table(int x_dtype, hipStream_t st, uint16_t** out) {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail("no current device");
-  void* p = g_gelu_table[dev].load(std::memory_order_acquire);
-  if (!p) {
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(gelu_table));
-    if (e != hipSuccess) return (int)e;
-    g_gelu_table[dev].store(p, std::memory_order_release);
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxGeluDevices) return unsupported("device ordinal %d beyond %d", dev, kMaxGeluDevices);
+  GeluTable& t = g_gelu[x_dtype == OGA_DT_F16 ? 1 : 0][dev];
+  if (t.state.load(std::memory_order_acquire) == kTableReady) {
+    *out = (uint16_t*)t.ptr;
+    return OGA_OK;
   }
-  *out = (uint16_t*)p;
-  return OGA_OK;
+  std::lock_guard<std::mutex> lock(t.mu);
+  if (!t.ptr) {
+    e = x_dtype == OGA_DT_F16 ? hipGetSymbolAddress(&t.ptr, HIP_SYMBOL(gelu_table_f16))
+                              : hipGetSymbolAddress(&t.ptr, HIP_SYMBOL(gelu_table_bf16));
+    if (e != hipSuccess) return (int)e;
+    if (!t.ptr) return fail("GELU table has no device address");
+  }
+  *out = (uint16_t*)t.ptr;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  e = hipStreamIsCapturing(st, &cap);
+  if (e != hipSuccess) return (int)e;
+  auto build = [&]() {
+    if (x_dtype == OGA_DT_F16)
+      hipLaunchKernelGGL(k_gelu_table<OGA_DT_F16>, dim3(256), dim3(256), 0, st, (uint16_t*)t.ptr);
+    else
+      hipLaunchKernelGGL(k_gelu_table<OGA_DT_BF16>, dim3(256), dim3(256), 0, st, (uint16_t*)t.ptr);
+    return launch_status();
+  };
+  // Under capture the graph builds the table itself (same values), so it
+  // never depends on an event recorded outside the graph.
+  if (cap != hipStreamCaptureStatusNone) return build();
+  if (t.state.load(std::memory_order_relaxed) == kTableNone) {
+    int rc = build();
+    if (rc) return rc;
+    if (!t.built && (e = hipEventCreateWithFlags(&t.built, hipEventDisableTiming)) != hipSuccess) return (int)e;
+    if ((e = hipEventRecord(t.built, st)) != hipSuccess) return (int)e;
+    t.state.store(kTablePending, std::memory_order_release);
+    return OGA_OK;
+  }
+  // Pending: done already, or make this stream wait for it.
+  e = hipEventQuery(t.built);
+  if (e == hipSuccess) {
+    t.state.store(kTableReady, std::memory_order_release);
+    return OGA_OK;
+  }
+  if (e != hipErrorNotReady) return (int)e;
+  e = hipStreamWaitEvent(st, t.built, 0);
+  return e == hipSuccess ? OGA_OK : (int)e;
 }
 
-extern "C" int oga_gelu_tanh_fp8_quantize_e4m3(const void* x, const float* scale, int scale_is_0dim, void* q,
-                                               int64_t n, void* stream) {
+extern "C" int oga_gelu_tanh_fp8_quantize_e4m3(const void* x, int x_dtype, const float* scale, int scale_is_0dim,
+                                               void* q, int64_t n, void* stream) {
   if (!x || !scale || !q) return fail("null pointer");
+  if (!x16_dt_ok(x_dtype)) return unsupported("x dtype must be bf16 or fp16");
   if (n < 0) return fail("bad size");
   if (n == 0) return OGA_OK;
   if (!aligned(x, 16) || !aligned(q, 16)) return fail("x/q must be 16-byte aligned");
-  uint16_t* table = nullptr;
-  int rc = gelu_table_ptr(&table);
-  if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(k_gelu_table, dim3(256), dim3(256), 0, st, table);
-  rc = launch_status();
+  uint16_t* table = nullptr;
+  int rc = gelu_table(x_dtype, st, &table);
   if (rc) return rc;
   // Steps of 1024 lanes x 32 elements; at most one workgroup per CU.
   const int64_t steps = (n + 32 * kGeluLanes - 1) / (32 * kGeluLanes);
   const int64_t wgs = steps < (int64_t)cu_count() ? steps : (int64_t)cu_count();
-  hipLaunchKernelGGL(k_gelu_quant, dim3((unsigned)wgs), dim3(kGeluLanes), 0, st, (const uint16_t*)x, scale,
-                     scale_is_0dim ? 1 : 0, (uint8_t*)q, n, (const uint16_t*)table);
+  if (x_dtype == OGA_DT_F16)
+    hipLaunchKernelGGL(k_gelu_quant<OGA_DT_F16>, dim3((unsigned)wgs), dim3(kGeluLanes), 0, st, (const uint16_t*)x,
+                       scale, scale_is_0dim ? 1 : 0, (uint8_t*)q, n, (const uint16_t*)table);
+  else
+    hipLaunchKernelGGL(k_gelu_quant<OGA_DT_BF16>, dim3((unsigned)wgs), dim3(kGeluLanes), 0, st, (const uint16_t*)x,
+                       scale, scale_is_0dim ? 1 : 0, (uint8_t*)q, n, (const uint16_t*)table);
   return launch_status();
 }
 
@@ -393,35 +487,22 @@ extern "C" int64_t oga_fp8_per_head_workspace_bytes(int64_t batch, int64_t token
 // Both passes of the per-head quantizer with the amax partials in `partial`
 // (batch * head_chunks(tokens) * heads floats; pass 1 writes every one that
 // pass 2 reads, so nothing needs clearing).
-static int per_head_run(const void* x, void* q, float* scale_out, float* partial, int64_t batch, int64_t tokens,
-                        int64_t heads, int64_t head_dim, hipStream_t st) {
+static int per_head_run(const void* x, int x_dtype, void* q, float* scale_out, float* partial, int64_t batch,
+                        int64_t tokens, int64_t heads, int64_t head_dim, hipStream_t st) {
   if (!x || !q || !scale_out || !partial) return fail("null pointer");
+  if (!x16_dt_ok(x_dtype)) return unsupported("x dtype must be bf16 or fp16");
   if (batch < 1 || tokens < 1 || heads < 1) return fail("empty shape");
   if (batch > 65535) return unsupported("batch > 65535");
   if (head_dim != 64 && head_dim != 128) return unsupported("head_dim must be 64 or 128");
   const int64_t row = heads * head_dim;
   if (row != 1024 && row != 2048 && row != 4096) return unsupported("heads*head_dim must be 1024, 2048 or 4096");
   if (!aligned(x, 16) || !aligned(q, 16)) return fail("x/q must be 16-byte aligned");
-  const uint16_t* xs = (const uint16_t*)x;
-  const int ch = (int)(row / 512);
-  if (head_dim == 128) {
-    if (ch == 8) launch_head_amax<8, 128>(xs, partial, batch, tokens, st);
-    else if (ch == 4) launch_head_amax<4, 128>(xs, partial, batch, tokens, st);
-    else launch_head_amax<2, 128>(xs, partial, batch, tokens, st);
-  } else {
-    if (ch == 8) launch_head_amax<8, 64>(xs, partial, batch, tokens, st);
-    else if (ch == 4) launch_head_amax<4, 64>(xs, partial, batch, tokens, st);
-    else launch_head_amax<2, 64>(xs, partial, batch, tokens, st);
-  }
-  int rc = launch_status();
-  if (rc) return rc;
-  const dim3 qgrid((unsigned)((tokens + kQuantTokens - 1) / kQuantTokens), (unsigned)heads, (unsigned)batch);
-  if (head_dim == 128)
-    hipLaunchKernelGGL(k_head_scale_quant<128>, qgrid, dim3(256), 0, st, xs, partial, scale_out, (uint8_t*)q, tokens,
-                       (int)heads, (int)head_chunks(tokens));
+  if (x_dtype == OGA_DT_F16)
+    launch_per_head<OGA_DT_F16>((const uint16_t*)x, (uint8_t*)q, scale_out, partial, batch, tokens, heads, head_dim,
+                                st);
   else
-    hipLaunchKernelGGL(k_head_scale_quant<64>, qgrid, dim3(256), 0, st, xs, partial, scale_out, (uint8_t*)q, tokens,
-                       (int)heads, (int)head_chunks(tokens));
+    launch_per_head<OGA_DT_BF16>((const uint16_t*)x, (uint8_t*)q, scale_out, partial, batch, tokens, heads,
+                                 head_dim, st);
   return launch_status();
 }
 
@@ -454,16 +535,19 @@ static int scratch_ptr(float** out) {
   return OGA_OK;
 }
 
-extern "C" int oga_fp8_quantize_per_head(const void* x, void* q, float* scale_out, void* workspace, int64_t batch,
-                                         int64_t tokens, int64_t heads, int64_t head_dim, void* stream) {
+extern "C" int oga_fp8_quantize_per_head(const void* x, int x_dtype, void* q, float* scale_out, void* workspace,
+                                         int64_t batch, int64_t tokens, int64_t heads, int64_t head_dim,
+                                         void* stream) {
   if (!workspace) return fail("null pointer");
-  return per_head_run(x, q, scale_out, (float*)workspace, batch, tokens, heads, head_dim, (hipStream_t)stream);
+  return per_head_run(x, x_dtype, q, scale_out, (float*)workspace, batch, tokens, heads, head_dim,
+                      (hipStream_t)stream);
 }
 
 extern "C" int64_t oga_fp8_per_head_noalloc_max_bytes(void) { return kPerHeadScratchBytes; }
 
-extern "C" int oga_fp8_quantize_per_head_noalloc(const void* x, void* q, float* scale_out, int64_t batch,
-                                                 int64_t tokens, int64_t heads, int64_t head_dim, void* stream) {
+extern "C" int oga_fp8_quantize_per_head_noalloc(const void* x, int x_dtype, void* q, float* scale_out,
+                                                 int64_t batch, int64_t tokens, int64_t heads, int64_t head_dim,
+                                                 void* stream) {
   if (batch < 1 || tokens < 1 || heads < 1) return fail("empty shape");
   const int64_t need = oga_fp8_per_head_workspace_bytes(batch, tokens, heads, head_dim);
   if (need > kPerHeadScratchBytes)
@@ -473,7 +557,7 @@ extern "C" int oga_fp8_quantize_per_head_noalloc(const void* x, void* q, float* 
   float* partial = nullptr;
   const int rc = scratch_ptr(&partial);
   if (rc) return rc;
-  return per_head_run(x, q, scale_out, partial, batch, tokens, heads, head_dim, (hipStream_t)stream);
+  return per_head_run(x, x_dtype, q, scale_out, partial, batch, tokens, heads, head_dim, (hipStream_t)stream);
 }
 
 extern "C" int oga_selftest_convert(const float* in, uint16_t* bf16_out, uint8_t* e4m3_out, int64_t n, void* stream) {

@@ -57,6 +57,13 @@ __all__ = [
     "fp8_qkv_from_packed_requant",
     "collect_video_qkv_packed_linear_stats",
     "collect_video_qkv_packed_requant_stats",
+    "collect_video_qkv_grouped_mm_stats",
+    "collect_video_qk_grouped_mm_stats",
+    "reset_video_qkv_grouped_mm_stats",
+    "reset_video_qk_grouped_mm_stats",
+    "reset_video_qkv_packed_stats",
+    "set_frozen_fp8_scales",
+    "frozen_fp8_scales",
 ]
 
 _FP8 = torch.float8_e4m3fn
@@ -133,12 +140,25 @@ def _dt(t: torch.Tensor) -> int:
     return _lib.DT_BF16 if t.dtype == torch.bfloat16 else _lib.DT_F32
 
 
+def _xdt(t: torch.Tensor) -> int:
+    """dtype code of a 16-bit activation (bf16 or fp16)."""
+    return _lib.DT_F16 if t.dtype == torch.float16 else _lib.DT_BF16
+
+
 def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
+
+
+def _aligned(t: torch.Tensor, nbytes: int = 16) -> bool:
+    """The C ABI's pointer precondition for a tensor it reads with 128-bit
+    (or wider) vectors. A contiguous view at an odd storage offset passes the
+    reference's guards but not this one, so it takes the torch path instead
+    of an argument error from the library."""
+    return t.data_ptr() % nbytes == 0
 
 
 # --------------------------------------------------------------------------
@@ -203,10 +223,13 @@ def _simple_residual_gate(x: torch.Tensor, y: torch.Tensor, gate: torch.Tensor) 
 # counterpart: a missing library raises instead of falling back)
 # --------------------------------------------------------------------------
 def _can_use_ada_from_table(x: torch.Tensor, scale_shift_table: torch.Tensor, timestep: torch.Tensor) -> bool:
-    """:1001-1018"""
+    """:1001-1018, plus the HIP kernels' own needs: x 16-byte aligned and at
+    most 65535 batches (one grid row per batch)."""
     if not x.is_cuda or not x.is_contiguous() or x.dtype != torch.bfloat16:
         return False
     if x.ndim != 3 or x.shape[-1] not in (2048, 4096):
+        return False
+    if not _aligned(x) or x.shape[0] > 65535:
         return False
     if not scale_shift_table.is_cuda or scale_shift_table.dtype not in (torch.bfloat16, torch.float32):
         return False
@@ -222,13 +245,16 @@ def _can_use_ada_from_table(x: torch.Tensor, scale_shift_table: torch.Tensor, ti
 
 
 def _can_use_fused_fp8_quantize(x: torch.Tensor, input_scale: torch.Tensor) -> bool:
-    """:1021-1022. The HIP kernel reads bf16 and a float32 scale on the GPU."""
+    """:1021-1022 (bf16 or fp16 x). The HIP kernel also needs x 16-byte
+    aligned and a float32 scale on x's device."""
     return (
         x.is_cuda
         and x.is_contiguous()
         and input_scale.numel() == 1
-        and x.dtype == torch.bfloat16
+        and x.dtype in (torch.bfloat16, torch.float16)
+        and _aligned(x)
         and input_scale.is_cuda
+        and input_scale.device == x.device
         and input_scale.dtype == torch.float32
     )
 
@@ -245,8 +271,11 @@ def _can_use_fused_bias_add(x: torch.Tensor, bias: torch.Tensor) -> bool:
 
 
 def _can_use_fused_fp8_quantize_per_head_4d(x: torch.Tensor) -> bool:
-    """:1489-1499, plus the HIP kernel's layout needs (H*D in {1024,2048,4096})."""
-    if not x.is_cuda or not x.is_contiguous() or x.dtype != torch.bfloat16:
+    """:1489-1499 (bf16 or fp16 x), plus the HIP kernel's layout needs (H*D in
+    {1024, 2048, 4096}, x 16-byte aligned)."""
+    if not x.is_cuda or not x.is_contiguous() or x.dtype not in (torch.bfloat16, torch.float16):
+        return False
+    if not _aligned(x):
         return False
     if x.ndim != 4:
         return False
@@ -278,7 +307,20 @@ def _fused_video_qk_rmsnorm_rope_guard_reason(q, k, q_weight, k_weight, cos, sin
         return "weight_dtype"
     if cos.dtype != sin.dtype or cos.dtype not in (torch.bfloat16, torch.float32):
         return "rope_dtype"
+    if not _aligned(q) or not _aligned(k):
+        return "qk_alignment"
+    if not _vec_ok(q_weight, q_weight.dtype) or not _vec_ok(k_weight, q_weight.dtype):
+        return "weight_alignment"
     return None
+
+
+def _vec_ok(t: torch.Tensor, dtype: torch.dtype) -> bool:
+    """A parameter vector the HIP kernels read 8 elements at a time, as the
+    wrapper passes it (`t.to(dtype).contiguous()`): a copy is aligned; the
+    tensor itself must start on an 8-element boundary."""
+    if t.dtype != dtype or not t.is_contiguous():
+        return True
+    return _aligned(t, 8 * t.element_size())
 
 
 def _can_use_fused_video_qk_rmsnorm_rope(q, k, q_weight, k_weight, cos, sin) -> bool:
@@ -298,6 +340,8 @@ def _fused_video_qkv_rmsnorm_rope_pack_guard_reason(q, k, v, q_weight, k_weight,
         return "v_noncontiguous"
     if v.dtype != q.dtype:
         return "v_dtype"
+    if not _aligned(v):
+        return "v_alignment"
     return None
 
 
@@ -311,16 +355,19 @@ def _can_use_fused_video_qk_bias_rmsnorm_rope(q, k, q_bias, k_bias, q_weight, k_
         return False
     if q_bias.dtype not in (torch.bfloat16, torch.float32) or k_bias.dtype != q_bias.dtype:
         return False
-    return True
+    return _vec_ok(q_bias, q_bias.dtype) and _vec_ok(k_bias, q_bias.dtype)
 
 
 def _can_use_fused_residual_gate(x: torch.Tensor, y: torch.Tensor, gate: torch.Tensor) -> bool:
-    """:1596-1609"""
+    """:1596-1609, plus the HIP kernel's needs: x and y 16-byte aligned, at
+    most 65535 batches."""
     if not x.is_cuda or not y.is_cuda or x.dtype != torch.bfloat16 or y.dtype != torch.bfloat16:
         return False
     if x.shape != y.shape or x.ndim < 2 or x.shape[-1] not in (2048, 4096):
         return False
     if not x.is_contiguous() or not y.is_contiguous():
+        return False
+    if not _aligned(x) or not _aligned(y) or (x.ndim == 3 and x.shape[0] > 65535):
         return False
     if not gate.is_cuda or gate.dtype != torch.bfloat16:
         return False
@@ -344,7 +391,8 @@ def _can_use_fused_head_gate_mul(out: torch.Tensor, gates: torch.Tensor, heads: 
 
 def _can_use_fused_adazero(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor) -> bool:
     """:1626-1637, plus conditions the reference's kernel needs but does not
-    check (contiguous x) and dtype/device conditions of the HIP kernel."""
+    check (contiguous x) and dtype/device/alignment conditions of the HIP
+    kernel (x 16-byte aligned, at most 65535 batches)."""
     if not x.is_cuda or x.dtype != torch.bfloat16:
         return False
     if x.ndim < 2 or x.shape[-1] not in (2048, 4096):
@@ -356,6 +404,8 @@ def _can_use_fused_adazero(x: torch.Tensor, scale: torch.Tensor, shift: torch.Te
     if scale.numel() != shift.numel():
         return False
     if not x.is_contiguous() or x.ndim > 3:
+        return False
+    if not _aligned(x) or (x.ndim == 3 and x.shape[0] > 65535):
         return False
     if not scale.is_cuda or not shift.is_cuda:
         return False
@@ -559,7 +609,7 @@ def fused_residual_gate_from_ada(
             scale_shift_table, timestep, x.shape[0], x.shape[1], x.shape[-1], gate_index
         )
         return _simple_residual_gate(x, y, gate)
-    if y.dtype != torch.bfloat16 or not y.is_cuda:
+    if y.dtype != torch.bfloat16 or not y.is_cuda or not _aligned(y):
         _fallback("fused_residual_gate_from_ada", x, y)
         (gate,) = _torch_ada_values_from_table(
             scale_shift_table, timestep, x.shape[0], x.shape[1], x.shape[-1], gate_index
@@ -597,6 +647,8 @@ def fused_residual_gate_bias_from_ada(
         or not y_no_bias.is_contiguous()
         or y_no_bias.shape != x.shape
         or not _can_use_fused_bias_add(y_no_bias, bias)
+        or not _aligned(y_no_bias)
+        or not (not bias.is_contiguous() or _aligned(bias, 32))
     ):
         _fallback("fused_residual_gate_bias_from_ada", x, y_no_bias, bias, scale_shift_table, timestep)
         y = y_no_bias + bias.to(y_no_bias.dtype)
@@ -675,8 +727,8 @@ def fused_fp8_quantize_e4m3(x: torch.Tensor, input_scale: torch.Tensor) -> torch
         return torch.clamp(x * input_scale.reciprocal(), fp8_min, fp8_max).to(_FP8)
     q = torch.empty_strided(x.shape, x.stride(), device=x.device, dtype=_FP8)
     _hip("fused_fp8_quantize_e4m3")
-    _lib.call("oga_fp8_quantize_e4m3", _ptr(x), _ptr(input_scale), int(input_scale.dim() == 0), _ptr(q), x.numel(),
-              _stream(x))
+    _lib.call("oga_fp8_quantize_e4m3", _ptr(x), _xdt(x), _ptr(input_scale), int(input_scale.dim() == 0), _ptr(q),
+              x.numel(), _stream(x))
     return q
 
 
@@ -694,7 +746,7 @@ def fused_gelu_tanh_fp8_quantize_e4m3(x: torch.Tensor, input_scale: torch.Tensor
         return torch.clamp(gelu * input_scale.reciprocal(), fp8_min, fp8_max).to(_FP8)
     q = torch.empty_strided(x.shape, x.stride(), device=x.device, dtype=_FP8)
     _hip("fused_gelu_tanh_fp8_quantize_e4m3")
-    _lib.call("oga_gelu_tanh_fp8_quantize_e4m3", _ptr(x), _ptr(input_scale), int(input_scale.dim() == 0), _ptr(q),
+    _lib.call("oga_gelu_tanh_fp8_quantize_e4m3", _ptr(x), _xdt(x), _ptr(input_scale), int(input_scale.dim() == 0), _ptr(q),
               x.numel(), _stream(x))
     return q
 
@@ -720,7 +772,7 @@ def fused_fp8_quantize_e4m3_per_head_4d(
     scale = torch.empty((batch, heads), device=x.device, dtype=torch.float32)
     q = torch.empty_strided(x.shape, x.stride(), device=x.device, dtype=_FP8)
     _hip("fused_fp8_quantize_e4m3_per_head_4d")
-    _lib.call("oga_fp8_quantize_per_head", _ptr(x), _ptr(q), _ptr(scale), _ptr(workspace), batch, tokens, heads,
+    _lib.call("oga_fp8_quantize_per_head", _ptr(x), _xdt(x), _ptr(q), _ptr(scale), _ptr(workspace), batch, tokens, heads,
               head_dim, _stream(x))
     return q, scale
 
@@ -975,19 +1027,60 @@ def _is_fp8_linear(linear) -> bool:
 
 
 _EQUAL_MEMO: dict = {}
+_FROZEN_SCALES = False
+
+
+def set_frozen_fp8_scales(frozen: bool) -> bool:
+    """Declares whether the FP8 linears' scale tensors stay fixed while the
+    flag is on (a loaded model's do). On: the Q/K/V guards remember the
+    result of comparing a tuple of scale tensors, which saves a
+    device-to-host synchronisation per call (each torch.equal on GPU tensors
+    is one, and it drains the launch queue in the middle of a block). The
+    remembered result is used only while every tensor is the same object,
+    with the same storage and, where torch tracks one, the same in-place
+    version counter; writes that bypass the counter (through `.data`, or
+    to an inference tensor inside inference mode) are not seen, which is
+    what the caller promises not to make. Off (the default): every call
+    compares, as the reference does (:1209-1214, :1258-1259). Returns the
+    previous setting."""
+    global _FROZEN_SCALES
+    prev = _FROZEN_SCALES
+    _FROZEN_SCALES = bool(frozen)
+    if not _FROZEN_SCALES:
+        _EQUAL_MEMO.clear()
+    return prev
+
+
+class frozen_fp8_scales:
+    """`with frozen_fp8_scales(): ...` turns set_frozen_fp8_scales on for the
+    block and restores the previous setting after it."""
+
+    def __enter__(self):
+        self._prev = set_frozen_fp8_scales(True)
+        return self
+
+    def __exit__(self, *exc):
+        set_frozen_fp8_scales(self._prev)
+        return False
+
+
+def _version_or_none(t: torch.Tensor):
+    """The in-place version counter, or None for a tensor without one (an
+    inference tensor: reading its `_version` raises)."""
+    try:
+        return t._version
+    except RuntimeError:
+        return None
 
 
 def _all_equal(tensors) -> bool:
     """torch.equal of every tensor with the first, as the reference's guards
-    evaluate it, remembered per tuple of tensors: on GPU tensors each
-    torch.equal is a device-to-host synchronisation, which stalls the launch
-    queue in the middle of a block, and a loaded model's scales do not change
-    between calls. The remembered result is used only while every tensor is
-    the same object (weak reference), with the same storage and the same
-    in-place version counter, so reassigning or modifying a scale in place
-    makes the next call compare again."""
+    evaluate it; remembered per tuple of tensors while
+    set_frozen_fp8_scales is on."""
+    if not _FROZEN_SCALES:
+        return all(torch.equal(tensors[0], t) for t in tensors[1:])
     key = tuple(id(t) for t in tensors)
-    state = tuple((t.data_ptr(), t._version) for t in tensors)
+    state = tuple((t.data_ptr(), _version_or_none(t)) for t in tensors)
     memo = _EQUAL_MEMO.get(key)
     if memo is not None:
         refs, old_state, result = memo
@@ -1113,14 +1206,138 @@ def fp8_qkv_from_shared_quantized_input(attn: torch.nn.Module, x: torch.Tensor):
             fp8_linear_from_quantized_e4m3(attn.to_v, qinput, out_dtype=x.dtype))
 
 
+# The grouped projections' bookkeeping, as the reference keeps it for
+# `fp8_qkv_from_grouped_mm` / `fp8_qk_from_grouped_mm` (:1926-1937,
+# :2114-2178): successful calls, fallbacks by reason (a guard's reason or an
+# exception's type name) and, for the first `checks` calls after a reset,
+# error statistics of the projections against the per-linear FP8 linears.
+_GROUPED_STATS = {
+    "qkv": {"calls": 0, "fallbacks": 0, "fallback_reasons": {}, "checks": [], "check_limit": 0},
+    "qk": {"calls": 0, "fallbacks": 0, "fallback_reasons": {}, "checks": [], "check_limit": 0},
+}
+_GROUPED_NAMES = {"qkv": ("to_q", "to_k", "to_v"), "qk": ("to_q", "to_k")}
+
+
+def _record_grouped_fallback(kind: str, reason: str) -> None:
+    """:2159-2176"""
+    st = _GROUPED_STATS[kind]
+    st["fallbacks"] += 1
+    st["fallback_reasons"][reason] = st["fallback_reasons"].get(reason, 0) + 1
+
+
+def _reset_grouped_stats(kind: str, checks: int) -> None:
+    st = _GROUPED_STATS[kind]
+    st["calls"] = 0
+    st["fallbacks"] = 0
+    st["fallback_reasons"] = {}
+    st["checks"] = []
+    st["check_limit"] = max(0, int(checks)) * len(_GROUPED_NAMES[kind])
+
+
+def reset_video_qkv_grouped_mm_stats(checks: int = 0) -> None:
+    """Zeroes the grouped Q/K/V counters as patch_ltx_video_qkv_grouped_mm(checks)
+    does (:2114-2123); the first `checks` calls are then compared with the
+    per-linear projections and recorded."""
+    _reset_grouped_stats("qkv", checks)
+
+
+def reset_video_qk_grouped_mm_stats(checks: int = 0) -> None:
+    """As reset_video_qkv_grouped_mm_stats for the grouped Q/K form (:2137-2146)."""
+    _reset_grouped_stats("qk", checks)
+
+
+def _collect_grouped(kind: str) -> dict:
+    st = _GROUPED_STATS[kind]
+    return {"calls": st["calls"], "fallbacks": st["fallbacks"], "fallback_reasons": dict(st["fallback_reasons"]),
+            "checks": list(st["checks"])}
+
+
+def collect_video_qkv_grouped_mm_stats() -> dict:
+    """:2127-2133"""
+    return _collect_grouped("qkv")
+
+
+def collect_video_qk_grouped_mm_stats() -> dict:
+    """:2150-2156"""
+    return _collect_grouped("qk")
+
+
+def _grouped_guard_reason(attn: torch.nn.Module, x: torch.Tensor, names: tuple[str, ...]) -> str | None:
+    """:1187-1233 (Q/K/V) and :1236-1278 (Q/K), with FP8Linear recognised by
+    its attributes and the same reasons as the reference records. The
+    reference's first three reasons (no torch._scaled_grouped_mm, ltx_core
+    import, the TRT-LLM branch) have no counterpart here: the grouped GEMM is
+    this library's."""
+    if not x.is_cuda or not x.is_contiguous() or x.dtype not in (torch.bfloat16, torch.float16):
+        return "input"
+    if x.ndim != 3 or x.shape[0] != 1 or x.shape[1] < 1 or x.shape[-1] != 4096:
+        return "shape"
+    linears = [getattr(attn, n, None) for n in names]
+    if not all(_is_fp8_linear(lin) for lin in linears):
+        return "linear_type"
+    if not all(getattr(lin, "bias", None) is not None for lin in linears):
+        return "bias"
+    if not _all_equal([lin.input_scale for lin in linears]):
+        return "input_scale"
+    feats = [_features(lin) for lin in linears]
+    if not all(fi == x.shape[-1] and fo == x.shape[-1] for fi, fo in feats):
+        return "features"
+    rows = x.shape[0] * x.shape[1]
+    if not (_scale_fits(linears[0].input_scale, rows)
+            and all(_scale_fits(lin.weight_scale, fo) for lin, (_, fo) in zip(linears, feats))):
+        return "scale_shape"
+    return None
+
+
+def _record_grouped_check(kind: str, attn: torch.nn.Module, x: torch.Tensor, outs) -> None:
+    """:1438-1486 — error statistics of the grouped projections against each
+    linear's own FP8 forward, for the first checks after a reset."""
+    st = _GROUPED_STATS[kind]
+    if len(st["checks"]) >= st["check_limit"]:
+        return
+    with torch.no_grad():
+        for name, out in zip(("q", "k", "v"), outs):
+            ref = fp8_linear_forward(getattr(attn, "to_" + name), x)
+            diff = (out.float() - ref.float()).abs()
+            denom = ref.float().abs().clamp_min(1e-6)
+            st["checks"].append({"tensor": name, "max_abs": float(diff.max().item()),
+                                 "mean_abs": float(diff.mean().item()),
+                                 "rms": float(torch.sqrt(torch.mean(diff.square())).item()),
+                                 "mean_rel": float((diff / denom).mean().item())})
+
+
+def _grouped_projections(kind: str, attn: torch.nn.Module, x: torch.Tensor):
+    """The body of fp8_qkv_from_grouped_mm / fp8_qk_from_grouped_mm: guard
+    (reason recorded), one quantization with to_q's input scale, one grouped
+    GEMM launch; an exception is recorded by type and gives None, as the
+    reference's try/except does (:919-921, :953-955). Under
+    OPENGENIE_AMD_STRICT the exception propagates instead."""
+    reason = _grouped_guard_reason(attn, x, _GROUPED_NAMES[kind])
+    if reason is not None:
+        _record_grouped_fallback(kind, reason)
+        return None
+    try:
+        linears = tuple(getattr(attn, n) for n in _GROUPED_NAMES[kind])
+        qinput = fused_fp8_quantize_e4m3(x.contiguous(), attn.to_q.input_scale)
+        outs = _fp8_grouped_linear(linears, qinput, x.dtype)
+        _record_grouped_check(kind, attn, x, outs)
+        _GROUPED_STATS[kind]["calls"] += 1
+        return outs
+    except _lib.LibraryMissing:
+        raise
+    except Exception as exc:
+        if _strict():
+            raise
+        _record_grouped_fallback(kind, type(exc).__name__)
+        return None
+
+
 def fp8_qkv_from_grouped_mm(attn: torch.nn.Module, x: torch.Tensor):
     """:890-925 — exact Q/K/V projections as one grouped FP8 GEMM with each
     linear's own weight scale and bias (one launch over the three linears'
-    tiles); None when the guard fails."""
-    if not _can_use_video_qkv_shared(attn, x, ("to_q", "to_k", "to_v"), grouped=True):
-        return None
-    qinput = fused_fp8_quantize_e4m3(x.contiguous(), attn.to_q.input_scale)
-    return _fp8_grouped_linear((attn.to_q, attn.to_k, attn.to_v), qinput, x.dtype)
+    tiles); None when the guard fails or the launch raises (reason recorded,
+    collect_video_qkv_grouped_mm_stats)."""
+    return _grouped_projections("qkv", attn, x)
 
 
 def fp8_qkv_from_quantized_e4m3(attn: torch.nn.Module, qinput: torch.Tensor, *, out_dtype: torch.dtype):
@@ -1136,11 +1353,9 @@ def fp8_qkv_from_quantized_e4m3(attn: torch.nn.Module, qinput: torch.Tensor, *, 
 
 def fp8_qk_from_grouped_mm(attn: torch.nn.Module, x: torch.Tensor):
     """:927-955 — exact Q/K projections as one grouped FP8 GEMM; None when the
-    guard fails."""
-    if not _can_use_video_qkv_shared(attn, x, ("to_q", "to_k"), grouped=True):
-        return None
-    qinput = fused_fp8_quantize_e4m3(x.contiguous(), attn.to_q.input_scale)
-    return _fp8_grouped_linear((attn.to_q, attn.to_k), qinput, x.dtype)
+    guard fails or the launch raises (reason recorded,
+    collect_video_qk_grouped_mm_stats)."""
+    return _grouped_projections("qk", attn, x)
 
 
 # --------------------------------------------------------------------------
@@ -1256,6 +1471,8 @@ def fp8_qkv_from_packed_linear(attn: torch.nn.Module, x: torch.Tensor):
     except _lib.LibraryMissing:
         raise
     except Exception as exc:  # the reference counts the exception and returns None (:847-849)
+        if _strict():
+            raise
         _record_packed_fallback("packed_linear", type(exc).__name__)
         return None
 
@@ -1330,5 +1547,7 @@ def fp8_qkv_from_packed_requant(attn: torch.nn.Module, x: torch.Tensor):
     except _lib.LibraryMissing:
         raise
     except Exception as exc:  # :884-886
+        if _strict():
+            raise
         _record_packed_fallback("packed_requant", type(exc).__name__)
         return None

@@ -26,6 +26,7 @@ from .numerics import (
     e4m3_encode,
     f32,
     mul,
+    round_to,
     sub,
 )
 
@@ -150,17 +151,20 @@ def fp8_quantize_e4m3(x: T, input_scale: float, scale_is_0dim: bool, device: str
     """`fused_fp8_quantize_e4m3` torch path (:146-148) -> uint8 e4m3fn codes.
 
     clamp(x * input_scale.reciprocal(), -448, 448).to(float8_e4m3fn), with
-    r = float32(1 / s). Dtype of `x * r`: a 0-dim scale does not promote, so
-    the product is bf16 (rounded); a (1,)-shaped scale makes it float32.
-    On a GPU the 0-dim float32 operand is itself converted to the common
-    dtype (bf16) before the multiply (TensorIterator casts non-CPU-scalar
-    inputs to the common dtype); a 0-dim CPU tensor is read at full float32
-    precision. `device` selects which of the two the restatement follows.
+    r = float32(1 / s), x bf16 or fp16 (the reference's guard takes both,
+    :1021-1022). Dtype of `x * r`: a 0-dim scale does not promote, so the
+    product has x's dtype (rounded to it); a (1,)-shaped scale makes it
+    float32. On a GPU the 0-dim float32 operand is itself converted to the
+    common dtype (x's) before the multiply (TensorIterator casts
+    non-CPU-scalar inputs to the common dtype); a 0-dim CPU tensor is read at
+    full float32 precision. `device` selects which of the two the
+    restatement follows.
     """
     r = np.float32(1.0) / np.float32(input_scale)
     if scale_is_0dim:
-        rv = bf16_round(r) if device == "cuda" else f32(r)
-        y = T(bf16_round(x.v * rv), x.dt) if x.dt == "bf16" else T(x.v * rv, x.dt)
+        rv = round_to(r, x.dt) if device == "cuda" else f32(r)
+        with np.errstate(over="ignore", invalid="ignore"):
+            y = T(round_to(x.v * rv, x.dt), x.dt)
     else:
         y = T(x.v * r, "f32")
     y = clamp(y, -E4M3_MAX, E4M3_MAX)
@@ -168,12 +172,12 @@ def fp8_quantize_e4m3(x: T, input_scale: float, scale_is_0dim: bool, device: str
 
 
 def gelu_tanh(x: T) -> T:
-    """torch.nn.functional.gelu(x, approximate='tanh') for bf16 x, step by step
-    as torch's GPU kernel evaluates it in float32 (the reference's torch path
-    :165-169 on the GPU):
+    """torch.nn.functional.gelu(x, approximate='tanh') for bf16 or fp16 x, step
+    by step as torch's GPU kernel evaluates it in float32 (the reference's
+    torch path :165-169 on the GPU):
 
         x3 = (x * x) * x;  inner = beta * fma(kappa, x3, x);
-        g = (0.5 * x) * (1 + tanh(inner)), rounded once to bf16,
+        g = (0.5 * x) * (1 + tanh(inner)), rounded once to x's dtype,
 
     beta = float32(sqrt(2) * 2/sqrt(pi) * 0.5), kappa = float32(0.044715).
     The fused multiply-add is evaluated in extended precision (the product
@@ -190,7 +194,7 @@ def gelu_tanh(x: T) -> T:
         t = np.tanh(inner.astype(np.float64)).astype(np.float32)
         g = (np.float32(0.5) * v) * (np.float32(1.0) + t)
     g = g.astype(np.float32)
-    return T(bf16_round(g) if x.dt == "bf16" else g, x.dt)
+    return T(round_to(g, x.dt), x.dt)
 
 
 def fp8_per_head_quantize(x: np.ndarray, device: str = "cuda"):

@@ -1,6 +1,7 @@
 """Bit-level number formats used by the oracle (test infrastructure only).
 
-bfloat16 values are carried as float32 arrays whose low 16 bits are zero.
+bfloat16 values are carried as float32 arrays whose low 16 bits are zero;
+float16 values as float32 arrays holding exactly representable values.
 float8_e4m3fn values are carried as uint8 codes.
 """
 
@@ -28,6 +29,19 @@ def bf16_round(a) -> np.ndarray:
     out = ((bits + 0x7FFF + lsb) & 0xFFFF0000).astype(np.uint32).view(np.float32)
     out = np.where(np.isnan(a), np.float32(np.nan), out)
     return out.astype(np.float32)
+
+
+def f16_round(a) -> np.ndarray:
+    """float32 -> nearest IEEE binary16 (ties to even, subnormals kept,
+    overflow to infinity), returned as float32: numpy's float32 -> float16
+    conversion, the textbook correctly rounded one. NaN stays NaN."""
+    a = f32(a)
+    with np.errstate(over="ignore", invalid="ignore"):
+        return a.astype(np.float16).astype(np.float32)
+
+
+def f16_from_bits(bits) -> np.ndarray:
+    return np.asarray(bits, dtype=np.uint16).view(np.float16).astype(np.float32)
 
 
 def bf16_bits(a) -> np.ndarray:
@@ -95,18 +109,27 @@ def e4m3_decode(codes) -> np.ndarray:
     return (sign * val).astype(np.float32)
 
 
+def round_to(v, dt: str) -> np.ndarray:
+    """float32 values rounded to dtype `dt` ('bf16', 'f16' or 'f32')."""
+    if dt == "bf16":
+        return bf16_round(v)
+    if dt == "f16":
+        return f16_round(v)
+    return f32(v)
+
+
 class T:
     """A tensor value as torch would hold it: float32 data plus a dtype tag.
 
-    dtype is 'bf16' or 'f32'. `dim0` marks a 0-dim tensor, which does not take
-    part in dtype promotion against dimensioned tensors of the same category
-    (torch's rule: bf16_tensor * f32_0dim -> bf16).
+    dtype is 'bf16', 'f16' or 'f32'. `dim0` marks a 0-dim tensor, which does
+    not take part in dtype promotion against dimensioned tensors of the same
+    category (torch's rule: bf16_tensor * f32_0dim -> bf16).
     """
 
     __slots__ = ("v", "dt", "dim0")
 
     def __init__(self, v, dt: str, dim0: bool = False):
-        assert dt in ("bf16", "f32")
+        assert dt in ("bf16", "f16", "f32")
         self.v = f32(v)
         self.dt = dt
         self.dim0 = dim0
@@ -114,7 +137,7 @@ class T:
     def to(self, dt: str) -> "T":
         if dt == self.dt:
             return self
-        return T(bf16_round(self.v) if dt == "bf16" else self.v, dt, self.dim0)
+        return T(round_to(self.v, dt), dt, self.dim0)
 
 
 def _promote(a: T, b: T) -> str:
@@ -122,12 +145,13 @@ def _promote(a: T, b: T) -> str:
         return b.dt
     if b.dim0 and not a.dim0:
         return a.dt
-    return "f32" if "f32" in (a.dt, b.dt) else "bf16"
+    if a.dt == b.dt:
+        return a.dt
+    return "f32"  # f32 with anything, and bf16 with f16 (torch.promote_types)
 
 
 def _finish(v: np.ndarray, dt: str, dim0: bool) -> T:
-    v = f32(v)
-    return T(bf16_round(v) if dt == "bf16" else v, dt, dim0)
+    return T(round_to(f32(v), dt), dt, dim0)
 
 
 def add(a: T, b: T) -> T:

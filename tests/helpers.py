@@ -11,6 +11,8 @@ from oracle.numerics import T
 def dt_of(t: torch.Tensor) -> str:
     if t.dtype == torch.bfloat16:
         return "bf16"
+    if t.dtype == torch.float16:
+        return "f16"
     if t.dtype == torch.float32:
         return "f32"
     raise TypeError(t.dtype)

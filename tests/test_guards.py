@@ -124,23 +124,118 @@ def test_per_head_cpu_path():
 
 
 def test_scale_equality_memo_follows_the_tensors():
-    """The Q/K/V guards' torch.equal of the input (and weight) scales is
-    remembered per tuple of tensors and recomputed when a tensor changes in
-    place, is replaced, or another tensor takes its place."""
+    """With frozen scales declared, the Q/K/V guards' torch.equal of the input
+    (and weight) scales is remembered per tuple of tensors and recomputed when
+    a tensor changes in place, is replaced, or another tensor takes its place."""
     a = torch.tensor([0.5])
     b = torch.tensor([0.5])
     c = torch.tensor([0.5])
-    assert L._all_equal([a, b, c])
-    assert L._all_equal([a, b, c])  # remembered
-    c.mul_(2.0)  # in place: version counter moves
-    assert not L._all_equal([a, b, c])
-    c.copy_(torch.tensor([0.5]))
-    assert L._all_equal([a, b, c])
-    c.data = torch.tensor([0.25])  # new storage
-    assert not L._all_equal([a, b, c])
-    d = torch.tensor([0.5])
-    assert L._all_equal([a, b, d])
-    assert not L._all_equal([a, torch.tensor([0.5, 0.5]), d])  # shapes differ: torch.equal is False
-    for trial in range(3):  # fresh tensors each time (ids may be reused after collection)
-        x, y = torch.tensor([float(trial)]), torch.tensor([float(trial) + (trial % 2)])
-        assert L._all_equal([x, y]) == torch.equal(x, y)
+    with L.frozen_fp8_scales():
+        assert L._all_equal([a, b, c])
+        assert L._all_equal([a, b, c])  # remembered
+        c.mul_(2.0)  # in place: version counter moves
+        assert not L._all_equal([a, b, c])
+        c.copy_(torch.tensor([0.5]))
+        assert L._all_equal([a, b, c])
+        c.data = torch.tensor([0.25])  # new storage
+        assert not L._all_equal([a, b, c])
+        d = torch.tensor([0.5])
+        assert L._all_equal([a, b, d])
+        assert not L._all_equal([a, torch.tensor([0.5, 0.5]), d])  # shapes differ: torch.equal is False
+        for trial in range(3):  # fresh tensors each time (ids may be reused after collection)
+            x, y = torch.tensor([float(trial)]), torch.tensor([float(trial) + (trial % 2)])
+            assert L._all_equal([x, y]) == torch.equal(x, y)
+    assert not L._FROZEN_SCALES and not L._EQUAL_MEMO
+
+
+def test_scale_equality_default_compares_every_call():
+    """By default (as the reference) every call compares: a write through
+    `.data`, which the version counter does not see, is still noticed."""
+    a = torch.tensor([0.5])
+    b = torch.tensor([0.5])
+    assert L._all_equal([a, b])
+    b.data.copy_(torch.tensor([0.25]))
+    assert not L._all_equal([a, b])
+    b.data.copy_(torch.tensor([0.5]))
+    assert L._all_equal([a, b])
+
+
+@pytest.mark.parametrize("frozen", [False, True])
+def test_scale_equality_under_inference_mode(frozen):
+    """Scales created under torch.inference_mode (as the reference loads its
+    model) have no version counter; the comparison works on them either way."""
+    with torch.inference_mode():
+        a = torch.tensor([0.5])
+        b = torch.tensor([0.5])
+        c = torch.tensor([0.75])
+    prev = L.set_frozen_fp8_scales(frozen)
+    try:
+        with torch.inference_mode():
+            assert L._all_equal([a, b])
+            assert not L._all_equal([a, c])
+            assert L._all_equal([a, b])
+        assert L._all_equal([a, b]) and not L._all_equal([b, c])
+    finally:
+        L.set_frozen_fp8_scales(prev)
+
+
+def _cpu_attn(seed=5):
+    from opengenie_amd.block import random_video_block
+
+    return random_video_block(4096, 32, device="cpu", seed=seed).attn1
+
+
+@pytest.mark.parametrize("kind", ["qkv", "qk"])
+def test_grouped_projection_bookkeeping_on_cpu(kind, monkeypatch):
+    """fp8_qkv_from_grouped_mm / fp8_qk_from_grouped_mm keep the reference's
+    bookkeeping (:890-955, :2114-2178): a failing guard returns None and
+    counts its reason; an exception inside the projection returns None and
+    counts its type name; under OPENGENIE_AMD_STRICT it propagates."""
+    fn = L.fp8_qkv_from_grouped_mm if kind == "qkv" else L.fp8_qk_from_grouped_mm
+    reset = L.reset_video_qkv_grouped_mm_stats if kind == "qkv" else L.reset_video_qk_grouped_mm_stats
+    collect = L.collect_video_qkv_grouped_mm_stats if kind == "qkv" else L.collect_video_qk_grouped_mm_stats
+    attn = _cpu_attn()
+    x = randn((1, 4, 4096), 1)
+    reset(checks=1)
+    assert fn(attn, x) is None  # CPU input: the guard's "input" reason
+    assert fn(attn, x[:, :, :2048]) is None
+    st = collect()
+    assert st == {"calls": 0, "fallbacks": 2, "fallback_reasons": {"input": 2}, "checks": []}
+
+    def boom(*a, **k):
+        raise RuntimeError("forced from the host")
+
+    monkeypatch.setattr(L, "_grouped_guard_reason", lambda *a: None)
+    monkeypatch.setattr(L, "_fp8_grouped_linear", boom)
+    assert fn(attn, x) is None
+    assert collect()["fallback_reasons"] == {"input": 2, "RuntimeError": 1}
+    monkeypatch.setenv("OPENGENIE_AMD_STRICT", "1")
+    with pytest.raises(RuntimeError):
+        fn(attn, x)
+    monkeypatch.delenv("OPENGENIE_AMD_STRICT")
+    reset()
+    assert collect() == {"calls": 0, "fallbacks": 0, "fallback_reasons": {}, "checks": []}
+
+
+def test_grouped_guard_reasons_follow_the_reference_order():
+    """The reasons of :1187-1233 in the reference's order, for the conditions
+    that do not need a GPU tensor to reach (the device check comes first)."""
+    attn = _cpu_attn(6)
+    x = randn((1, 4, 4096), 2)
+    names = ("to_q", "to_k", "to_v")
+    assert L._grouped_guard_reason(attn, x, names) == "input"
+    assert L._grouped_guard_reason(attn, x.float(), names) == "input"
+
+
+def test_misaligned_views_fall_back_before_the_library():
+    """A contiguous view at an odd storage offset passes the reference's
+    guards; the guards here also check the C ABI's 16-byte precondition, so
+    such a view takes the torch path (on the GPU the same guard sends it
+    there instead of to an argument error)."""
+    buf = torch.zeros(1 + 2 * 4096, dtype=torch.bfloat16)
+    x = buf[1:].view(1, 2, 4096)
+    assert x.is_contiguous() and x.data_ptr() % 16 == 2
+    assert not L._aligned(x)
+    assert L._vec_ok(buf[1:4097], torch.bfloat16) is False
+    assert L._vec_ok(buf[1:4097], torch.float32) is True  # a converted copy is aligned
+    assert L._vec_ok(buf[1:8193:2], torch.bfloat16) is True  # .contiguous() copies it

@@ -14,7 +14,7 @@ import torch
 
 import oracle.torch_ref as tr
 from oracle import ltx_ops as O
-from oracle.numerics import T, bf16_from_bits, bf16_round, e4m3_decode, e4m3_encode
+from oracle.numerics import T, bf16_from_bits, bf16_round, e4m3_decode, e4m3_encode, f16_from_bits, f16_round
 from tests.helpers import assert_same_bits, bf16_ulp_distance, nan_canon, np32, randn, to_T
 
 
@@ -29,6 +29,27 @@ def test_bf16_round_matches_torch_on_random_and_edge_bits():
     ours = bf16_round(a)
     ref = torch.from_numpy(a.copy()).to(torch.bfloat16).float().numpy()
     assert_same_bits(ours, ref, "bf16_round")
+
+
+def test_f16_round_matches_torch_on_random_and_edge_bits():
+    rng = np.random.default_rng(2)
+    bits = rng.integers(0, 2 ** 32, size=1 << 21, dtype=np.uint64).astype(np.uint32)
+    # around the largest finite half (65504), its overflow midpoint (65520),
+    # the subnormal range (2^-24 quantum) and ties at both
+    edges = np.array([0x477FE000, 0x477FEFFF, 0x477FF000, 0x477FF001, 0x33800000, 0x33000000, 0x33000001,
+                      0x33C00000, 0x38800000, 0x387FC000, 0x387FE000, 0x3F801000, 0x3F803000, 0x7F800000,
+                      0xFF800000, 0x7FC00000, 0x00000001, 0x80000001], dtype=np.uint32)
+    a = np.concatenate([bits, edges]).view(np.float32)
+    ours = f16_round(a)
+    ref = torch.from_numpy(a.copy()).to(torch.float16).float().numpy()
+    assert_same_bits(ours, ref, "f16_round")
+
+
+def test_e4m3_encode_matches_torch_exhaustively_over_f16():
+    x = f16_from_bits(np.arange(1 << 16, dtype=np.uint16))
+    ours = e4m3_encode(x)
+    ref = torch.from_numpy(x.copy()).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(nan_canon(ours), nan_canon(ref))
 
 
 def test_e4m3_encode_matches_torch_exhaustively_over_bf16():
@@ -195,6 +216,24 @@ def test_fp8_quantize_matches_torch_cpu_exhaustively(scale, zero_dim):
     assert np.array_equal(nan_canon(ours), nan_canon(ref))
 
 
+@pytest.mark.parametrize("scale", [0.05, 0.37, 1.0, 3.3e-3, 2.0e-5])
+@pytest.mark.parametrize("zero_dim", [True, False])
+def test_fp8_quantize_f16_matches_torch_cpu_exhaustively(scale, zero_dim):
+    """Every fp16 bit pattern (the reference's guard takes fp16 x too,
+    :1021-1022): the product has x's dtype for a 0-dim scale, float32 for a
+    (1,) one. 2e-5 makes 1/s overflow fp16's range (CPU semantics keep the
+    float32 reciprocal)."""
+    x = f16_from_bits(np.arange(1 << 16, dtype=np.uint16))
+    xt = torch.from_numpy(x.copy()).to(torch.float16)
+    s = torch.tensor(scale, dtype=torch.float32)
+    if not zero_dim:
+        s = s.reshape(1)
+    ref = tr.fp8_quantize_e4m3(xt, s).view(torch.uint8).numpy()
+    with np.errstate(over="ignore", invalid="ignore"):
+        ours = O.fp8_quantize_e4m3(T(x, "f16"), float(s.reshape(())), zero_dim, device="cpu")
+    assert np.array_equal(nan_canon(ours), nan_canon(ref))
+
+
 def test_fp8_quantize_gpu_semantics_differs_only_by_rounded_reciprocal():
     # With a reciprocal that is already a bf16 value the CPU and GPU forms agree.
     x = bf16_from_bits(np.arange(1 << 16, dtype=np.uint16))
@@ -226,6 +265,22 @@ def test_gelu_tanh_matches_torch_cpu_on_every_bf16():
     eq = (g.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(g) & np.isnan(ref))
     bad = np.flatnonzero(~eq)
     assert bad.size <= 4, bad.size
+    assert np.all((x[bad] > -5.2) & (x[bad] < -5.0)) and np.all(ref[bad] == 0) and np.all(np.abs(g[bad]) < 2e-7)
+
+
+def test_gelu_tanh_matches_torch_cpu_on_every_f16():
+    """All 65536 fp16 inputs against torch's CPU gelu(approximate='tanh') in
+    fp16 (float32 steps, one rounding to fp16). As for bf16, the only
+    differences are where torch's vectorised CPU tanh returns exactly -1 for
+    an argument whose correctly rounded tanh is -(1 - 2^-24): torch's GELU is
+    -0 there and the oracle's a tiny negative value (x in [-5.16, -5.06]).
+    The GPU test pins the oracle against torch's GPU kernel on every input."""
+    x = f16_from_bits(np.arange(1 << 16, dtype=np.uint16))
+    g = O.gelu_tanh(T(x, "f16")).v
+    ref = torch.nn.functional.gelu(torch.from_numpy(x.copy()).to(torch.float16), approximate="tanh").float().numpy()
+    eq = (g.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(g) & np.isnan(ref))
+    bad = np.flatnonzero(~eq)
+    assert bad.size <= 32, bad.size
     assert np.all((x[bad] > -5.2) & (x[bad] < -5.0)) and np.all(ref[bad] == 0) and np.all(np.abs(g[bad]) < 2e-7)
 
 
