@@ -857,10 +857,14 @@ def fused_video_qk_bias_rmsnorm_rope(q, k, q_bias, k_bias, q_weight, k_weight, e
 def qk_rmsnorm(x: torch.Tensor, weight: torch.Tensor | None, eps: float) -> torch.Tensor:
     """The attention module's q/k RMSNorm where no RoPE follows (the text
     cross-attention, pe = None: `attn_module.q_norm(q)` / `k_norm(k)`,
-    :1866-1867): torch.nn.functional.rms_norm over the last dimension, one
-    rounding of x * inv * w. Runs the RMSNorm pass of the preattention kernel
-    without its rotation for bf16 x with 2048 or 4096 columns; otherwise the
-    torch expression."""
+    :1866-1867): torch.nn.functional.rms_norm over the last dimension. Runs
+    the RMSNorm pass of the preattention kernel without its rotation for bf16
+    x with 2048 or 4096 columns, otherwise the torch expression. The kernel
+    takes the mean square from the exact sum of squares and rounds x * inv * w
+    once, which torch's CPU rms_norm matches; torch's GPU rms_norm sums the
+    squares in another float32 order and differs from it by at most one bf16
+    step in rare elements, so this is not bit-identical to the GPU torch call
+    it replaces (the fusion is opt-in: the block harness's `fuse_norm`)."""
     cols = x.shape[-1] if x.dim() else 0
     w = None if weight is None else weight.contiguous()
     ok = (x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous() and cols in (2048, 4096)

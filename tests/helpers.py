@@ -58,6 +58,14 @@ def bf16_ulp_distance(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     return np.abs(key(a) - key(b))
 
 
+def bf16_step(a) -> np.ndarray:
+    """Spacing of the bf16 values at |a|, elementwise: 2^(e - 7) for a normal
+    a = m * 2^e (1 <= m < 2), the subnormal spacing 2^-133 below 2^-126."""
+    a = np.abs(np.asarray(a, dtype=np.float64))
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -126)))
+    return np.exp2(e - 7)
+
+
 def nan_canon(codes: np.ndarray) -> np.ndarray:
     """e4m3fn codes with both NaN codes (0x7F, 0xFF) mapped to 0x7F.
 

@@ -21,7 +21,10 @@ Shapes:
   FP8 quantizer      (9216, 4096) with 0.1 % outliers x50, amax/448 scale
   FP8 linear         9216 x 4096 -> 16384 (nine whole rounds), 16384 -> 4096
                      and 4096 -> 4096 (split-K tails), grouped Q/K/V 4096 ->
-                     3 x 4096: sampled rows against the oracle, the bias
+                     3 x 4096: every output against a full-size checker
+                     (decoded e4m3 codes, a float32 device matmul, the
+                     reference's two roundings), sampled rows against the
+                     oracle (which also pins the checker there), the bias
                      epilogue on every element
 """
 
@@ -247,6 +250,51 @@ def test_fp8_quantize_config_shape(zero_dim):
 
 
 # ------------------------------------------------------------ FP8 linear at 9216 tokens
+def _device_fp8_linear(a8: torch.Tensor, w8: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor,
+                       bias: torch.Tensor | None) -> torch.Tensor:
+    """Full-size checker of the FP8 linear, fixed by the mathematics: e4m3
+    codes decode exactly to float32 and every product of two e4m3 values is
+    exact in float32, so a float32 device matmul (TF32 off) computes the
+    reference's accumulator up to float32 summation rounding; then the
+    reference's two roundings, R(acc * sa * sb) and R(out + R(bias))
+    (triton_ltx_ops.py:1691-1709)."""
+    prev = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        acc = a8.float() @ w8.float().t()
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = prev
+    out = (acc * (sa.float().reshape(()) * sb.float().reshape(()))).to(torch.bfloat16)
+    del acc
+    if bias is not None:
+        out = (out.float() + bias.to(torch.bfloat16).float()).to(torch.bfloat16)
+    return out
+
+
+def _bf16_steps_t(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """Distance in bf16 steps between two bf16 tensors (monotone integer map
+    of the bit patterns), on the device."""
+    def key(x):
+        u = x.contiguous().view(torch.int16).to(torch.int32) & 0xFFFF
+        return torch.where(u >= 0x8000, 0x8000 - u, u)
+    return (key(a) - key(b)).abs()
+
+
+def _linear_full_check(got: torch.Tensor, ref: torch.Tensor, what: str) -> None:
+    """The GEMM bar of _linear_rows_check on every output, on the device."""
+    g32, r32 = got.float(), ref.float()
+    close = torch.isclose(g32, r32, rtol=1e-2, atol=1e-3 * float(r32.abs().max()))
+    far = int((~close).sum())
+    steps = _bf16_steps_t(got, ref)
+    over1 = float((steps > 1).float().mean())
+    worst_far = int(steps[~close].max()) if far else 0
+    print(f"{what}: {got.numel()} outputs, {far} outside rtol 1e-2 (worst {worst_far} steps), "
+          f"{over1:.2e} more than one step away")
+    assert far / got.numel() < 1e-5, (what, far)
+    assert worst_far <= 2, (what, worst_far)
+    assert over1 < 1e-2, (what, over1)
+
+
 def _linear_rows_check(got_rows: np.ndarray, ref_rows: np.ndarray) -> None:
     """The FP8 linear's bar against the float64-accumulated oracle (as the
     small-shape tests): rtol 1e-2 with an outlier allowance of 1e-5 at most
@@ -268,9 +316,11 @@ def test_fp8_linear_config_shapes(n, k):
     16384 -> 4096 and 4096 -> 4096 are two whole rounds, then the split-K
     tail (4 and 2 K-chunks) and its reduce. Config 2's data: x ~N(0,1) with
     0.1 % of the entries x50, per-tensor amax/448 scales, W from N(0,0.02),
-    bf16 bias ~N(0,0.01). Every 127th row (and the last) against the oracle
-    at the GEMM bar; every element of the biased output equal to
-    R(out_nobias + R(bias)) from the unbiased call on the same schedule."""
+    bf16 bias ~N(0,0.01). Every output against the full-size device checker
+    at the GEMM bar; every 127th row (and the last) against the oracle, and
+    the checker against the oracle on those rows; every element of the
+    biased output equal to R(out_nobias + R(bias)) from the unbiased call on
+    the same schedule."""
     from opengenie_amd import _lib
     from opengenie_amd.ltx_ops import fp8_scaled_mm
 
@@ -295,18 +345,23 @@ def test_fp8_linear_config_shapes(n, k):
     _ran("fp8_scaled_mm")
     want = (out0.float() + gb.float()).to(torch.bfloat16)  # R(out_nobias + R(bias)), bias already bf16
     assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    del out0, want
+    full = _device_fp8_linear(ga, gw, gsa, gsb, gb)
+    _linear_full_check(out, full, f"FP8 linear 9216x{k}->{n}")
     rows = np.unique(np.concatenate([np.arange(0, m, 127), [m - 1]]))
     a_codes = a.view(torch.uint8).numpy()
     ref = O.fp8_linear(a_codes[rows], w.view(torch.uint8).numpy(), float(sa), float(sb), to_T(bias))
     got = out_np(out)[rows]
     _linear_rows_check(got, ref)
+    _linear_rows_check(out_np(full)[rows], ref)  # the checker itself, against the oracle
 
 
 def test_fp8_grouped_qkv_config_shape():
     """The grouped Q/K/V projection at 9216 tokens (one launch over the 1728
     tiles of the three 4096 -> 4096 linears, 6.75 rounds of the CUs, no split)
-    with each linear's own weight scale and bias: every 127th row of q, k and
-    v against the oracle at the GEMM bar."""
+    with each linear's own weight scale and bias: every output of q, k and v
+    against the full-size device checker, every 127th row against the oracle
+    at the GEMM bar."""
     from opengenie_amd import ltx_ops as L
     from opengenie_amd.block import random_video_block
 
@@ -327,3 +382,6 @@ def test_fp8_grouped_qkv_config_shape():
                            float(lin.weight_scale.float().cpu()), to_T(lin.bias.cpu()))
         got = out_np(got_t).reshape(9216, -1)[rows]
         _linear_rows_check(got, ref)
+        xq_d = torch.from_numpy(xq).to(DEV).view(torch.float8_e4m3fn)
+        full = _device_fp8_linear(xq_d, lin.weight, lin.input_scale, lin.weight_scale, lin.bias)
+        _linear_full_check(got_t.reshape(9216, -1), full, "grouped Q/K/V 9216x4096->4096")

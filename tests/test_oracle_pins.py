@@ -15,7 +15,7 @@ import torch
 import oracle.torch_ref as tr
 from oracle import ltx_ops as O
 from oracle.numerics import T, bf16_from_bits, bf16_round, e4m3_decode, e4m3_encode, f16_from_bits, f16_round
-from tests.helpers import assert_same_bits, bf16_ulp_distance, nan_canon, np32, randn, to_T
+from tests.helpers import assert_same_bits, bf16_step, bf16_ulp_distance, nan_canon, np32, randn, to_T
 
 
 # ----------------------------------------------------------------- numerics
@@ -137,6 +137,21 @@ def test_adazero_from_ada_matches_torch(table_dtype, ts_dtype, broadcast):
     d = bf16_ulp_distance(bf16_round(ours.v), bf16_round(np32(ref)))
     # Only the float32 sum of squares can differ from torch's; rare and small.
     assert (d > 0).mean() < 2e-3
+    shift, scale = O.ada_values_from_table(to_T(table), to_T(ts), 1, 9, 2048, 3, 4)
+    _adazero_differs_only_in_the_norm(x, scale, shift, ref)
+
+
+def _adazero_differs_only_in_the_norm(x, scale: T, shift: T, ref: torch.Tensor) -> None:
+    """Every difference between the oracle and torch comes from the RMSNorm
+    step: the oracle's normalized row is within one bf16 step of torch's
+    rms_norm, and the oracle's remaining steps, R(R(n * R(1 + scale)) +
+    shift), applied to torch's own normalized row give torch's output bit for
+    bit (so no element can be off by more than that one step carried through
+    the two roundings)."""
+    n_t = torch.nn.functional.rms_norm(x, (x.shape[-1],), eps=1e-6)
+    assert bf16_ulp_distance(O.rms_norm(to_T(x), 1e-6).v, np32(n_t)).max() <= 1
+    tail = O.add(O.mul(to_T(n_t), O.add_scalar(scale, 1.0)), shift)
+    assert_same_bits(bf16_round(tail.v) if tail.dt == "bf16" else tail.v, np32(ref), "AdaZero after the norm")
 
 
 def test_adazero_with_strided_scale_shift_matches_torch():
@@ -147,6 +162,7 @@ def test_adazero_with_strided_scale_shift_matches_torch():
     ref = tr.adazero(x, 1e-6, scale, shift)
     ours = O.adazero(to_T(x), 1e-6, to_T(scale), to_T(shift))
     assert (bf16_ulp_distance(ours.v, np32(ref)) > 0).mean() < 2e-3
+    _adazero_differs_only_in_the_norm(x, to_T(scale), to_T(shift), ref)
 
 
 @pytest.mark.parametrize("ts_dtype", [torch.bfloat16, torch.float32])
@@ -338,9 +354,16 @@ def test_video_qk_rmsnorm_rope_matches_torch(cos_dtype):
     q, k, qw, kw, cos, sin = _rope_inputs(8, cos_dtype=cos_dtype)
     rq, rk = tr.video_qk_rmsnorm_rope(q, k, qw, kw, 1e-6, cos, sin)
     oq, ok = O.video_qk_rmsnorm_rope(to_T(q), to_T(k), to_T(qw), to_T(kw), 1e-6, to_T(cos), to_T(sin))
-    for o, r in ((oq, rq), (ok, rk)):
+    for x, w, o, r in ((q, qw, oq, rq), (k, kw, ok, rk)):
         d = bf16_ulp_distance(bf16_round(o.v), bf16_round(np32(r)))
         assert (d > 0).mean() < 2e-3
+        # every difference comes from the RMSNorm step: the normalized rows
+        # are within one bf16 step, and the oracle's split RoPE of torch's own
+        # normalized row is torch's output bit for bit
+        n_t = torch.nn.functional.rms_norm(x, (4096,), weight=w, eps=1e-6)
+        assert bf16_ulp_distance(O.rms_norm(to_T(x), 1e-6, to_T(w)).v, np32(n_t)).max() <= 1
+        rot = O.split_rope(to_T(n_t), to_T(cos), to_T(sin))
+        assert_same_bits(rot.v, np32(r), "split RoPE after the norm")
 
 
 def test_split_rope_invariants():
