@@ -93,11 +93,11 @@ def make_fp8_linear_inputs(seed: int, device: str, m: int = M, k: int = K, n: in
     return x, s_in, w, s_w, bias
 
 
-def _graph_time_us(fn, reps: int = 20, inner: int = 25, rounds: int = 3, settle_s: float = 0.3) -> float:
+def _graph_time_us(fn, reps: int = 20, inner: int = 25, rounds: int = 5, settle_s: float = 0.3) -> float:
     """Mean per-call GPU time of fn: `inner` calls captured in one HIP graph,
     replayed for `settle_s` seconds first (the clock after a change of
     workload takes that long to settle), then `reps` times between two
-    events on the capture stream; the best of `rounds` such measurements."""
+    events on the capture stream; the median of `rounds` such measurements."""
     import time
 
     import torch
@@ -120,7 +120,7 @@ def _graph_time_us(fn, reps: int = 20, inner: int = 25, rounds: int = 3, settle_
         graph.replay()
         torch.cuda.synchronize()
     st = torch.cuda.current_stream()
-    best = float("inf")
+    per = []
     for _ in range(rounds):
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
@@ -129,9 +129,9 @@ def _graph_time_us(fn, reps: int = 20, inner: int = 25, rounds: int = 3, settle_
             graph.replay()
         e1.record(st)
         e1.synchronize()
-        best = min(best, e0.elapsed_time(e1) * 1000.0 / (reps * inner))
+        per.append(e0.elapsed_time(e1) * 1000.0 / (reps * inner))
     del graph
-    return best
+    return statistics.median(per)
 
 
 def _settled_time_us(fn, reps: int = 10, settle_s: float = 0.5, batches: int = 5) -> float:
@@ -186,8 +186,8 @@ def _cold_graph_time_us(fn, flush: CacheFlush) -> float:
     """Per-call GPU time of fn with its inputs out of the caches: a HIP graph
     of (cache flush, fn) pairs minus a graph of the flushes alone, so every
     call reads its inputs from HBM."""
-    both = _graph_time_us(lambda: (flush(), fn()), reps=10, inner=10, rounds=2)
-    alone = _graph_time_us(flush, reps=10, inner=10, rounds=2)
+    both = _graph_time_us(lambda: (flush(), fn()), reps=10, inner=10, rounds=3)
+    alone = _graph_time_us(flush, reps=10, inner=10, rounds=3)
     return both - alone
 
 
@@ -275,15 +275,43 @@ def fused_op_rows(seed: int) -> dict:
 ATT_N, ATT_H, ATT_D = 9216, 32, 128
 
 
+def _block_op_work(name: str, ctx_tokens: int) -> tuple[str, float] | None:
+    """Algorithmic work of one op of the block slice at 9216 tokens (the
+    timestep embedding is one row shared by all tokens, read once): ("bytes",
+    B) for the HBM-bound ops, ("flop", F) for the FP8 GEMMs and attention;
+    None for steps that combine a quantizer and a GEMM."""
+    row = M * 4096 * 2  # one (9216, 4096) bf16 tensor
+    tab = {
+        "msa.adazero": ("bytes", 2 * row), "ff.adazero": ("bytes", 2 * row), "ca.adazero": ("bytes", 2 * row),
+        "msa.adazero_fp8": ("bytes", 1.5 * row), "ff.adazero_fp8": ("bytes", 1.5 * row),
+        "ca.adazero_fp8": ("bytes", 1.5 * row),
+        "msa.qk_rmsnorm_rope": ("bytes", 4 * row + 2 * 32 * M * 64 * 2),
+        "msa.residual_gate_bias": ("bytes", 3 * row), "ca.residual_gate": ("bytes", 3 * row),
+        "ff.residual_gate": ("bytes", 3 * row),
+        "ca.rms_norm": ("bytes", 2 * row), "ca.adaln_affine": ("bytes", 2 * row),
+        "ca.q_rmsnorm": ("bytes", 2 * row),
+        "ff.gelu_quant": ("bytes", M * 16384 * 3), "ff.gelu": ("bytes", M * 16384 * 4),
+        "msa.qkv_grouped": ("flop", 2.0 * M * 4096 * 3 * 4096), "ca.q_linear": ("flop", 2.0 * M * 4096 * 4096),
+        "ff.up_linear": ("flop", 2.0 * M * 4096 * 16384), "ff.down_linear": ("flop", 2.0 * M * 16384 * 4096),
+        "msa.attention": ("flop", 4.0 * M * M * 4096), "ca.attention": ("flop", 4.0 * M * ctx_tokens * 4096),
+    }
+    return tab.get(name)
+
+
 def block_rows(seed: int, reps: int = 5, ctx_tokens: int = 256) -> dict:
     """One video transformer-block slice at 9216 tokens (self-attention, text
     cross-attention over ctx_tokens text tokens, feed-forward; the production
     op order of opengenie_amd.block), random-init synthetic parameters of the
     LTX-2.3 shapes; HIP events on the current stream around the whole slice
-    and between its three branches."""
+    and between its three branches. Then, per mode, every op of the slice
+    timed between HIP events recorded after each launch
+    (`block.launch_marks`), with achieved GB/s (row ops) or TFLOP/s (GEMMs,
+    attention) where the op has its own algorithmic work. The FP8 scales are
+    declared fixed (`frozen_fp8_scales`), as a loaded model's are."""
     import torch
 
     from opengenie_amd import block as B
+    from opengenie_amd import ltx_ops as L
 
     blk = B.random_video_block(4096, 32, seed=seed + 40)
     g = _gen(seed + 41, "cuda")
@@ -295,31 +323,67 @@ def block_rows(seed: int, reps: int = 5, ctx_tokens: int = 256) -> dict:
     sin = torch.randn((1, 32, M, 64), generator=g, device="cuda").clamp(-1, 1).to(torch.bfloat16)
     st = torch.cuda.current_stream()
     rows = {}
-    for key in ("production_flags", "mi355x_fusions", "mi355x_fusions_ada_quant"):
+    modes = ("production_flags", "mi355x_fusions", "mi355x_fusions_ada_quant")
+
+    def run(key):
         # production flags; then the MI355X-side fusions (grouped Q/K/V,
         # rms_norm + AdaLN as one AdaZero, GELU in the down-projection's
         # quantizer); then also each AdaZero that feeds an FP8 linear writing
         # that linear's e4m3 input
         fuse = key != "production_flags"
         aq = key == "mi355x_fusions_ada_quant"
-        parts = {"self_attention": [], "text_cross_attention": [], "feed_forward": [], "block": []}
-        for rep in range(reps + 2):
-            ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
-            ev[0].record(st)
-            x1 = B.video_self_attention(blk, vx, ts, cos, sin, qkv_grouped=fuse, fuse_ada_quant=aq)
-            ev[1].record(st)
-            x2 = B.video_text_cross_attention(blk, x1, ctx, ts, pts, fuse_norm=fuse, fuse_ada_quant=aq)
-            ev[2].record(st)
-            B.video_feed_forward(blk, x2, ts, fuse_gelu_quant=fuse, fuse_ada_quant=aq)
-            ev[3].record(st)
-            ev[3].synchronize()
-            if rep < 2:
-                continue
-            for i, k in enumerate(("self_attention", "text_cross_attention", "feed_forward")):
-                parts[k].append(ev[i].elapsed_time(ev[i + 1]) * 1000.0)
-            parts["block"].append(ev[0].elapsed_time(ev[3]) * 1000.0)
-        rows[key] = {k: round(statistics.median(v), 1) for k, v in parts.items()}
-    rows["shape"] = f"vx (1,{M},4096), text context (1,{ctx_tokens},4096), 32 heads, FFN 16384; us per call"
+        x1 = B.video_self_attention(blk, vx, ts, cos, sin, qkv_grouped=fuse, fuse_ada_quant=aq)
+        x2 = B.video_text_cross_attention(blk, x1, ctx, ts, pts, fuse_norm=fuse, fuse_ada_quant=aq)
+        return B.video_feed_forward(blk, x2, ts, fuse_gelu_quant=fuse, fuse_ada_quant=aq)
+
+    with L.frozen_fp8_scales():
+        for key in modes:
+            parts = {"self_attention": [], "text_cross_attention": [], "feed_forward": [], "block": []}
+            for rep in range(reps + 2):
+                ev = {}
+
+                def mark(name):
+                    e = torch.cuda.Event(enable_timing=True)
+                    e.record(st)
+                    ev[name] = e
+
+                mark("start")
+                with B.launch_marks(mark):
+                    run(key)
+                ev[list(ev)[-1]].synchronize()
+                if rep < 2:
+                    continue
+                names = list(ev)
+                bounds = {"self_attention": ("start", [n for n in names if n.startswith("msa.")][-1]),
+                          "text_cross_attention": ([n for n in names if n.startswith("msa.")][-1],
+                                                   [n for n in names if n.startswith("ca.")][-1]),
+                          "feed_forward": ([n for n in names if n.startswith("ca.")][-1], names[-1]),
+                          "block": ("start", names[-1])}
+                for k, (a, b) in bounds.items():
+                    parts[k].append(ev[a].elapsed_time(ev[b]) * 1000.0)
+                for prev, name in zip(names, names[1:]):
+                    parts.setdefault("op:" + name, []).append(ev[prev].elapsed_time(ev[name]) * 1000.0)
+            row = {k: round(statistics.median(v), 1) for k, v in parts.items() if not k.startswith("op:")}
+            kern = {}
+            for k, v in parts.items():
+                if not k.startswith("op:"):
+                    continue
+                name, us = k[3:], statistics.median(v)
+                ent = {"us": round(us, 1)}
+                work = _block_op_work(name, ctx_tokens)
+                if work and work[0] == "bytes":
+                    gbs = work[1] / (us * 1e-6) / 1e9
+                    ent.update({"GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)})
+                elif work:
+                    tf = work[1] / (us * 1e-6) / 1e12
+                    peak = BF16_PEAK_TFLOPS if name.endswith("attention") else FP8_PEAK_TFLOPS
+                    ent.update({"TFLOP/s": round(tf, 1), "frac_peak": round(tf / peak, 3)})
+                kern[name] = ent
+            row["ops"] = kern
+            rows[key] = row
+    rows["shape"] = (f"vx (1,{M},4096), text context (1,{ctx_tokens},4096), 32 heads, FFN 16384; us per call; "
+                     f"ops: time between HIP events recorded after consecutive launches (median of {reps}), "
+                     f"row-op bytes with the shared timestep row read once")
     return rows
 
 
@@ -430,18 +494,24 @@ COPY_ELEMS = 64 * 1024 * 1024  # bf16 elements per calibration copy: 128 MiB rea
 
 def copy_reference(graph: bool = True, reps: int = 10) -> dict:
     """Achievable streaming bandwidth on this GPU: torch's device copy of a
-    bf16 tensor (read + write), for calibration next to the fused ops. With
-    graph=False the copies are plain eager launches (one kernel each), the
-    known-size workload that scales the FETCH_SIZE / WRITE_SIZE counters."""
+    bf16 tensor (read + write), for calibration next to the fused ops, warm
+    and, at the sizes of the ops timed cold, cold (the same flush-and-subtract
+    method as `us_cold`: what a plain copy of those bytes reaches under it).
+    With graph=False the copies are plain eager launches (one kernel each),
+    the known-size workload that scales the FETCH_SIZE / WRITE_SIZE
+    counters."""
     import torch
 
     out = {}
-    sizes = (37_748_736 // 2, 461_373_440 // 4) if graph else (COPY_ELEMS,)
+    # bytes moved: AdaZero (1,2304,4096) 37.7 MB, the quantizer 113 MB, Q/K
+    # RMSNorm+RoPE 377 MB, the continuation ops 461 MB
+    sizes = (37_748_736 // 4, 113_246_208 // 4, 377_487_360 // 4, 461_373_440 // 4) if graph else (COPY_ELEMS,)
+    flush = CacheFlush("cuda") if graph else None
     for n in sizes:
         a = torch.empty(n, device="cuda", dtype=torch.bfloat16).normal_()
         b = torch.empty_like(a)
         if graph:
-            small = n * 4 < 200_000_000  # 100 calls per graph for the small copy, as for the small ops
+            small = n * 4 < 200_000_000  # 100 calls per graph for the small copies, as for the small ops
             us = _graph_time_us(lambda: b.copy_(a), reps=5 if small else 10, inner=100 if small else 10)
         else:
             st = torch.cuda.current_stream()
@@ -454,8 +524,12 @@ def copy_reference(graph: bool = True, reps: int = 10) -> dict:
             e1.synchronize()
             us = e0.elapsed_time(e1) * 1000.0 / reps
         gbs = 2 * n * 2 / (us * 1e-6) / 1e9
-        out[f"copy_{2 * n * 2 // 1_000_000}MB"] = {"bytes": 2 * n * 2, "us": round(us, 3), "GB/s": round(gbs, 1),
-                                                    "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        row = {"bytes": 2 * n * 2, "us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        if graph and n * 4 < 400_000_000:
+            uc = _cold_graph_time_us(lambda: b.copy_(a), flush)
+            row.update({"us_cold": round(uc, 3), "frac_cold": round(2 * n * 2 / (uc * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+        out[f"copy_{2 * n * 2 // 1_000_000}MB"] = row
+        del a, b
     return out
 
 
@@ -686,6 +760,10 @@ def main() -> None:
     assert rc == 0
     gemm_us = e0.elapsed_time(e1) * 1000.0 / reps
     achieved = flops / (gemm_us * 1e-6) / 1e12
+    # torch._scaled_mm (hipBLASLt) + the bias add on the same inputs, beside it
+    wt = w.t()
+    torch_us = _settled_time_us(lambda: torch._scaled_mm(q, wt, scale_a=s_in, scale_b=s_w, out_dtype=torch.bfloat16,
+                                                         use_fast_accum=True) + bias, reps=10)
 
     fused = {} if args.no_fused else fused_op_rows(args.seed)
     if fused:
@@ -718,7 +796,8 @@ def main() -> None:
                      "traffic_split": {"fetch": GEMM_TRAFFIC_FETCH, "write": GEMM_TRAFFIC_WRITE,
                                        "algorithmic": GEMM_ALGORITHMIC_BYTES, "unit": "bytes/launch",
                                        "source": GEMM_TRAFFIC_SOURCE},
-                     "us_per_launch": round(gemm_us, 2)},
+                     "us_per_launch": round(gemm_us, 2),
+                     "torch_scaled_mm_plus_bias_us": round(torch_us, 2)},
         "fused_ops": fused,
         "attention": attention,
         "fp8_linears": linears,

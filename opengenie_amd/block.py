@@ -131,6 +131,33 @@ class Stages:
         return self.t[k]
 
 
+_MARK = None
+
+
+class launch_marks:
+    """`with launch_marks(fn): ...` calls fn(name) after each op of a block
+    slice is enqueued (names as `branch.op`), e.g. to record a HIP event on
+    the stream after every launch and time each op of the slice."""
+
+    def __init__(self, fn):
+        self.fn = fn
+
+    def __enter__(self):
+        global _MARK
+        self._prev, _MARK = _MARK, self.fn
+        return self
+
+    def __exit__(self, *exc):
+        global _MARK
+        _MARK = self._prev
+        return False
+
+
+def _mark(name: str) -> None:
+    if _MARK is not None:
+        _MARK(name)
+
+
 def _rms_norm(x: torch.Tensor, eps: float, weight: torch.Tensor | None = None) -> torch.Tensor:
     """ltx_core.utils.rms_norm / the attention module's q/k RMSNorm: torch's
     rms_norm over the last dimension."""
@@ -154,28 +181,41 @@ def video_self_attention(block: VideoBlock, vx: torch.Tensor, timesteps: torch.T
             and L._video_qkv_linears_ok(a, vx, ("to_q", "to_k", "to_v"), grouped=True)):
         norm_q8 = L.fused_adazero_from_ada_fp8(vx, block.eps, block.table, timesteps, a.to_q.input_scale,
                                                shift_index=0, scale_index=1)
+        _mark("msa.adazero_fp8")
         qkv = L.fp8_qkv_from_quantized_e4m3(a, norm_q8, out_dtype=vx.dtype)
+        _mark("msa.qkv_grouped")
     if qkv is None:
         norm_q8 = None
         norm_vx = L.fused_adazero_from_ada(vx, block.eps, block.table, timesteps, shift_index=0, scale_index=1)
+        _mark("msa.adazero")
         qkv = L.fp8_qkv_from_grouped_mm(a, norm_vx) if qkv_grouped else None
+        if qkv is not None:
+            _mark("msa.quant_qkv_grouped")
     if qkv is not None:
         q, k, v = qkv
     else:
         q = L.fp8_linear_forward(a.to_q, norm_vx)
+        _mark("msa.quant_q_linear")
         k = L.fp8_linear_forward(a.to_k, norm_vx)
+        _mark("msa.quant_k_linear")
         v = L.fp8_linear_forward(a.to_v, norm_vx)
+        _mark("msa.quant_v_linear")
     qr, kr = L.fused_video_qk_rmsnorm_rope(q, k, a.q_norm_weight, a.k_norm_weight, block.eps, cos, sin)
+    _mark("msa.qk_rmsnorm_rope")
     o = attention_video(qr, kr, v, a.heads)
+    _mark("msa.attention")
     if a.to_gate_logits is not None:
         gates = 2.0 * torch.sigmoid(a.to_gate_logits(norm_vx))
         og = L.fused_head_gate_mul_bf16(o, gates, a.heads, o.shape[-1] // a.heads)
+        _mark("msa.head_gates")
     else:
         gates, og = None, o
     proj = L.fp8_linear_without_bias(a.to_out, og, out_dtype=og.dtype)
     if proj is None:
         raise RuntimeError("to_out is not an FP8 linear")
+    _mark("msa.quant_out_linear")
     out = L.fused_residual_gate_bias_from_ada(vx, proj, a.to_out.bias, block.table, timesteps, gate_index=2)
+    _mark("msa.residual_gate_bias")
     if stages is not None:
         for name, val in (("msa.x", vx), ("msa.norm", norm_vx), ("msa.norm_q8", norm_q8), ("msa.q", q), ("msa.k", k), ("msa.v", v),
                           ("msa.qr", qr), ("msa.kr", kr), ("msa.attn", o), ("msa.gates", gates),
@@ -211,29 +251,43 @@ def video_text_cross_attention(block: VideoBlock, vx: torch.Tensor, context: tor
         shift_kv, scale_kv = (block.prompt_table[None, None].to(device=vx.device, dtype=vx.dtype)
                               + prompt_timestep.reshape(b, prompt_timestep.shape[1], 2, -1)).unbind(dim=2)
         enc = context * (1 + scale_kv) + shift_kv
+    _mark("ca.context_affine")
     attn_in_q8 = None
     if fuse_norm and fuse_ada_quant:
         normed = attn_in = None
         attn_in_q8 = L.fused_adazero_from_ada_fp8(vx, block.eps, block.table, timesteps, a.to_q.input_scale,
                                                   shift_index=6, scale_index=7)
+        _mark("ca.adazero_fp8")
     elif fuse_norm:
         normed = None
         attn_in = L.fused_adazero_from_ada(vx, block.eps, block.table, timesteps, shift_index=6, scale_index=7)
+        _mark("ca.adazero")
     else:
         normed = _rms_norm(vx, block.eps)
+        _mark("ca.rms_norm")
         attn_in = L.fused_adaln_affine_from_ada(normed, block.table, timesteps, shift_index=6, scale_index=7)
+        _mark("ca.adaln_affine")
     qk_norm = L.qk_rmsnorm if fuse_norm else (lambda x, w, eps: _rms_norm(x, eps, w))
     if attn_in_q8 is not None:
         qp = L.fp8_linear_from_quantized_e4m3(a.to_q, attn_in_q8, out_dtype=vx.dtype)
+        _mark("ca.q_linear")
     else:
         qp = L.fp8_linear_forward(a.to_q, attn_in)
+        _mark("ca.quant_q_linear")
     kp = L.fp8_linear_forward(a.to_k, enc)
+    _mark("ca.quant_k_linear")
     q = qk_norm(qp, a.q_norm_weight, block.eps)
+    _mark("ca.q_rmsnorm")
     k = qk_norm(kp, a.k_norm_weight, block.eps)
+    _mark("ca.k_rmsnorm")
     v = L.fp8_linear_forward(a.to_v, enc)
+    _mark("ca.quant_v_linear")
     o = attention_video(q, k, v, a.heads)
+    _mark("ca.attention")
     ca = L.fp8_linear_forward(a.to_out, o)
+    _mark("ca.quant_out_linear")
     out = L.fused_residual_gate_from_ada(vx, ca, block.table, timesteps, gate_index=8, count_video_ada=False)
+    _mark("ca.residual_gate")
     if stages is not None:
         for name, val in (("ca.x", vx), ("ca.enc", enc), ("ca.normed", normed), ("ca.in", attn_in),
                           ("ca.in_q8", attn_in_q8), ("ca.qp", qp),
@@ -255,19 +309,28 @@ def video_feed_forward(block: VideoBlock, vx: torch.Tensor, timesteps: torch.Ten
         y = None
         yq = L.fused_adazero_from_ada_fp8(vx, block.eps, block.table, timesteps, block.ff_up.input_scale,
                                           shift_index=3, scale_index=4)
+        _mark("ff.adazero_fp8")
         h = L.fp8_linear_from_quantized_e4m3(block.ff_up, yq, out_dtype=vx.dtype)
+        _mark("ff.up_linear")
     else:
         yq = None
         y = L.fused_adazero_from_ada(vx, block.eps, block.table, timesteps, shift_index=3, scale_index=4)
+        _mark("ff.adazero")
         h = L.fp8_linear_forward(block.ff_up, y)
+        _mark("ff.quant_up_linear")
     if fuse_gelu_quant:
         g = None
         qg = L.fused_gelu_tanh_fp8_quantize_e4m3(h, block.ff_down.input_scale)
+        _mark("ff.gelu_quant")
         d = L.fp8_linear_from_quantized_e4m3(block.ff_down, qg, out_dtype=h.dtype)
+        _mark("ff.down_linear")
     else:
         g = torch.nn.functional.gelu(h, approximate="tanh")
+        _mark("ff.gelu")
         d = L.fp8_linear_forward(block.ff_down, g)
+        _mark("ff.quant_down_linear")
     out = L.fused_residual_gate_from_ada(vx, d, block.table, timesteps, gate_index=5)
+    _mark("ff.residual_gate")
     if stages is not None:
         for name, val in (("ff.x", vx), ("ff.norm", y), ("ff.norm_q8", yq), ("ff.h", h), ("ff.gelu", g), ("ff.down", d),
                           ("ff.out", out)):
