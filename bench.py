@@ -224,6 +224,17 @@ def fused_op_rows(seed: int) -> dict:
         "x(1,2304,4096) ts broadcast", fn)
     del x, table, ts
 
+    # AdaZero straight into the next FP8 linear's e4m3 input, (1, 9216, 4096),
+    # one timestep row for all tokens, a 0-dim input scale.
+    x9 = torch.randn((1, M, C), generator=g, device=dev).to(torch.bfloat16)
+    table = (torch.randn((6, C), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    ts = (torch.randn((1, 1, 6 * C), generator=g, device=dev) * 0.5).to(torch.bfloat16).expand(1, M, 6 * C)
+    s9 = torch.tensor(8.0 / 448, device=dev)
+    fn = lambda: L.fused_adazero_from_ada_fp8(x9, 1e-6, table, ts, s9, shift_index=0, scale_index=1)  # noqa: E731
+    rec("adazero_from_ada_fp8", M * C * 3 + 2 * C * 2 * 2, _graph_time_us(fn, inner=25), "x(1,9216,4096) ts broadcast",
+        fn)
+    del x9, table, ts
+
     # FP8 input quantizer at 9216 x 4096.
     xq = torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
     sq = torch.tensor(0.05, device=dev)

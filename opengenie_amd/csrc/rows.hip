@@ -422,6 +422,13 @@ enum { TAB_NONE = 0, TAB_BF16 = 1, TAB_F32 = 2 };
 // k_fp8_quant takes it (the float32 reciprocal of the scale; for a 0-dim
 // scale, Q8_BF16, r and the product are rounded to bf16), so only the codes
 // reach memory. The scale's kind is a template flag, not a per-value select.
+// The clamp must keep NaN (torch.clamp propagates it), which costs a compare
+// and a select beside v_med3_f32 per value. A row whose sum of squares is
+// finite, with finite Ada values (checked once per workgroup when they are
+// shared by all tokens) and a finite r >= 2^-126, cannot produce a NaN (x*inv
+// is then finite, (1 + scale) and shift finite, so y is finite or an
+// overflowed infinity, and y*r is never inf*0), so such rows take
+// v_med3_f32 alone; the others keep the NaN-preserving clamp.
 enum { Q8_NONE = 0, Q8_F32 = 1, Q8_BF16 = 2 };
 template <int CH, bool UNIFORM, int D0, int D1, int TAB, int Q8 = Q8_NONE>
 __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int64_t waves_per_batch) {
@@ -434,6 +441,7 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
   constexpr bool HT = TAB != TAB_NONE;
   constexpr int TD = TAB == TAB_F32 ? OGA_DT_F32 : OGA_DT_BF16;
   __shared__ float4 cst[2][2 * G];  // [shift | scale part][column / 4]
+  __shared__ uint32_t ada_bad[kAdaWaves];  // per wave: a shared Ada value is not finite
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int tid = threadIdx.x;
@@ -483,6 +491,7 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
     for (int j = 0; j < CH; ++j) xv[j] = *(const uint4*)(xb + tl * C + j * 512);
   }
   // Constants to LDS.
+  bool bad_const = false;
 #pragma unroll
   for (int q = 0; q < GPT; ++q) {
     const int gi = (tid + q * NT) % G;
@@ -517,15 +526,32 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
           c1[i] = B1 ? rbf(f) : f;
         }
       }
+      if constexpr (Q8 != Q8_NONE && UNIFORM) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) bad_const |= !__builtin_isfinite(c0[i]) || !__builtin_isfinite(c1[i]);
+      }
       cst[0][2 * gi] = make_float4(c0[0], c0[1], c0[2], c0[3]);
       cst[0][2 * gi + 1] = make_float4(c0[4], c0[5], c0[6], c0[7]);
       cst[1][2 * gi] = make_float4(c1[0], c1[1], c1[2], c1[3]);
       cst[1][2 * gi + 1] = make_float4(c1[4], c1[5], c1[6], c1[7]);
     }
   }
+  if constexpr (Q8 != Q8_NONE && UNIFORM) {
+    const uint64_t bm = __ballot(bad_const);
+    if (lane == 0) ada_bad[w] = bm != 0;
+  }
   // LDS writes done, then the barrier; no vmcnt drain (the row loads stay
   // in flight across it).
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  // Rows may take the NaN-free clamp (Q8): the workgroup's shared Ada values
+  // and r are finite (r normal); each row adds its own finite sum of squares.
+  bool clean_consts = false;
+  if constexpr (Q8 != Q8_NONE && UNIFORM) {
+    uint32_t any_bad = 0;
+#pragma unroll
+    for (int i = 0; i < kAdaWaves; ++i) any_bad |= ada_bad[i];
+    clean_consts = !any_bad && __builtin_isfinite(qr) && qr >= 0x1p-126f;
+  }
 
   const int64_t ts0 = a.s0.ts_off + b * a.s0.ts_sb + lane * 8;
   const int64_t ts1 = a.s1.ts_off + b * a.s1.ts_sb + lane * 8;
@@ -567,6 +593,9 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
     }
     const double tot = wave_sum_d((ss[0] + ss[1]) + (ss[2] + ss[3]));
     const float inv = 1.0f / sqrtf((float)(tot / (double)C) + a.eps);
+    // The chunks of the row; CLEAN: the row cannot produce a NaN (see above).
+    auto tail = [&](auto clean_c) {
+    constexpr bool CLEAN = decltype(clean_c)::value;
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       // Groups of kAdaSchedGroup chunks: keeps the constants' LDS reads (and
@@ -616,12 +645,18 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           float lo = bf16_lo(ow[i]) * qr, hi = bf16_hi(ow[i]) * qr;
-          if constexpr (Q8 == Q8_BF16) {
-            lo = rbf(lo);
-            hi = rbf(hi);
+          if constexpr (Q8 == Q8_BF16) {  // both rounded by one conversion
+            const uint32_t pq = pack_bf16(lo, hi);
+            lo = bf16_lo(pq);
+            hi = bf16_hi(pq);
           }
-          qv[2 * i] = clamp448(lo);
-          qv[2 * i + 1] = clamp448(hi);
+          if constexpr (CLEAN) {
+            qv[2 * i] = __builtin_amdgcn_fmed3f(lo, -448.0f, 448.0f);
+            qv[2 * i + 1] = __builtin_amdgcn_fmed3f(hi, -448.0f, 448.0f);
+          } else {
+            qv[2 * i] = clamp448(lo);
+            qv[2 * i + 1] = clamp448(hi);
+          }
         }
         typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
         const u32x2 o = {e4m3x4(qv[0], qv[1], qv[2], qv[3]), e4m3x4(qv[4], qv[5], qv[6], qv[7])};
@@ -630,10 +665,25 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
         st_nt16(yb + t * C + j * 512, make_uint4(ow[0], ow[1], ow[2], ow[3]));
       }
     }
+    };
+    if constexpr (Q8 != Q8_NONE && UNIFORM) {
+      if (clean_consts && __builtin_isfinite(tot))
+        tail(IC<1>{});
+      else
+        tail(IC<0>{});
+    } else {
+      tail(IC<0>{});
+    }
   };
+  // Rows alternate between two load buffers, so a row's next-row loads never
+  // need a register copy at the loop's end.
   if (t_first < a.tokens) {
-    row(IC<1>{}, t_first, xv, xv);  // its loads went out before the fill
-    for (int64_t t = t_first + V; t < a.tokens; t += V) row(IC<0>{}, t, xv, xv);
+    uint4 xw[CH];
+    row(IC<1>{}, t_first, xv, xw);  // its loads went out before the fill
+    for (int64_t t = t_first + V; t < a.tokens; t += 2 * V) {
+      row(IC<0>{}, t, xw, xv);
+      if (t + V < a.tokens) row(IC<0>{}, t + V, xv, xw);
+    }
   }
 }
 
