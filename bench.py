@@ -771,10 +771,13 @@ def main() -> None:
     assert rc == 0
     gemm_us = e0.elapsed_time(e1) * 1000.0 / reps
     achieved = flops / (gemm_us * 1e-6) / 1e12
-    # torch._scaled_mm (hipBLASLt) + the bias add on the same inputs, beside it
+    # torch._scaled_mm (hipBLASLt) on the same inputs, beside it: with the
+    # reference's separate bias add, and alone (no bias)
     wt = w.t()
     torch_us = _settled_time_us(lambda: torch._scaled_mm(q, wt, scale_a=s_in, scale_b=s_w, out_dtype=torch.bfloat16,
                                                          use_fast_accum=True) + bias, reps=10)
+    torch_nobias_us = _settled_time_us(lambda: torch._scaled_mm(q, wt, scale_a=s_in, scale_b=s_w,
+                                                                out_dtype=torch.bfloat16, use_fast_accum=True), reps=10)
 
     fused = {} if args.no_fused else fused_op_rows(args.seed)
     if fused:
@@ -808,7 +811,8 @@ def main() -> None:
                                        "algorithmic": GEMM_ALGORITHMIC_BYTES, "unit": "bytes/launch",
                                        "source": GEMM_TRAFFIC_SOURCE},
                      "us_per_launch": round(gemm_us, 2),
-                     "torch_scaled_mm_plus_bias_us": round(torch_us, 2)},
+                     "torch_scaled_mm_plus_bias_us": round(torch_us, 2),
+                     "torch_scaled_mm_no_bias_us": round(torch_nobias_us, 2)},
         "fused_ops": fused,
         "attention": attention,
         "fp8_linears": linears,

@@ -138,6 +138,37 @@ def test_adazero_from_ada_fp8(rows, cols, params, tdt, sdt, bc, batch, scale, ze
         assert (np.abs(np32(out.float())) == 448).any()
 
 
+@pytest.mark.parametrize("scale", [0.02, 0.5 / 448, 1.0e38, 3.0e38])
+@pytest.mark.parametrize("zero_dim", [True, False])
+def test_adazero_fp8_clean_and_unclean_rows(scale, zero_dim):
+    """Finite Ada values, so a workgroup's rows take the clamp without a NaN
+    select unless the row itself is not finite: rows with a NaN, an infinity,
+    a mean square beyond float32 (finite in the float64 sum, inv = 0) and
+    ordinary rows side by side, at scales whose r is normal and (1e38, 3e38)
+    below 2^-126, where every row keeps the NaN-preserving clamp. Codes bit
+    for bit against the oracle, NaN codes sign-free."""
+    from opengenie_amd.ltx_ops import fused_adazero_from_ada_fp8
+
+    cols, params, rows = 4096, 6, 300
+    x = randn((1, rows, cols), 781)
+    x[0, 7, 11] = float("nan")
+    x[0, 100, 5] = float("inf")
+    x[0, 101, 6] = float("-inf")
+    x[0, 150] = x[0, 150] * 1e30
+    x[0, 151] = 0.0
+    table = randn((params, cols), 782, std=0.02)
+    ts = randn((1, 1, params * cols), 783, std=0.5).expand(1, rows, params * cols)
+    s = torch.tensor(scale, dtype=torch.float32) if zero_dim else torch.tensor([scale], dtype=torch.float32)
+    out = fused_adazero_from_ada_fp8(g(x), 1e-6, g(table), g(ts), g(s), shift_index=3, scale_index=4)
+    _ran("fused_adazero_from_ada_fp8")
+    ref = O.adazero_from_ada(to_T(x), 1e-6, to_T(table), to_T(ts), 3, 4)
+    with np.errstate(over="ignore", invalid="ignore"):
+        codes = O.fp8_quantize_e4m3(O.bf(bf16_round(ref.v)), float(s.reshape(())), zero_dim, device="cuda")
+    got = out.view(torch.uint8).cpu().numpy()
+    assert np.array_equal(nan_canon(got), nan_canon(codes.reshape(got.shape)))
+    assert ((got[0, 7] & 0x7F) == 0x7F).all()  # the NaN row is NaN throughout
+
+
 def test_adazero_from_ada_special_values():
     """Rows with a NaN, an infinity, both infinities, all zeros, signed zeros
     and a mean square beyond float32 (1e30: inv = 0), and Ada columns with a
