@@ -278,7 +278,33 @@ def fused_op_rows(seed: int) -> dict:
     rec("residual_gate_bias_from_ada", 4 * per_tok + 2 * C * 2, us, "x,y(1,14080,4096) per-token ts")
     us = _graph_time_us(lambda: L.fused_residual_gate_from_ada(xc, yc, tab9, tsc, gate_index=8), inner=10)
     rec("residual_gate_from_ada", 4 * per_tok + C * 2, us, "x,y(1,14080,4096) per-token ts")
-    del xc, yc, tsc, flush
+    del xc, yc, tsc
+    # The residual gate (one timestep row shared by all tokens) at growing
+    # token counts, warm and cold: a least-squares line through time against
+    # bytes separates the streaming rate (its slope) from the fixed cost of a
+    # launch (ramp-up and tail: its intercept), which dominates small calls.
+    sweep = {"tokens": [], "bytes": [], "us": [], "us_cold": []}
+    ts1 = (torch.randn((1, 1, 9 * C), generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    for nt in (1152, 2304, 4608, 9216, 14080, 28160):
+        xs = torch.randn((1, nt, C), generator=g, device=dev).to(torch.bfloat16)
+        ys = torch.randn((1, nt, C), generator=g, device=dev).to(torch.bfloat16)
+        tse = ts1.expand(1, nt, 9 * C)
+        fn = lambda: L.fused_residual_gate_from_ada(xs, ys, tab9, tse, gate_index=8)  # noqa: E731
+        sweep["tokens"].append(nt)
+        sweep["bytes"].append(3 * nt * C * 2 + 2 * C * 2)
+        sweep["us"].append(round(_graph_time_us(fn, reps=5, inner=50 if nt <= 4608 else 10), 3))
+        sweep["us_cold"].append(round(_cold_graph_time_us(fn, flush), 3))
+        del xs, ys
+    for key in ("us", "us_cold"):
+        n_ = len(sweep["bytes"])
+        mb = sum(sweep["bytes"]) / n_
+        mt = sum(sweep[key]) / n_
+        slope = (sum((bb - mb) * (tt - mt) for bb, tt in zip(sweep["bytes"], sweep[key]))
+                 / sum((bb - mb) ** 2 for bb in sweep["bytes"]))  # us per byte
+        sweep[key + "_fit"] = {"stream_GB/s": round(1e-3 / slope, 1), "stream_frac": round(1e-3 / slope / HBM_PEAK_GBS, 4),
+                               "fixed_us": round(mt - slope * mb, 2)}
+    rows["residual_gate_size_sweep"] = sweep
+    del flush
     torch.cuda.empty_cache()
     return rows
 
