@@ -256,6 +256,19 @@ int oga_fp8_linear_ws(const void* a, int64_t lda, const void* w, int64_t ldw, co
                       int64_t m, int64_t n, int64_t k, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * The FP8 linear with its output dtype: out_dtype OGA_DT_BF16 (as
+ * oga_fp8_linear_ws) or OGA_DT_F16, the patched FP8Linear.forward of an fp16
+ * model (out_dtype = x.dtype, triton_ltx_ops.py:1697-1709):
+ * out = R(R(acc * scale_a * scale_b) + R(bias)) with R rounding to fp16;
+ * the bias of an fp16 output is passed as fp16 (bias_dtype OGA_DT_F16, the
+ * reference's bias.to(out.dtype)). Other arguments as oga_fp8_linear_ws.
+ */
+int oga_fp8_linear_dt_ws(const void* a, int64_t lda, const void* w, int64_t ldw, const float* scale_a,
+                         const float* scale_b, const void* bias, int bias_dtype, void* out, int out_dtype,
+                         int64_t ldo, int64_t m, int64_t n, int64_t k, void* workspace, int64_t workspace_bytes,
+                         void* stream);
+
+/*
  * Dense non-causal attention: the video self-attention that the reference
  * runs through FlashAttention-3 flash_attn_func(q, k, v) on [B, N, H, D]
  * views (benchmarks/official_ltx23_benchmark.py:3294-3369).

@@ -60,6 +60,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "oga_fp8_linear": (_i32, [_p, _i64, _p, _i64, _p, _p, _p, _i32, _p, _i64, _i64, _i64, _i64, _p]),
     "oga_fp8_linear_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "oga_fp8_linear_ws": (_i32, [_p, _i64, _p, _i64, _p, _p, _p, _i32, _p, _i64, _i64, _i64, _i64, _p, _i64, _p]),
+    "oga_fp8_linear_dt_ws": (_i32, [_p, _i64, _p, _i64, _p, _p, _p, _i32, _p, _i32, _i64, _i64, _i64, _i64, _p, _i64,
+                                    _p]),
     "oga_fp8_linear_grouped_ws": (_i32, [_p, _i64, _p, _i64, _p, _p, _p, _i32, _p, _i64, _i64, _i64, _i64, _i64, _p,
                                          _i64, _p]),
     "oga_attention": (_i32, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64, _f32, _p]),

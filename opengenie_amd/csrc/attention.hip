@@ -622,8 +622,10 @@ template <int OFF>
 OGA_DEVICE i32x8 lds_b256(uint32_t a0, uint32_t a1) {
   static_assert(OFF >= 0 && OFF < 65536, "LDS offset");
   uint4 lo, hi;
+  // Early-clobber outputs: the first read's data returns after the second
+  // read has issued, so its destination must not share a register with a1.
   asm volatile("ds_read_b128 %0, %2 offset:%4\n\tds_read_b128 %1, %3 offset:%4"
-               : "=v"(lo), "=v"(hi)
+               : "=&v"(lo), "=&v"(hi)
                : "v"(a0), "v"(a1), "i"(OFF));
   i32x8 r = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
   return r;

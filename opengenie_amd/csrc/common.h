@@ -81,6 +81,14 @@ OGA_DEVICE float rhf(float v) {
   return (float)(_Float16)v;
 }
 
+// Pack two floats into two fp16 (nearest even, v_cvt_f16_f32 each); the
+// empty asm keeps the operands float32 registers (see rhf).
+OGA_DEVICE uint32_t pack_f16(float lo, float hi) {
+  asm("" : "+v"(lo), "+v"(hi));
+  const _Float16 a = (_Float16)lo, b = (_Float16)hi;
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
 // The 16-bit activation dtypes (XDT = OGA_DT_BF16 or OGA_DT_F16): a value of
 // x's dtype from its bits, rounding to x's dtype, and 8 elements of a
 // 16-byte vector as floats.

@@ -1,11 +1,13 @@
-// FP8 (e4m3fn) x FP8 -> bf16 linear with the exact bias epilogue.
+// FP8 (e4m3fn) x FP8 -> bf16 (or fp16) linear with the exact bias epilogue.
 //
 // Reference: ltx_serve/triton_ltx_ops.py :1671-1718 (patched FP8Linear
 // forward: quantize, torch._scaled_mm(q, W.t(), scale_a, scale_b,
 // out_dtype=bf16), then `+ bias` in bf16 through fused_bias_add_bf16), with
 // :742-781 for the from-quantized / without-bias forms.
 //   out = R(acc * (scale_a * scale_b));  out = R(out + R(bias))  (if bias)
-// acc is the float32 sum over k of a[m,k]*w[n,k] (each product exact).
+// acc is the float32 sum over k of a[m,k]*w[n,k] (each product exact); R
+// rounds to the output dtype, bf16 or, for an fp16 FP8Linear (out_dtype =
+// x.dtype, :1697-1709), fp16 (the O16 template flag of every epilogue).
 //
 // Tiling (gfx950). A workgroup of 4 waves, one per SIMD, owns a 256 (M) x
 // 256 (N) output tile; wave (wm, wn) owns 128 (M) x 128 (N) of it as 4 x 4
@@ -74,6 +76,18 @@ static_assert(3 * 4096 < 65536, "fragment offsets must fit the 16-bit immediate"
 
 constexpr int kMaxGroups = 4;
 
+// The output dtype's rounding, packing and unpacking (O16: fp16, else bf16).
+template <bool O16>
+OGA_DEVICE float rout(float v) { return O16 ? rhf(v) : rbf(v); }
+template <bool O16>
+OGA_DEVICE uint32_t pack_out(float lo, float hi) { return O16 ? pack_f16(lo, hi) : pack_bf16(lo, hi); }
+template <bool O16>
+OGA_DEVICE float out_lo(uint32_t w) { return O16 ? f16_lo(w) : bf16_lo(w); }
+template <bool O16>
+OGA_DEVICE float out_hi(uint32_t w) { return O16 ? f16_hi(w) : bf16_hi(w); }
+// A 16-bit bias is in the output dtype (the host passes bias.to(fp16) for an
+// fp16 output), so R(bias) is the value itself.
+
 struct GemmArgs {
   const uint8_t* a;
   const uint8_t* w;
@@ -85,6 +99,7 @@ struct GemmArgs {
   int m, n, k;
   int tiles_m, tiles_n;
   int bias_dt;
+  int out_f16;  // output dtype fp16 (else bf16); the host picks the O16 instances by it
   int xcd_remap;
   // Persistent kernel: `units` work units, either whole tiles (the first
   // nfull tiles) or K-chunks of the remaining tiles, each cut into `split`
@@ -122,8 +137,10 @@ constexpr int slab_pos(int r, int c) { return (r >> 1) * 256 + (((r & 1) * 8 + c
 template <int OFF>
 OGA_DEVICE i32x8 frag(uint32_t a0, uint32_t a1) {
   uint4 lo, hi;
+  // Early-clobber outputs: the first read's data returns after the second
+  // read has issued, so its destination must not share a register with a1.
   asm volatile("ds_read_b128 %0, %2 offset:%4\n\tds_read_b128 %1, %3 offset:%4"
-               : "=v"(lo), "=v"(hi)
+               : "=&v"(lo), "=&v"(hi)
                : "v"(a0), "v"(a1), "i"(OFF));
   i32x8 r = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
   return r;
@@ -165,6 +182,7 @@ constexpr bool frag_bases_match() {
 }
 static_assert(frag_bases_match(), "folded fragment addresses differ from slab_pos");
 
+template <bool O16>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1))) void k_fp8_gemm(
     GemmArgs g) {
   __shared__ uint4 smem[kLdsBytes / 16];
@@ -385,7 +403,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
   const int64_t ncol0 = n0 + wn * 128;  // first output column of the wave's block
   float bv[4][4][4];
   if (has_bias) {
-    const bool bf = g.bias_dt == OGA_DT_BF16;
+    const bool bf = g.bias_dt != OGA_DT_F32;  // 16 bits: the output dtype
     const bool vec = ncol0 + 128 <= g.n && ((uintptr_t)g.bias % (bf ? 8 : 16)) == 0;
     if (vec) {
       if (bf) {
@@ -398,10 +416,10 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
         for (int i = 0; i < 4; ++i)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            bv[i][q][0] = __uint_as_float(raw[i][q].x << 16);
-            bv[i][q][1] = __uint_as_float(raw[i][q].x & 0xFFFF0000u);
-            bv[i][q][2] = __uint_as_float(raw[i][q].y << 16);
-            bv[i][q][3] = __uint_as_float(raw[i][q].y & 0xFFFF0000u);
+            bv[i][q][0] = out_lo<O16>(raw[i][q].x);
+            bv[i][q][1] = out_hi<O16>(raw[i][q].x);
+            bv[i][q][2] = out_lo<O16>(raw[i][q].y);
+            bv[i][q][3] = out_hi<O16>(raw[i][q].y);
           }
       } else {
 #pragma unroll
@@ -409,10 +427,10 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             const float4 f = *(const float4*)((const float*)g.bias + ncol0 + i * 32 + q * 8 + 4 * fh);
-            bv[i][q][0] = rbf(f.x);
-            bv[i][q][1] = rbf(f.y);
-            bv[i][q][2] = rbf(f.z);
-            bv[i][q][3] = rbf(f.w);
+            bv[i][q][0] = rout<O16>(f.x);
+            bv[i][q][1] = rout<O16>(f.y);
+            bv[i][q][2] = rout<O16>(f.z);
+            bv[i][q][3] = rout<O16>(f.w);
           }
       }
     } else {
@@ -423,9 +441,11 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int64_t c = min(ncol0 + i * 32 + q * 8 + 4 * fh + e, (int64_t)g.n - 1);
-            const float v = bf ? __uint_as_float(((uint32_t)((const uint16_t*)g.bias)[c]) << 16)
-                               : ((const float*)g.bias)[c];
-            bv[i][q][e] = rbf(v);
+            if (bf) {
+              bv[i][q][e] = out_lo<O16>((uint32_t)((const uint16_t*)g.bias)[c]);
+            } else {
+              bv[i][q][e] = rout<O16>(((const float*)g.bias)[c]);
+            }
           }
     }
   }
@@ -443,13 +463,13 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float v = rbf(acc[i][j][q * 4 + e] * sc);
+          float v = rout<O16>(acc[i][j][q * 4 + e] * sc);
           if (has_bias) v = v + bv[i][q][e];
           o[e] = v;
         }
         uint2 pk;
-        pk.x = pack_bf16(o[0], o[1]);
-        pk.y = pack_bf16(o[2], o[3]);
+        pk.x = pack_out<O16>(o[0], o[1]);
+        pk.y = pack_out<O16>(o[2], o[3]);
         const uint32_t addr = ob + (j * 32 + fr) * kOutPitch + nl * 2;
         asm volatile("ds_write_b64 %0, %1" ::"v"(addr), "v"(pk) : "memory");
       }
@@ -579,7 +599,7 @@ __device__ const uint16_t kNegZeroRow[128] = {
 #undef OGA_NZ8
 };
 
-template <bool PARTIAL>
+template <bool PARTIAL, bool O16>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1))) void k_fp8_gemm_ring(
     GemmArgs g) {
   __shared__ uint4 smem[(kABufs + kWBufs) * kSlabBytes / 16];
@@ -880,8 +900,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const f32x16& a = acc[2 * H + ii][J];
-          pk[ii][q].x = pack_bf16(acc_read(a[q * 4 + 0]) * sc, acc_read(a[q * 4 + 1]) * sc);
-          pk[ii][q].y = pack_bf16(acc_read(a[q * 4 + 2]) * sc, acc_read(a[q * 4 + 3]) * sc);
+          pk[ii][q].x = pack_out<O16>(acc_read(a[q * 4 + 0]) * sc, acc_read(a[q * 4 + 1]) * sc);
+          pk[ii][q].y = pack_out<O16>(acc_read(a[q * 4 + 2]) * sc, acc_read(a[q * 4 + 3]) * sc);
         }
       __builtin_amdgcn_sched_barrier(0);
     };
@@ -908,8 +928,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
         u32x4 y;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          y[e] = pack_bf16(__uint_as_float(ov[u][e] << 16) + __uint_as_float(bw[e] << 16),
-                           __uint_as_float(ov[u][e] & 0xFFFF0000u) + __uint_as_float(bw[e] & 0xFFFF0000u));
+          y[e] = pack_out<O16>(out_lo<O16>(ov[u][e]) + out_lo<O16>(bw[e]),
+                               out_hi<O16>(ov[u][e]) + out_hi<O16>(bw[e]));
         buffer_store_x4(y, ro, olane + u * orow4, H * 128, kStoreNT);
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -977,6 +997,7 @@ constexpr bool reduce_writes_conflict_free() {
   return true;
 }
 static_assert(reduce_writes_conflict_free(), "reduce staging writes would conflict");
+template <bool O16>
 __global__ __launch_bounds__(256) void k_fp8_splitk_reduce(GemmArgs g) {
   constexpr int kPerTile = kWaves * 64 * 64;  // float4s per tile chunk
   constexpr int kPerWave = 64 * 64;            // float4s of one wave's accumulators
@@ -1019,8 +1040,8 @@ __global__ __launch_bounds__(256) void k_fp8_splitk_reduce(GemmArgs g) {
     const int r = 32 * j + (lane & 31);
     const int cc = 32 * i + 8 * q + 4 * (lane >> 5);
     uint2 pk;
-    pk.x = pack_bf16(rbf(sum[k][0] * sc), rbf(sum[k][1] * sc));
-    pk.y = pack_bf16(rbf(sum[k][2] * sc), rbf(sum[k][3] * sc));
+    pk.x = pack_out<O16>(sum[k][0] * sc, sum[k][1] * sc);
+    pk.y = pack_out<O16>(sum[k][2] * sc, sum[k][3] * sc);
     *(uint2*)(stage + r * kReduceRow + cc * 2) = pk;
   }
   __syncthreads();
@@ -1036,9 +1057,8 @@ __global__ __launch_bounds__(256) void k_fp8_splitk_reduce(GemmArgs g) {
     const uint32_t w[4] = {lo.x, lo.y, hi.x, hi.y};
     uint32_t y[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e)  // bf16 pairs: the low half is the lower column
-      y[e] = pack_bf16(__uint_as_float(w[e] << 16) + __uint_as_float(bb[e] << 16),
-                       __uint_as_float(w[e] & 0xFFFF0000u) + __uint_as_float(bb[e] & 0xFFFF0000u));
+    for (int e = 0; e < 4; ++e)  // 16-bit pairs: the low half is the lower column
+      y[e] = pack_out<O16>(out_lo<O16>(w[e]) + out_lo<O16>(bb[e]), out_hi<O16>(w[e]) + out_hi<O16>(bb[e]));
     *(uint4*)(out + (int64_t)row * g.ldo + col) = make_uint4(y[0], y[1], y[2], y[3]);
   }
 }
@@ -1087,8 +1107,10 @@ SplitPlan split_plan(int64_t m, int64_t n, int64_t k, int64_t cus) {
   return p;
 }
 
-bool bias_ok(const void* bias, int bias_dtype) {
-  return !bias || (bias_dtype == OGA_DT_BF16 && aligned(bias, 16));
+// The persistent kernel and the reduce read the bias as 16-byte pieces of
+// 16-bit values in the output dtype.
+bool bias_ok(const void* bias, int bias_dtype, int out_dtype = OGA_DT_BF16) {
+  return !bias || (bias_dtype == out_dtype && aligned(bias, 16));
 }
 
 // Common argument checks of the FP8 linear entry points (n: all columns).
@@ -1124,14 +1146,24 @@ int launch_ring(GemmArgs& g, void* workspace, int64_t workspace_bytes, hipStream
   g.units = p.nfull;
   int64_t grid = g.units < cus ? g.units : cus;
   g.xcd_remap = (g.units % 8) == 0 && (grid % 8) == 0;
-  if (grid > 0)  // none when every tile is split (fewer tiles than CUs)
-    hipLaunchKernelGGL(k_fp8_gemm_ring<false>, dim3((unsigned)grid), dim3(64 * kWaves), 0, stream, g);
+  if (grid > 0) {  // none when every tile is split (fewer tiles than CUs)
+    if (g.out_f16)
+      hipLaunchKernelGGL((k_fp8_gemm_ring<false, true>), dim3((unsigned)grid), dim3(64 * kWaves), 0, stream, g);
+    else
+      hipLaunchKernelGGL((k_fp8_gemm_ring<false, false>), dim3((unsigned)grid), dim3(64 * kWaves), 0, stream, g);
+  }
   if (p.split > 1) {
     g.units = p.units - p.nfull;
     grid = g.units < cus ? g.units : cus;
     g.xcd_remap = (g.units % 8) == 0 && (grid % 8) == 0;
-    hipLaunchKernelGGL(k_fp8_gemm_ring<true>, dim3((unsigned)grid), dim3(64 * kWaves), 0, stream, g);
-    hipLaunchKernelGGL(k_fp8_splitk_reduce, dim3((unsigned)((nt - p.nfull) * kWaves)), dim3(256), 0, stream, g);
+    // the K-chunks write float32 partials (no epilogue: one instance)
+    hipLaunchKernelGGL((k_fp8_gemm_ring<true, false>), dim3((unsigned)grid), dim3(64 * kWaves), 0, stream, g);
+    if (g.out_f16)
+      hipLaunchKernelGGL(k_fp8_splitk_reduce<true>, dim3((unsigned)((nt - p.nfull) * kWaves)), dim3(256), 0, stream,
+                         g);
+    else
+      hipLaunchKernelGGL(k_fp8_splitk_reduce<false>, dim3((unsigned)((nt - p.nfull) * kWaves)), dim3(256), 0, stream,
+                         g);
   }
   return launch_status();
 }
@@ -1157,17 +1189,20 @@ extern "C" int64_t oga_fp8_linear_workspace_bytes(int64_t m, int64_t n, int64_t 
   return split_plan(m, n, k, cu_count()).ws_bytes;
 }
 
-extern "C" int oga_fp8_linear_ws(const void* a, int64_t lda, const void* w, int64_t ldw, const float* scale_a,
-                                 const float* scale_b, const void* bias, int bias_dtype, void* out, int64_t ldo,
-                                 int64_t m, int64_t n, int64_t k, void* workspace, int64_t workspace_bytes,
-                                 void* stream) {
+extern "C" int oga_fp8_linear_dt_ws(const void* a, int64_t lda, const void* w, int64_t ldw, const float* scale_a,
+                                    const float* scale_b, const void* bias, int bias_dtype, void* out, int out_dtype,
+                                    int64_t ldo, int64_t m, int64_t n, int64_t k, void* workspace,
+                                    int64_t workspace_bytes, void* stream) {
   if (!w || !scale_b || !out) return fail("null pointer");
+  if (out_dtype != OGA_DT_BF16 && out_dtype != OGA_DT_F16) return unsupported("output dtype must be bf16 or fp16");
   if (const int rc = check_args(a, lda, ldw, scale_a, ldo, m, n, k, workspace, workspace_bytes)) return rc;
   if (m == 0 || n == 0) return OGA_OK;
   if (ldo < n) return fail("leading dimension smaller than the row");
   if (!aligned(w, 16)) return fail("a/w rows must be 16-byte aligned");
   if (!aligned(out, 16)) return fail("out rows must be 16-byte aligned");
-  if (bias && !dt_ok(bias_dtype)) return fail("bias dtype must be bf16 or f32");
+  if (out_dtype == OGA_DT_F16 && bias && bias_dtype != OGA_DT_F16)
+    return fail("an fp16 output takes an fp16 bias (bias.to(fp16))");
+  if (out_dtype == OGA_DT_BF16 && bias && !dt_ok(bias_dtype)) return fail("bias dtype must be bf16 or f32");
   GemmArgs g{};
   set_shape(g, a, lda, ldw, scale_a, ldo, m, n, k);
   g.w = (const uint8_t*)w;
@@ -1175,10 +1210,11 @@ extern "C" int oga_fp8_linear_ws(const void* a, int64_t lda, const void* w, int6
   g.bias = bias;
   g.bias_dt = bias_dtype;
   g.out = (uint16_t*)out;
+  g.out_f16 = out_dtype == OGA_DT_F16;
   // The persistent kernel needs two slabs per tile, whole 128-column wave
   // blocks and no bias or a 16-byte aligned bf16 bias; other shapes take one
   // workgroup per tile.
-  if (k >= 2 * GKS && n % 128 == 0 && bias_ok(bias, bias_dtype)) {
+  if (k >= 2 * GKS && n % 128 == 0 && bias_ok(bias, bias_dtype, out_dtype)) {
     for (int i = 0; i < kMaxGroups; ++i) {  // one group; the others repeat it
       g.wg[i] = g.w;
       g.sbg[i] = g.sb;
@@ -1190,8 +1226,19 @@ extern "C" int oga_fp8_linear_ws(const void* a, int64_t lda, const void* w, int6
   }
   const int64_t nt = (int64_t)g.tiles_m * g.tiles_n;
   g.xcd_remap = (nt % 8) == 0;
-  hipLaunchKernelGGL(k_fp8_gemm, dim3((unsigned)nt), dim3(64 * kWaves), 0, (hipStream_t)stream, g);
+  if (g.out_f16)
+    hipLaunchKernelGGL(k_fp8_gemm<true>, dim3((unsigned)nt), dim3(64 * kWaves), 0, (hipStream_t)stream, g);
+  else
+    hipLaunchKernelGGL(k_fp8_gemm<false>, dim3((unsigned)nt), dim3(64 * kWaves), 0, (hipStream_t)stream, g);
   return launch_status();
+}
+
+extern "C" int oga_fp8_linear_ws(const void* a, int64_t lda, const void* w, int64_t ldw, const float* scale_a,
+                                 const float* scale_b, const void* bias, int bias_dtype, void* out, int64_t ldo,
+                                 int64_t m, int64_t n, int64_t k, void* workspace, int64_t workspace_bytes,
+                                 void* stream) {
+  return oga_fp8_linear_dt_ws(a, lda, w, ldw, scale_a, scale_b, bias, bias_dtype, out, OGA_DT_BF16, ldo, m, n, k,
+                              workspace, workspace_bytes, stream);
 }
 
 extern "C" int oga_fp8_linear(const void* a, int64_t lda, const void* w, int64_t ldw, const float* scale_a,

@@ -145,6 +145,11 @@ def _xdt(t: torch.Tensor) -> int:
     return _lib.DT_F16 if t.dtype == torch.float16 else _lib.DT_BF16
 
 
+def _any_dt(t: torch.Tensor) -> int:
+    """dtype code of a bf16, fp16 or float32 tensor."""
+    return {torch.bfloat16: _lib.DT_BF16, torch.float16: _lib.DT_F16, torch.float32: _lib.DT_F32}[t.dtype]
+
+
 def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
@@ -904,7 +909,10 @@ def fused_video_qkv_rmsnorm_rope_pack(q, k, v, q_weight, k_weight, eps, cos, sin
 # FP8 linear
 # --------------------------------------------------------------------------
 def _can_use_fp8_gemm(qflat: torch.Tensor, weight: torch.Tensor, scale_a, scale_b, bias, out_dtype) -> bool:
-    if out_dtype != torch.bfloat16:
+    """The HIP FP8 GEMM: e4m3 operands on the GPU (K a multiple of 128,
+    16-byte rows), one float32 scale each, a bf16/fp16/f32 bias, bf16 or
+    fp16 output."""
+    if out_dtype not in (torch.bfloat16, torch.float16):
         return False
     if not (qflat.is_cuda and weight.is_cuda) or qflat.dtype != _FP8 or weight.dtype != _FP8:
         return False
@@ -922,7 +930,7 @@ def _can_use_fp8_gemm(qflat: torch.Tensor, weight: torch.Tensor, scale_a, scale_
     if bias is not None:
         if not bias.is_cuda or bias.ndim != 1 or bias.shape[0] != weight.shape[0]:
             return False
-        if bias.dtype not in (torch.bfloat16, torch.float32):
+        if bias.dtype not in (torch.bfloat16, torch.float32, torch.float16):
             return False
     return True
 
@@ -939,7 +947,8 @@ def fp8_scaled_mm(
     """`torch._scaled_mm(qinput, weight.t(), scale_a, scale_b, out_dtype)`
     followed, if bias is given, by `out + bias.to(out.dtype)` (two roundings),
     as the reference's FP8Linear path computes (:742-759, :1691-1709).
-    qinput [M, K] and weight [N, K] are float8_e4m3fn."""
+    qinput [M, K] and weight [N, K] are float8_e4m3fn; out_dtype bf16 or
+    fp16 (an fp16 model's FP8Linear) on the HIP path."""
     if not _can_use_fp8_gemm(qinput, weight, scale_a, scale_b, bias, out_dtype):
         _fallback("fp8_scaled_mm", qinput, weight)
         out = torch._scaled_mm(qinput, weight.t(), scale_a=scale_a, scale_b=scale_b, out_dtype=out_dtype,
@@ -950,15 +959,19 @@ def fp8_scaled_mm(
     m, k = qinput.shape
     n = weight.shape[0]
     out = torch.empty((m, n), device=qinput.device, dtype=out_dtype)
+    if bias is not None and out_dtype == torch.float16:
+        bias = bias.to(torch.float16)  # the reference's bias.to(out.dtype): R(bias) in fp16
+    elif bias is not None and bias.dtype == torch.float16:
+        bias = bias.float()  # exact; the bf16 kernel rounds it to bf16 itself
     bias_c = bias.contiguous() if bias is not None else None
     _hip("fp8_scaled_mm")
     # Split-K workspace for a last round of tiles that would not fill the
     # CUs (torch's caching allocator makes the per-call tensor cheap).
     ws_bytes = int(_lib.load().oga_fp8_linear_workspace_bytes(m, n, k))
     ws = torch.empty((ws_bytes // 4,), device=qinput.device, dtype=torch.float32) if ws_bytes else None
-    _lib.call("oga_fp8_linear_ws", _ptr(qinput), qinput.stride(0), _ptr(weight), weight.stride(0), _ptr(scale_a),
-              _ptr(scale_b), _ptr(bias_c), _dt(bias_c) if bias_c is not None else 0, _ptr(out), out.stride(0), m, n,
-              k, _ptr(ws), ws_bytes, _stream(qinput))
+    _lib.call("oga_fp8_linear_dt_ws", _ptr(qinput), qinput.stride(0), _ptr(weight), weight.stride(0),
+              _ptr(scale_a), _ptr(scale_b), _ptr(bias_c), _any_dt(bias_c) if bias_c is not None else 0, _ptr(out),
+              _xdt(out), out.stride(0), m, n, k, _ptr(ws), ws_bytes, _stream(qinput))
     return out
 
 
@@ -1010,8 +1023,9 @@ def fp8_linear_without_bias(linear: torch.nn.Module, x: torch.Tensor, *,
 
 def fp8_linear_forward(linear: torch.nn.Module, x: torch.Tensor) -> torch.Tensor:
     """The patched `FP8Linear.forward` of `patch_ltx_fp8_quantize(triton_bias_add=True)`
-    (:1671-1718): quantize x with the module's input_scale, FP8 GEMM, then the
-    exact bf16 bias add — here fused into the GEMM epilogue."""
+    (:1671-1718): quantize x with the module's input_scale, FP8 GEMM to
+    x.dtype (bf16 or fp16), then the exact bias add in that dtype — here
+    fused into the GEMM epilogue."""
     origin_shape = x.shape
     qinput = fused_fp8_quantize_e4m3(x.contiguous(), linear.input_scale)
     qflat = qinput.reshape(-1, qinput.shape[-1]) if qinput.dim() == 3 else qinput

@@ -225,28 +225,32 @@ def fp8_per_head_quantize(x: np.ndarray, device: str = "cuda"):
 # --------------------------------------------------------------------------
 # FP8 linear
 # --------------------------------------------------------------------------
-def fp8_scaled_mm(a_codes: np.ndarray, w_codes: np.ndarray, scale_a: float, scale_b: float) -> np.ndarray:
-    """torch._scaled_mm(a, w.t(), scale_a, scale_b, out_dtype=bf16).
+def fp8_scaled_mm(a_codes: np.ndarray, w_codes: np.ndarray, scale_a: float, scale_b: float,
+                  out_dt: str = "bf16") -> np.ndarray:
+    """torch._scaled_mm(a, w.t(), scale_a, scale_b, out_dtype=bf16 or fp16).
 
     a [M, K] and w [N, K] are e4m3fn codes. The products of two e4m3 values
     are exact; the sum is taken in float64, scaled by scale_a*scale_b, rounded
-    to float32 and then to bf16. Matches a float32-accumulating GEMM up to its
-    accumulation rounding (the parity bar is rtol 1e-2).
+    to float32 and then to the output dtype `out_dt` ('bf16' or 'f16'; an
+    fp16 FP8Linear passes out_dtype=x.dtype, :1697-1709). Matches a
+    float32-accumulating GEMM up to its accumulation rounding (the parity
+    bar is a few output steps).
     """
     a = e4m3_decode(a_codes).astype(np.float64)
     w = e4m3_decode(w_codes).astype(np.float64)
     acc = a @ w.T
     out = (acc * (float(np.float32(scale_a)) * float(np.float32(scale_b)))).astype(np.float32)
-    return bf16_round(out)
+    return round_to(out, out_dt)
 
 
-def fp8_linear(a_codes, w_codes, scale_a, scale_b, bias: T | None) -> np.ndarray:
+def fp8_linear(a_codes, w_codes, scale_a, scale_b, bias: T | None, out_dt: str = "bf16") -> np.ndarray:
     """Patched `FP8Linear.forward` (:1691-1709): _scaled_mm, then `+ bias` in
-    bf16 (R(out + R(bias)), `fused_bias_add_bf16` / `output + bias.to(bf16)`)."""
-    out = fp8_scaled_mm(a_codes, w_codes, scale_a, scale_b)
+    the output dtype (R(out + R(bias)), `fused_bias_add_bf16` /
+    `output + bias.to(output.dtype)`, :742-760)."""
+    out = fp8_scaled_mm(a_codes, w_codes, scale_a, scale_b, out_dt)
     if bias is None:
         return out
-    return bias_add(bf(out), bias).v
+    return bias_add(T(out, out_dt), bias).v
 
 
 def fp8_requantize_common_scale(w_codes: np.ndarray, w_scale: float, common: float) -> np.ndarray:

@@ -116,22 +116,22 @@ def video_qk_rmsnorm_rope(q, k, qw, kw, eps, cos, sin):
     return split_rope(qn, cos, sin), split_rope(kn, cos, sin)
 
 
-def fp8_linear(qinput, weight, input_scale, weight_scale, bias):
-    """:742-759 / :1691-1709: _scaled_mm then `+ bias.to(bf16)`."""
+def fp8_linear(qinput, weight, input_scale, weight_scale, bias, out_dtype=torch.bfloat16):
+    """:742-759 / :1691-1709: _scaled_mm then `+ bias.to(out_dtype)`."""
     out = torch._scaled_mm(qinput, weight.t(), scale_a=input_scale, scale_b=weight_scale,
-                           out_dtype=torch.bfloat16)
+                           out_dtype=out_dtype)
     if bias is not None:
         out = out + bias.to(out.dtype)
     return out
 
 
-def fp8_linear_decoded(qinput, weight, input_scale, weight_scale, bias):
+def fp8_linear_decoded(qinput, weight, input_scale, weight_scale, bias, out_dtype=torch.bfloat16):
     """The arithmetic of :1691-1709 with torch's float32 matmul of the decoded
     e4m3 codes in place of torch._scaled_mm (which runs below 1 GFLOP/s on a
     CPU): R(R(acc * (scale_a * scale_b)) + R(bias)), acc the float32 sum of
     the exact code products."""
     acc = qinput.float() @ weight.float().t()
-    out = (acc * (input_scale.float() * weight_scale.float())).to(torch.bfloat16)
+    out = (acc * (input_scale.float() * weight_scale.float())).to(out_dtype)
     if bias is not None:
         out = out + bias.to(out.dtype)
     return out

@@ -58,6 +58,14 @@ def bf16_ulp_distance(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     return np.abs(key(a) - key(b))
 
 
+def f16_ulp_distance(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Distance in fp16 steps between two arrays of fp16 values (monotone map)."""
+    def key(x):
+        u = np.asarray(x, dtype=np.float32).astype(np.float16).view(np.uint16).astype(np.int64)
+        return np.where(u & 0x8000, 0x8000 - u, u)
+    return np.abs(key(a) - key(b))
+
+
 def bf16_step(a) -> np.ndarray:
     """Spacing of the bf16 values at |a|, elementwise: 2^(e - 7) for a normal
     a = m * 2^e (1 <= m < 2), the subnormal spacing 2^-133 below 2^-126."""

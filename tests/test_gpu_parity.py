@@ -16,8 +16,8 @@ import torch
 
 import oracle.torch_ref as tr
 from oracle import ltx_ops as O
-from oracle.numerics import T, bf16_from_bits, bf16_round, e4m3_decode, e4m3_encode
-from tests.helpers import assert_same_bits, bf16_ulp_distance, nan_canon, np32, randn, to_T
+from oracle.numerics import T, bf16_from_bits, bf16_round, e4m3_decode, e4m3_encode, f16_round
+from tests.helpers import assert_same_bits, bf16_ulp_distance, f16_ulp_distance, nan_canon, np32, randn, to_T
 
 pytestmark = pytest.mark.gpu
 
@@ -743,9 +743,141 @@ def test_fp8_linear_split_k_through_c_abi(m, n, k):
     assert (bf16_ulp_distance(outs[0], outs[1]) > 1).mean() < 1e-3
 
 
-def _bias_epilogue_ref(out_nobias: np.ndarray, bias: torch.Tensor) -> np.ndarray:
-    """R(out + R(bias)): the second rounding of the FP8 linear (:1705-1709)."""
-    return bf16_round(out_nobias + bf16_round(np32(bias))[None, :])
+def _bias_epilogue_ref(out_nobias: np.ndarray, bias: torch.Tensor, r=bf16_round) -> np.ndarray:
+    """R(out + R(bias)): the second rounding of the FP8 linear (:1705-1709),
+    R the output dtype's rounding."""
+    return r(out_nobias + r(np32(bias))[None, :])
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 520, 384), (512, 768, 1024), (1, 16, 128),
+                                   (4352, 4096, 4096),  # whole-tile rounds + split-K last round
+                                   (256, 4096, 4096),   # split-K only
+                                   (600, 16384, 384)])
+@pytest.mark.parametrize("bias_dtype", [None, torch.bfloat16, torch.float32, torch.float16])
+def test_fp8_linear_fp16_output(m, n, k, bias_dtype):
+    """An fp16 FP8Linear: out_dtype fp16, out = R(R(acc * sa * sb) + R(bias))
+    with R rounding to fp16, against the oracle; every schedule of the
+    kernel (one workgroup per tile, persistent, split-K reduce)."""
+    from opengenie_amd.ltx_ops import fp8_scaled_mm
+
+    x = randn((m, k), 270 + m, std=1.0)
+    sa = (x.float().abs().amax() / 448.0).reshape(())
+    a = torch.clamp(x.float() / sa, -448, 448).to(torch.float8_e4m3fn)
+    w, sb = _fp8_weights(n, k, 271 + n)
+    bias = randn((n,), 272, dtype=bias_dtype, std=0.01) if bias_dtype is not None else None
+    out = fp8_scaled_mm(g(a), g(w), g(sa), g(sb), g(bias) if bias is not None else None, out_dtype=torch.float16)
+    _ran("fp8_scaled_mm")
+    assert out.dtype == torch.float16 and out.shape == (m, n)
+    ref = O.fp8_linear(a.view(torch.uint8).numpy(), w.view(torch.uint8).numpy(), float(sa), float(sb),
+                       to_T(bias) if bias is not None else None, out_dt="f16")
+    got = out_np(out)
+    # fp16 carries 3 more mantissa bits than bf16, so the float32 sum order
+    # shows in more outputs: within 2 fp16 steps, and at most a few percent
+    # more than one step (sums near zero, bias cancellation).
+    close = np.isclose(got, ref, rtol=2e-3, atol=1e-3 * float(np.abs(ref).max()))
+    assert (~close).mean() < 1e-4, (~close).sum()
+    assert (f16_ulp_distance(got[~close], ref[~close]) <= 2).all()
+    if m * n >= 4096:  # a fraction of 16 outputs says nothing
+        assert (f16_ulp_distance(got, ref) > 1).mean() < 3e-2
+    else:
+        assert f16_ulp_distance(got, ref).max() <= 2
+    # the same oracle rounding to bf16 misses most outputs (only about one in
+    # eight fp16 values is also a bf16 value): the rounding is fp16's
+    if m * n >= 4096:
+        ref_bf = O.fp8_linear(a.view(torch.uint8).numpy(), w.view(torch.uint8).numpy(), float(sa), float(sb),
+                              to_T(bias) if bias is not None else None)
+        assert (f16_ulp_distance(got, ref_bf) > 0).mean() > 0.75
+
+
+@pytest.mark.parametrize("m,n,k,use_ws", [
+    (4352, 4096, 4096, False),  # persistent whole-tile schedule
+    (4352, 4096, 4096, True),   # + split-K last round
+    (256, 4096, 4096, True),    # split-K only
+    (300, 520, 384, False),     # one workgroup per tile (N not a multiple of 128)
+])
+def test_fp8_linear_fp16_bias_epilogue_is_exact(m, n, k, use_ws):
+    """fp16 output through oga_fp8_linear_dt_ws: with and without an fp16
+    bias, out_bias == R16(out_nobias + bias) bit for bit."""
+    from opengenie_amd import _lib
+
+    lib = _lib.load()
+    x = randn((m, k), 280 + m, std=1.0)
+    sa = (x.float().abs().amax() / 448.0).reshape(())
+    a = torch.clamp(x.float() / sa, -448, 448).to(torch.float8_e4m3fn)
+    w, sb = _fp8_weights(n, k, 281 + n)
+    bias = randn((n,), 282, dtype=torch.float16, std=0.01)
+    ga, gw, gsa, gsb, gb = g(a), g(w), g(sa).float(), g(sb).float(), g(bias)
+    ws_bytes = int(lib.oga_fp8_linear_workspace_bytes(m, n, k)) if use_ws else 0
+    if use_ws:
+        assert ws_bytes > 0
+    ws = torch.empty((max(ws_bytes, 4) // 4,), device="cuda", dtype=torch.float32)
+    stream = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for bp in (None, gb):
+        out = torch.empty((m, n), device="cuda", dtype=torch.float16)
+        _lib.call("oga_fp8_linear_dt_ws", ga.data_ptr(), k, gw.data_ptr(), k, gsa.data_ptr(), gsb.data_ptr(),
+                  bp.data_ptr() if bp is not None else None, _lib.DT_F16, out.data_ptr(), _lib.DT_F16, n, m, n, k,
+                  ws.data_ptr() if use_ws else None, ws_bytes, stream)
+        torch.cuda.synchronize()
+        outs.append(out.cpu().view(torch.int16).numpy())
+    nob = outs[0].view(np.float16).astype(np.float32)
+    exp = _bias_epilogue_ref(nob, bias, f16_round).astype(np.float16).view(np.int16)
+    assert np.array_equal(outs[1], exp), int((outs[1] != exp).sum())
+    # an fp16 output with a bf16 bias is refused (the host converts it first)
+    out = torch.empty((m, n), device="cuda", dtype=torch.float16)
+    with pytest.raises(RuntimeError):
+        _lib.call("oga_fp8_linear_dt_ws", ga.data_ptr(), k, gw.data_ptr(), k, gsa.data_ptr(), gsb.data_ptr(),
+                  g(bias.to(torch.bfloat16)).data_ptr(), _lib.DT_BF16, out.data_ptr(), _lib.DT_F16, n, m, n, k,
+                  None, 0, stream)
+
+
+def test_fp8_linear_fp16_output_against_torch_scaled_mm():
+    """torch._scaled_mm with out_dtype fp16 on the same codes (hipBLASLt):
+    the same roundings, so within one fp16 step bar the sum order."""
+    from opengenie_amd.ltx_ops import fp8_scaled_mm
+
+    m, n, k = 1024, 4096, 4096
+    x = randn((m, k), 290, std=1.0)
+    sa = (x.float().abs().amax() / 448.0).reshape(())
+    a = g(torch.clamp(x.float() / sa, -448, 448).to(torch.float8_e4m3fn))
+    w, sb = _fp8_weights(n, k, 291)
+    w, sa, sb = g(w), g(sa).float(), g(sb).float()
+    bias = g(randn((n,), 292, std=0.01))
+    try:
+        ref = torch._scaled_mm(a, w.t(), scale_a=sa, scale_b=sb, out_dtype=torch.float16, use_fast_accum=True)
+    except RuntimeError as exc:  # the installed hipBLASLt may lack an fp8 -> fp16 kernel
+        pytest.skip(f"torch._scaled_mm fp16 output: {exc}")
+    ref = ref + bias.to(torch.float16)
+    out = fp8_scaled_mm(a, w, sa, sb, bias, out_dtype=torch.float16)
+    _ran("fp8_scaled_mm")
+    d = f16_ulp_distance(out_np(out), out_np(ref))
+    assert (d > 1).mean() < 3e-2 and (d > 0).mean() < 0.5, ((d > 1).mean(), (d > 0).mean())
+
+
+def test_fp8_linear_forward_fp16_module():
+    """The patched FP8Linear.forward with an fp16 input: out_dtype = x.dtype,
+    the fp16 quantizer and the fp16 GEMM both on the HIP path."""
+    from opengenie_amd.ltx_ops import fp8_linear_forward
+
+    class Lin(torch.nn.Module):
+        pass
+
+    lin = Lin()
+    w, sb = _fp8_weights(1024, 512, 293)
+    lin.weight = g(w)
+    lin.weight_scale = g(sb).float()
+    lin.input_scale = g(torch.tensor(0.0123))
+    lin.bias = g(randn((1024,), 294, std=0.01))  # bf16, as a checkpoint holds it
+    x = randn((1, 333, 512), 295, dtype=torch.float16)
+    out = fp8_linear_forward(lin, g(x))
+    _ran("fused_fp8_quantize_e4m3")
+    _ran("fp8_scaled_mm")
+    assert out.shape == (1, 333, 1024) and out.dtype == torch.float16
+    q = O.fp8_quantize_e4m3(to_T(x), 0.0123, True, device="cuda").reshape(333, 512)
+    ref = O.fp8_linear(q, w.view(torch.uint8).numpy(), 0.0123, float(sb), to_T(lin.bias.cpu()), out_dt="f16")
+    got = out_np(out).reshape(333, 1024)
+    close = np.isclose(got, ref, rtol=2e-3, atol=1e-3 * float(np.abs(ref).max()))
+    assert (~close).mean() < 1e-4 and (f16_ulp_distance(got[~close], ref[~close]) <= 2).all()
 
 
 @pytest.mark.parametrize("m,n,k,bias_dtype,use_ws", [

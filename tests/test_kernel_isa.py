@@ -10,10 +10,15 @@ may read a tile before its DMA has landed, a timing-dependent error in the
 attention output. n may leave the DMA of the next step in flight (the K and
 V DMA of one tile: 4 instructions per wave of an 8-wave workgroup), which
 was sent after the tile the step reads; loads complete in order.
+
+The GEMM and attention kernels read their MFMA operand fragments with
+inline-assembly ds_read pairs, whose data the compiler takes to be there at
+once: no instruction may name a register such a read will still write.
 """
 
 from __future__ import annotations
 
+import functools
 import os
 import re
 import subprocess
@@ -26,6 +31,7 @@ from opengenie_amd import build
 CSRC = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "opengenie_amd", "csrc")
 
 
+@functools.lru_cache(maxsize=None)
 def _device_asm(src: str) -> str:
     """The device assembly of src; the same source must also assemble (-S
     alone does not check inline-assembly operands such as offset ranges)."""
@@ -111,3 +117,101 @@ def test_fp8_attention_barriers_wait_for_lds_dma():
     assert sum(1 for ins in body if ins == "s_barrier") >= 2
     assert any("load_lds" in ins for ins in body)
     assert barrier_violations(body, max_vmcnt=2) == []
+
+
+# ----------------------------------------------------------------- LDS reads
+_LDS_RESULT = ("ds_read", "ds_load", "ds_bpermute", "ds_permute", "ds_swizzle")
+
+
+def _vregs(text: str) -> set:
+    out = set()
+    for m in re.finditer(r"\bv\[(\d+):(\d+)\]|\bv(\d+)\b", text):
+        if m.group(1) is not None:
+            out.update(range(int(m.group(1)), int(m.group(2)) + 1))
+        else:
+            out.add(int(m.group(3)))
+    return out
+
+
+def lds_read_hazards(body: list[str]) -> list[int]:
+    """Indexes of instructions that name a VGPR an LDS read still in flight
+    will write: the read's data returns after later instructions issue, so
+    such a register may be read before the data lands, or overwritten by it
+    afterwards. s_waitcnt lgkmcnt(n) retires all but the newest n LDS
+    operations (LDS operations complete in order); the check runs through
+    each straight-line stretch (an unconditional branch ends one). The
+    compiler places its own waits for the LDS reads it sees; inline-assembly
+    reads are the kernel's to wait for, and a multi-instruction asm block
+    with outputs that are not early-clobber can hand the first read's
+    destination to the second read as its address."""
+    pending: list[set] = []
+    bad = []
+    for i, ins in enumerate(body):
+        if not ins or ins.startswith("."):
+            continue
+        op, _, args = ins.partition(" ")
+        if op.endswith(":"):
+            continue
+        if op in ("s_branch", "s_endpgm", "s_setpc_b64"):
+            pending = []
+            continue
+        if op == "s_waitcnt":
+            m = re.search(r"lgkmcnt\((\d+)\)", args)
+            if m:
+                del pending[:max(0, len(pending) - int(m.group(1)))]
+            continue
+        busy = set().union(*pending) if pending else set()
+        if op.startswith("ds_"):
+            ops = [a.strip() for a in re.split(r",(?![^\[]*\])", args)]
+            returns = op.startswith(_LDS_RESULT) or "_rtn" in op
+            dst = _vregs(ops[0]) if returns else set()
+            srcs = set().union(*(_vregs(o) for o in (ops[1:] if returns else ops)))
+            if (srcs | dst) & busy:
+                bad.append(i)
+            pending.append(dst)
+        elif op.startswith(("s_load", "s_buffer_load")):
+            pending.append(set())  # also counted by lgkmcnt
+        elif _vregs(args) & busy:
+            bad.append(i)
+    return bad
+
+
+def test_lds_read_hazard_check_sees_both_mistakes():
+    # the first read's destination is the second read's address
+    body = ["ds_read_b128 v[2:5], v2 offset:0", "ds_read_b128 v[6:9], v3 offset:0", "s_waitcnt lgkmcnt(0)"]
+    assert lds_read_hazards(body) == [1]
+    body = ["ds_read_b128 v[10:13], v2 offset:0", "ds_read_b128 v[14:17], v3 offset:0", "s_waitcnt lgkmcnt(0)",
+            "v_add_f32_e32 v0, v10, v14"]
+    assert lds_read_hazards(body) == []
+    # a use before the wait, and one that the wait of the newest read leaves open
+    body = ["ds_read_b64 v[4:5], v1", "v_mov_b32_e32 v6, v4", "s_waitcnt lgkmcnt(0)"]
+    assert lds_read_hazards(body) == [1]
+    body = ["ds_read_b64 v[4:5], v1", "ds_read_b64 v[8:9], v1 offset:8", "s_waitcnt lgkmcnt(1)",
+            "v_mov_b32_e32 v6, v4", "v_mov_b32_e32 v7, v8"]
+    assert lds_read_hazards(body) == [4]
+    body = ["ds_read_b64 v[4:5], v1", "s_branch .LBB0_2", ".LBB0_1:", "v_mov_b32_e32 v4, 0"]
+    assert lds_read_hazards(body) == []
+
+
+@pytest.mark.skipif(not os.path.exists("/opt/rocm/bin/hipcc") and not os.environ.get("HIPCC"),
+                    reason="hipcc not present")
+@pytest.mark.parametrize("src", ["fp8_gemm.hip", "attention.hip"])
+def test_no_register_of_an_outstanding_lds_read_is_named(src):
+    """Every kernel of the two sources that read LDS through inline assembly
+    (the other sources leave their LDS reads to the compiler, which waits for
+    them itself): no instruction names a register that an LDS read still in
+    flight will write. For the operand fragments this needs the
+    early-clobber outputs of their two-read asm."""
+    asm = _device_asm(os.path.join(CSRC, src))
+    lines = asm.splitlines()
+    kernels = [i for i, l in enumerate(lines) if re.match(r"^_Z\w+:", l) and ".amdhsa" not in l]
+    assert kernels
+    checked = 0
+    for start in kernels:
+        end = next((i for i in range(start, len(lines)) if lines[i].strip().startswith(".Lfunc_end")), None)
+        if end is None:
+            continue
+        body = [l.split(";")[0].strip() for l in lines[start + 1:end]]
+        assert lds_read_hazards(body) == [], (src, lines[start])
+        checked += 1
+    assert checked >= 1

@@ -15,7 +15,8 @@ import torch
 import oracle.torch_ref as tr
 from oracle import ltx_ops as O
 from oracle.numerics import T, bf16_from_bits, bf16_round, e4m3_decode, e4m3_encode, f16_from_bits, f16_round
-from tests.helpers import assert_same_bits, bf16_step, bf16_ulp_distance, nan_canon, np32, randn, to_T
+from tests.helpers import (assert_same_bits, bf16_step, bf16_ulp_distance, f16_ulp_distance, nan_canon, np32,
+                           randn, to_T)
 
 
 # ----------------------------------------------------------------- numerics
@@ -325,6 +326,21 @@ def test_fp8_scaled_mm_matches_torch_scaled_mm_cpu():
     assert (bf16_ulp_distance(ours, np32(ref)) > 1).mean() < 1e-3
 
 
+def test_fp8_scaled_mm_fp16_matches_torch_scaled_mm_cpu():
+    """An fp16 FP8Linear (out_dtype = x.dtype): _scaled_mm to fp16, then
+    `+ bias.to(fp16)`; the same oracle with bf16 rounding must not pass."""
+    a, sa = _fp8_codes((48, 256), 54, 1.0)
+    w, sb = _fp8_codes((80, 256), 55, 0.02)
+    bias = randn((80,), 56, std=0.01)
+    ref = np32(tr.fp8_linear(a, w, torch.tensor(sa), torch.tensor(sb), bias, out_dtype=torch.float16))
+    args = (a.view(torch.uint8).numpy(), w.view(torch.uint8).numpy(), sa, sb, to_T(bias))
+    ours = O.fp8_linear(*args, out_dt="f16")
+    assert np.array_equal(ours, f16_round(ours))
+    d = f16_ulp_distance(ours, ref)
+    assert d.max() <= 1 and (d > 0).mean() < 0.02, (d.max(), (d > 0).mean())
+    assert (f16_ulp_distance(O.fp8_linear(*args), ref) > 1).mean() > 0.5
+
+
 def test_fp8_scaled_mm_brute_force_tiny():
     rng = np.random.default_rng(53)
     a = rng.integers(0, 256, size=(3, 16), dtype=np.uint8)
@@ -337,6 +353,13 @@ def test_fp8_scaled_mm_brute_force_tiny():
         for j in range(5):
             s = sum(av[i, k] * wv[j, k] for k in range(16)) * 0.125
             assert out[i, j] == bf16_round(np.float32(s))
+    bias = np.float32([3.0e-3, -7.1e-2, 1.9e-4, 0.5, -2.25])
+    out16 = O.fp8_linear(a, w, 0.5, 0.25, T(bf16_round(bias), "bf16"), out_dt="f16")
+    for i in range(3):
+        for j in range(5):
+            s = sum(av[i, k] * wv[j, k] for k in range(16)) * 0.125
+            r = np.float16(np.float32(s))
+            assert out16[i, j] == np.float32(np.float16(np.float32(r) + np.float32(np.float16(bf16_round(bias)[j]))))
 
 
 # ----------------------------------------------------------------- Q/K RoPE
