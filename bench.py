@@ -324,6 +324,7 @@ def _block_op_work(name: str, ctx_tokens: int) -> tuple[str, float] | None:
         "ca.adazero_fp8": ("bytes", 1.5 * row),
         "msa.qk_rmsnorm_rope": ("bytes", 4 * row + 2 * 32 * M * 64 * 2),
         "msa.residual_gate_bias": ("bytes", 3 * row), "ca.residual_gate": ("bytes", 3 * row),
+        "msa.residual_gate_bias_adazero": ("bytes", 3.5 * row), "ca.residual_gate_adazero": ("bytes", 3.5 * row),
         "ff.residual_gate": ("bytes", 3 * row),
         "ca.rms_norm": ("bytes", 2 * row), "ca.adaln_affine": ("bytes", 2 * row),
         "ca.q_rmsnorm": ("bytes", 2 * row),
@@ -344,7 +345,12 @@ def block_rows(seed: int, reps: int = 5, ctx_tokens: int = 256) -> dict:
     timed between HIP events recorded after each launch
     (`block.launch_marks`), with achieved GB/s (row ops) or TFLOP/s (GEMMs,
     attention) where the op has its own algorithmic work. The FP8 scales are
-    declared fixed (`frozen_fp8_scales`), as a loaded model's are."""
+    declared fixed (`frozen_fp8_scales`), as a loaded model's are. A spin
+    kernel (`torch.cuda._sleep`, ~10 ms) runs before each rep's start event,
+    so the host enqueues the slice while the GPU is busy and no interval
+    holds host launch time (without it the first op of a rep, and any op
+    whose host-side work outlasts the GPU's, measured the host); the same
+    slice without the head start is reported as `block_host_paced`."""
     import torch
 
     from opengenie_amd import block as B
@@ -360,35 +366,43 @@ def block_rows(seed: int, reps: int = 5, ctx_tokens: int = 256) -> dict:
     sin = torch.randn((1, 32, M, 64), generator=g, device="cuda").clamp(-1, 1).to(torch.bfloat16)
     st = torch.cuda.current_stream()
     rows = {}
-    modes = ("production_flags", "mi355x_fusions", "mi355x_fusions_ada_quant")
+    modes = ("production_flags", "mi355x_fusions", "mi355x_fusions_ada_quant", "mi355x_fusions_residual_ada")
 
     def run(key):
         # production flags; then the MI355X-side fusions (grouped Q/K/V,
         # rms_norm + AdaLN as one AdaZero, GELU in the down-projection's
         # quantizer); then also each AdaZero that feeds an FP8 linear writing
-        # that linear's e4m3 input
+        # that linear's e4m3 input; then also each residual gate and the next
+        # branch's AdaZero pass as one
         fuse = key != "production_flags"
-        aq = key == "mi355x_fusions_ada_quant"
-        x1 = B.video_self_attention(blk, vx, ts, cos, sin, qkv_grouped=fuse, fuse_ada_quant=aq)
-        x2 = B.video_text_cross_attention(blk, x1, ctx, ts, pts, fuse_norm=fuse, fuse_ada_quant=aq)
-        return B.video_feed_forward(blk, x2, ts, fuse_gelu_quant=fuse, fuse_ada_quant=aq)
+        aq = key in ("mi355x_fusions_ada_quant", "mi355x_fusions_residual_ada")
+        ra = key == "mi355x_fusions_residual_ada"
+        return B.video_block_forward(blk, vx, ctx, ts, pts, cos, sin, fuse_gelu_quant=fuse, qkv_grouped=fuse,
+                                     fuse_norm=fuse, fuse_ada_quant=aq, fuse_residual_ada=ra)
 
     with L.frozen_fp8_scales():
         for key in modes:
-            parts = {"self_attention": [], "text_cross_attention": [], "feed_forward": [], "block": []}
-            for rep in range(reps + 2):
+            parts = {"self_attention": [], "text_cross_attention": [], "feed_forward": [], "block": [],
+                     "block_host_paced": []}
+            for rep in range(2 * reps + 2):
                 ev = {}
+                head_start = rep % 2 == 0
 
                 def mark(name):
                     e = torch.cuda.Event(enable_timing=True)
                     e.record(st)
                     ev[name] = e
 
+                if head_start:
+                    torch.cuda._sleep(20_000_000)  # GPU cycles: ~10 ms at the loaded clock
                 mark("start")
                 with B.launch_marks(mark):
                     run(key)
                 ev[list(ev)[-1]].synchronize()
                 if rep < 2:
+                    continue
+                if not head_start:
+                    parts["block_host_paced"].append(ev["start"].elapsed_time(ev[list(ev)[-1]]) * 1000.0)
                     continue
                 names = list(ev)
                 bounds = {"self_attention": ("start", [n for n in names if n.startswith("msa.")][-1]),

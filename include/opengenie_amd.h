@@ -104,6 +104,33 @@ int oga_residual_gate_bias_from_ada(const void* x, const void* y, const void* bi
                                     const void* timestep, int ts_dtype, const int64_t ts_strides[4],
                                     int gate_index, void* stream);
 
+/*
+ * A residual gate followed by the AdaZero pass that reads its output, in
+ * one pass over the rows. No single counterpart in the reference: it is the
+ * composition of `fused_residual_gate_bias_from_ada` (triton_ltx_ops.py
+ * :204-262; bias NULL: `fused_residual_gate_from_ada`, :640-692) and
+ * `fused_adazero_from_ada` (:40-91), optionally with the FP8Linear input
+ * quantizer after it (`fused_fp8_quantize_e4m3`, :144-161), as the block
+ * runs them back to back: the self-attention's residual (:3057-3064) then
+ * the cross-attention's rms_norm + AdaLN (:2856-2862), and the
+ * cross-attention's residual (:2881-2888) then the feed-forward's AdaZero
+ * (:3226-3233).
+ *   x_out = R(x + R?(R(y + R(bias)) * gate))  (bias NULL: R(x + R?(y * gate)))
+ *   out   = AdaZero(x_out) with shift/scale rows shift_index/scale_index,
+ *           bf16 rows, or with input_scale given the e4m3 codes of
+ *           oga_adazero_from_ada_fp8 (scale_zero_dim as there).
+ * Both outputs are bit-identical to the two (three) separate calls. Takes
+ * cols 4096, a timestep row shared by all tokens (ts_strides[1] == 0), and
+ * 16-byte table and timestep rows; bias, if given, (cols,) bf16 or f32,
+ * 32-byte aligned. x_out may be x (in place); out must not overlap either.
+ */
+int oga_residual_gate_adazero_from_ada(const void* x, const void* y, const void* bias, int bias_dtype,
+                                      void* x_out, void* out, int64_t batch, int64_t tokens, int64_t cols,
+                                      const void* table, int table_dtype, int64_t tab_s0, int64_t tab_s1,
+                                      const void* timestep, int ts_dtype, const int64_t ts_strides[4],
+                                      int gate_index, int shift_index, int scale_index, float eps,
+                                      const float* input_scale, int scale_zero_dim, void* stream);
+
 /* `fused_residual_gate_bf16` (triton_ltx_ops.py:590-611):
  * out = R(x + R(y * gate)), gate bf16 broadcast to (batch, tokens, cols)
  * through strides (b, t, c). */

@@ -41,6 +41,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                           _i32, _p]),
     "oga_residual_gate_bias_from_ada": (_i32, [_p, _p, _p, _i32, _p, _i64, _i64, _i64, _p, _i32, _i64, _i64, _p,
                                                _i32, _i64p, _i32, _p]),
+    "oga_residual_gate_adazero_from_ada": (_i32, [_p, _p, _p, _i32, _p, _p, _i64, _i64, _i64, _p, _i32, _i64, _i64,
+                                                  _p, _i32, _i64p, _i32, _i32, _i32, _f32, _p, _i32, _p]),
     "oga_residual_gate_bf16": (_i32, [_p, _p, _p, _i64p, _p, _i64, _i64, _i64, _p]),
     "oga_bias_add_bf16": (_i32, [_p, _p, _i32, _p, _i64, _i64, _p]),
     "oga_head_gate_mul_bf16": (_i32, [_p, _p, _i64, _i64, _p, _i64, _i64, _i64, _p]),

@@ -166,13 +166,17 @@ def _rms_norm(x: torch.Tensor, eps: float, weight: torch.Tensor | None = None) -
 
 def video_self_attention(block: VideoBlock, vx: torch.Tensor, timesteps: torch.Tensor, cos: torch.Tensor,
                          sin: torch.Tensor, stages: Stages | None = None, *, qkv_grouped: bool = False,
-                         fuse_ada_quant: bool = False) -> torch.Tensor:
+                         fuse_ada_quant: bool = False, next_adazero: dict | None = None):
     """:3006-3083 with `_attention_without_out_bias` (:2561-2648). With
     `qkv_grouped` the three projections run as one grouped FP8 GEMM
     (`fp8_qkv_from_grouped_mm`, :890-925; off in the reference's
     production), otherwise as three FP8 linears. With `fuse_ada_quant` as
     well, and no head gates (their logits read the bf16 AdaZero rows), the
-    AdaZero pass writes the grouped GEMM's e4m3 input itself."""
+    AdaZero pass writes the grouped GEMM's e4m3 input itself. With
+    `next_adazero` (the keyword arguments of the AdaZero pass that reads the
+    output: shift_index, scale_index, and input_scale for e4m3 codes) the
+    residual gate and that pass run as one (`fused_residual_gate_adazero_from_ada`)
+    and the call returns (output, that pass's output)."""
     a = block.attn1
     norm_vx = norm_q8 = qkv = None
     # The grouped projection's guard is checked before the e4m3 AdaZero pass,
@@ -214,20 +218,27 @@ def video_self_attention(block: VideoBlock, vx: torch.Tensor, timesteps: torch.T
     if proj is None:
         raise RuntimeError("to_out is not an FP8 linear")
     _mark("msa.quant_out_linear")
-    out = L.fused_residual_gate_bias_from_ada(vx, proj, a.to_out.bias, block.table, timesteps, gate_index=2)
-    _mark("msa.residual_gate_bias")
+    nxt = None
+    if next_adazero is not None:
+        out, nxt = L.fused_residual_gate_adazero_from_ada(vx, proj, block.table, timesteps, gate_index=2,
+                                                          eps=block.eps, bias=a.to_out.bias, **next_adazero)
+        _mark("msa.residual_gate_bias_adazero")
+    else:
+        out = L.fused_residual_gate_bias_from_ada(vx, proj, a.to_out.bias, block.table, timesteps, gate_index=2)
+        _mark("msa.residual_gate_bias")
     if stages is not None:
         for name, val in (("msa.x", vx), ("msa.norm", norm_vx), ("msa.norm_q8", norm_q8), ("msa.q", q), ("msa.k", k), ("msa.v", v),
                           ("msa.qr", qr), ("msa.kr", kr), ("msa.attn", o), ("msa.gates", gates),
                           ("msa.gated", og), ("msa.proj", proj), ("msa.out", out)):
             stages[name] = val
-    return out
+    return out if next_adazero is None else (out, nxt)
 
 
 def video_text_cross_attention(block: VideoBlock, vx: torch.Tensor, context: torch.Tensor,
                                timesteps: torch.Tensor, prompt_timestep: torch.Tensor,
                                stages: Stages | None = None, *, fuse_norm: bool = False,
-                               fuse_context: bool | None = None, fuse_ada_quant: bool = False) -> torch.Tensor:
+                               fuse_context: bool | None = None, fuse_ada_quant: bool = False,
+                               pre_norm: torch.Tensor | None = None, next_adazero: dict | None = None):
     """:2810-2888 (cross_attention_adaln, production flags). rms_norm
     followed by the AdaLN affine of Ada rows 6/7 is AdaZero's composition
     (R(R(R(rms_norm(x)) R(1 + scale)) + shift)); with `fuse_norm` it runs as
@@ -239,7 +250,10 @@ def video_text_cross_attention(block: VideoBlock, vx: torch.Tensor, context: tor
     the q/k RMSNorms (the module's q_norm/k_norm with no RoPE after them,
     :1866-1867) run as `qk_rmsnorm` launches instead of torch's rms_norm.
     `fuse_ada_quant` (with `fuse_norm`) has that AdaZero pass write the
-    q-projection's e4m3 input directly."""
+    q-projection's e4m3 input directly. `pre_norm` is that pass's output
+    computed already (by the previous residual gate's fused pass: bf16 rows,
+    or e4m3 codes with `fuse_ada_quant`); `next_adazero` as in
+    `video_self_attention`."""
     a = block.attn2
     b = vx.shape[0]
     if fuse_context is None:
@@ -253,7 +267,10 @@ def video_text_cross_attention(block: VideoBlock, vx: torch.Tensor, context: tor
         enc = context * (1 + scale_kv) + shift_kv
     _mark("ca.context_affine")
     attn_in_q8 = None
-    if fuse_norm and fuse_ada_quant:
+    if pre_norm is not None:
+        normed = None
+        attn_in, attn_in_q8 = (None, pre_norm) if pre_norm.dtype == torch.float8_e4m3fn else (pre_norm, None)
+    elif fuse_norm and fuse_ada_quant:
         normed = attn_in = None
         attn_in_q8 = L.fused_adazero_from_ada_fp8(vx, block.eps, block.table, timesteps, a.to_q.input_scale,
                                                   shift_index=6, scale_index=7)
@@ -286,26 +303,42 @@ def video_text_cross_attention(block: VideoBlock, vx: torch.Tensor, context: tor
     _mark("ca.attention")
     ca = L.fp8_linear_forward(a.to_out, o)
     _mark("ca.quant_out_linear")
-    out = L.fused_residual_gate_from_ada(vx, ca, block.table, timesteps, gate_index=8, count_video_ada=False)
-    _mark("ca.residual_gate")
+    nxt = None
+    if next_adazero is not None:
+        out, nxt = L.fused_residual_gate_adazero_from_ada(vx, ca, block.table, timesteps, gate_index=8,
+                                                          eps=block.eps, count_video_ada=False, **next_adazero)
+        _mark("ca.residual_gate_adazero")
+    else:
+        out = L.fused_residual_gate_from_ada(vx, ca, block.table, timesteps, gate_index=8, count_video_ada=False)
+        _mark("ca.residual_gate")
     if stages is not None:
         for name, val in (("ca.x", vx), ("ca.enc", enc), ("ca.normed", normed), ("ca.in", attn_in),
                           ("ca.in_q8", attn_in_q8), ("ca.qp", qp),
                           ("ca.kp", kp), ("ca.q", q), ("ca.k", k), ("ca.v", v), ("ca.attn", o), ("ca.proj", ca),
                           ("ca.out", out)):
             stages[name] = val
-    return out
+    return out if next_adazero is None else (out, nxt)
 
 
 def video_feed_forward(block: VideoBlock, vx: torch.Tensor, timesteps: torch.Tensor, *,
                        fuse_gelu_quant: bool = False, fuse_ada_quant: bool = False,
-                       stages: Stages | None = None) -> torch.Tensor:
+                       stages: Stages | None = None, pre_norm: torch.Tensor | None = None) -> torch.Tensor:
     """:3224-3258. With `fuse_gelu_quant` the GELU-tanh runs inside the
     down-projection's input quantizer (`fused_gelu_tanh_fp8_quantize_e4m3`,
     :164-182, off in the reference's production); otherwise torch's GELU
     (tanh) in bf16, then the down-projection's own quantizer. With
-    `fuse_ada_quant` the AdaZero pass writes the up-projection's e4m3 input."""
-    if fuse_ada_quant:
+    `fuse_ada_quant` the AdaZero pass writes the up-projection's e4m3 input.
+    `pre_norm`: that pass's output computed already (bf16 rows or e4m3
+    codes), as in `video_text_cross_attention`."""
+    if pre_norm is not None and pre_norm.dtype == torch.float8_e4m3fn:
+        y, yq = None, pre_norm
+        h = L.fp8_linear_from_quantized_e4m3(block.ff_up, yq, out_dtype=vx.dtype)
+        _mark("ff.up_linear")
+    elif pre_norm is not None:
+        y, yq = pre_norm, None
+        h = L.fp8_linear_forward(block.ff_up, y)
+        _mark("ff.quant_up_linear")
+    elif fuse_ada_quant:
         y = None
         yq = L.fused_adazero_from_ada_fp8(vx, block.eps, block.table, timesteps, block.ff_up.input_scale,
                                           shift_index=3, scale_index=4)
@@ -341,16 +374,32 @@ def video_feed_forward(block: VideoBlock, vx: torch.Tensor, timesteps: torch.Ten
 def video_block_forward(block: VideoBlock, vx: torch.Tensor, context: torch.Tensor, timesteps: torch.Tensor,
                         prompt_timestep: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, *,
                         fuse_gelu_quant: bool = False, qkv_grouped: bool = False, fuse_norm: bool = False,
-                        fuse_ada_quant: bool = False, stages: Stages | None = None) -> torch.Tensor:
+                        fuse_ada_quant: bool = False, fuse_residual_ada: bool = False,
+                        stages: Stages | None = None) -> torch.Tensor:
     """The video branches of one block: self-attention, text cross-attention,
     feed-forward (:2989-3298 without the audio and audio-video branches).
     vx (B, N, C) bf16; context (B, T, C) bf16; timesteps (B, N, 9C) or a
     stride-0 token axis; prompt_timestep (B, T, 2C); cos/sin [B or 1, H, N, 64].
     `fuse_ada_quant` has each AdaZero pass that feeds an FP8 linear write that
-    linear's e4m3 input instead of bf16 rows (`fused_adazero_from_ada_fp8`)."""
-    vx = video_self_attention(block, vx, timesteps, cos, sin, stages, qkv_grouped=qkv_grouped,
-                              fuse_ada_quant=fuse_ada_quant)
-    vx = video_text_cross_attention(block, vx, context, timesteps, prompt_timestep, stages, fuse_norm=fuse_norm,
-                                    fuse_ada_quant=fuse_ada_quant)
+    linear's e4m3 input instead of bf16 rows (`fused_adazero_from_ada_fp8`).
+    `fuse_residual_ada` runs each branch's residual gate together with the
+    next branch's AdaZero pass (`fused_residual_gate_adazero_from_ada`): the
+    self-attention's with the cross-attention's (which is an AdaZero pass
+    only with `fuse_norm`), the cross-attention's with the feed-forward's."""
+    ca_next = ff_next = None
+    if fuse_residual_ada:
+        if fuse_norm:
+            ca_next = {"shift_index": 6, "scale_index": 7}
+            if fuse_ada_quant:
+                ca_next["input_scale"] = block.attn2.to_q.input_scale
+        ff_next = {"shift_index": 3, "scale_index": 4}
+        if fuse_ada_quant:
+            ff_next["input_scale"] = block.ff_up.input_scale
+    r = video_self_attention(block, vx, timesteps, cos, sin, stages, qkv_grouped=qkv_grouped,
+                             fuse_ada_quant=fuse_ada_quant, next_adazero=ca_next)
+    vx, pre_ca = r if ca_next is not None else (r, None)
+    r = video_text_cross_attention(block, vx, context, timesteps, prompt_timestep, stages, fuse_norm=fuse_norm,
+                                   fuse_ada_quant=fuse_ada_quant, pre_norm=pre_ca, next_adazero=ff_next)
+    vx, pre_ff = r if ff_next is not None else (r, None)
     return video_feed_forward(block, vx, timesteps, fuse_gelu_quant=fuse_gelu_quant, fuse_ada_quant=fuse_ada_quant,
-                              stages=stages)
+                              stages=stages, pre_norm=pre_ff)

@@ -90,6 +90,11 @@ struct RowArgs {
   int q8;
   const float* qscale;
   int q_zero_dim;
+  // AdaZero after a residual gate (k_adazero_rows with RES): the gate's Ada
+  // source and the residual output x' = R(x + R?(y_in * gate)); the AdaZero
+  // then normalises x'.
+  AdaSrc s2;
+  uint16_t* xout;
 };
 
 template <int OP>
@@ -411,6 +416,12 @@ __global__ __launch_bounds__(512) void k_adazero_gather(RowArgs a, int rows_per_
 #define OGA_ADA_WAVES 12
 #endif
 constexpr int kAdaWaves = OGA_ADA_WAVES;
+// The residual-gate form holds a second row buffer (y_in) and takes more
+// registers: two waves per SIMD.
+constexpr int kResAdaWaves = 8;
+enum { RES_NONE = 0, RES_GATE = 1, RES_GATE_BIAS = 2 };
+template <int RES>
+constexpr int ada_waves() { return RES == RES_NONE ? kAdaWaves : kResAdaWaves; }
 #ifndef OGA_ADA_SCHED_GROUP
 #define OGA_ADA_SCHED_GROUP 2
 #endif
@@ -429,25 +440,35 @@ enum { TAB_NONE = 0, TAB_BF16 = 1, TAB_F32 = 2 };
 // is then finite, (1 + scale) and shift finite, so y is finite or an
 // overflowed infinity, and y*r is never inf*0), so such rows take
 // v_med3_f32 alone; the others keep the NaN-preserving clamp.
+//
+// RES (RES_GATE, RES_GATE_BIAS; shared timestep row only): the row is first
+// the residual gate x' = R(x + R?(y_in * gate)) (RES_GATE_BIAS:
+// R(x + R?(R(y_in + R(bias)) * gate))), as k_elem computes it, stored to
+// xout; AdaZero then normalises x'. The gate comes from the same table and
+// timestep tensor as shift and scale (so the same dtypes), and lands in LDS
+// with R(bias) beside them.
 enum { Q8_NONE = 0, Q8_F32 = 1, Q8_BF16 = 2 };
-template <int CH, bool UNIFORM, int D0, int D1, int TAB, int Q8 = Q8_NONE>
-__global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int64_t waves_per_batch) {
+template <int CH, bool UNIFORM, int D0, int D1, int TAB, int Q8 = Q8_NONE, int RES = RES_NONE>
+__global__ __launch_bounds__(64 * ada_waves<RES>()) void k_adazero_rows(RowArgs a, int64_t waves_per_batch) {
+  static_assert(RES == RES_NONE || (UNIFORM && D0 == D1), "the residual form takes a shared timestep row");
+  constexpr int NW = ada_waves<RES>();
   constexpr int C = CH * 512;
   constexpr int G = C / 8;  // groups of 8 columns
-  constexpr int NT = 64 * kAdaWaves;
+  constexpr int NT = 64 * NW;
   constexpr int GPT = (G + NT - 1) / NT;
   constexpr bool B0 = D0 == OGA_DT_BF16;
   constexpr bool B1 = D1 == OGA_DT_BF16;
   constexpr bool HT = TAB != TAB_NONE;
   constexpr int TD = TAB == TAB_F32 ? OGA_DT_F32 : OGA_DT_BF16;
-  __shared__ float4 cst[2][2 * G];  // [shift | scale part][column / 4]
-  __shared__ uint32_t ada_bad[kAdaWaves];  // per wave: a shared Ada value is not finite
+  constexpr int NC = RES == RES_NONE ? 2 : 4;
+  __shared__ float4 cst[NC][2 * G];  // [shift | scale part | gate | R(bias)][column / 4]
+  __shared__ uint32_t ada_bad[NW];   // per wave: a shared Ada value is not finite
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int tid = threadIdx.x;
   const int64_t b = blockIdx.y;
   const int64_t V = waves_per_batch;
-  const int64_t v = (int64_t)blockIdx.x * kAdaWaves + w;
+  const int64_t v = (int64_t)blockIdx.x * NW + w;
   // A wave past the batch's V waves takes no rows but joins the fill.
   const int64_t t_first = v < V ? v : a.tokens;
 
@@ -461,19 +482,31 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
   // flight (rows first made the fill wait for the row too: 6.47 against
   // 6.41 us at 1x2304x4096, 13.71 against 13.44 us with per-token
   // timesteps).
-  Raw8<TD> tr0[GPT], tr1[GPT];
-  Raw8<D0> u0[GPT];
+  Raw8<TD> tr0[GPT], tr1[GPT], tr2[GPT];
+  Raw8<D0> u0[GPT], u2[GPT];
   Raw8<D1> u1[GPT];
+  uint4 bias_raw[GPT][2];  // bf16: [0]; float32: [0], [1]
 #pragma unroll
   for (int q = 0; q < GPT; ++q) {
     const int gi = (tid + q * NT) % G;
     if constexpr (HT) {
       tr0[q] = raw8_load<TD>(a.s0.tab, a.s0.tab_off + gi * 8);
       tr1[q] = raw8_load<TD>(a.s1.tab, a.s1.tab_off + gi * 8);
+      if constexpr (RES != RES_NONE) tr2[q] = raw8_load<TD>(a.s2.tab, a.s2.tab_off + gi * 8);
     }
     if constexpr (UNIFORM) {
       u0[q] = raw8_load<D0>(a.s0.ts, a.s0.ts_off + b * a.s0.ts_sb + gi * 8);
       u1[q] = raw8_load<D1>(a.s1.ts, a.s1.ts_off + b * a.s1.ts_sb + gi * 8);
+      if constexpr (RES != RES_NONE) u2[q] = raw8_load<D0>(a.s2.ts, a.s2.ts_off + b * a.s2.ts_sb + gi * 8);
+    }
+    if constexpr (RES == RES_GATE_BIAS) {  // a uniform branch; only constant loads are in flight here
+      if (a.bias_dt == OGA_DT_BF16) {
+        bias_raw[q][0] = *(const uint4*)((const uint16_t*)a.bias + gi * 8);
+        bias_raw[q][1] = make_uint4(0, 0, 0, 0);
+      } else {
+        bias_raw[q][0] = *(const uint4*)((const float*)a.bias + gi * 8);
+        bias_raw[q][1] = *(const uint4*)((const float*)a.bias + gi * 8 + 4);
+      }
     }
   }
   const uint16_t* const xb = a.x + b * a.tokens * C + lane * 8;
@@ -484,11 +517,16 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
     qr = 1.0f / a.qscale[0];
     if constexpr (Q8 == Q8_BF16) qr = rbf(qr);
   }
-  uint4 xv[CH];
+  const uint16_t* const ib = a.y + b * a.tokens * C + lane * 8;  // RES: y_in rows
+  uint16_t* const xo = a.xout + b * a.tokens * C + lane * 8;      // RES: x' rows
+  uint4 xv[CH], yv[CH];
   {
     const int64_t tl = t_first < a.tokens ? t_first : a.tokens - 1;
 #pragma unroll
-    for (int j = 0; j < CH; ++j) xv[j] = *(const uint4*)(xb + tl * C + j * 512);
+    for (int j = 0; j < CH; ++j) {
+      xv[j] = *(const uint4*)(xb + tl * C + j * 512);
+      if constexpr (RES != RES_NONE) yv[j] = *(const uint4*)(ib + tl * C + j * 512);
+    }
   }
   // Constants to LDS.
   bool bad_const = false;
@@ -530,6 +568,37 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
 #pragma unroll
         for (int i = 0; i < 8; ++i) bad_const |= !__builtin_isfinite(c0[i]) || !__builtin_isfinite(c1[i]);
       }
+      if constexpr (RES != RES_NONE) {
+        // the gate: R?(R?tab(table) + ts) as k_elem's ada_value8 computes it
+        float c2[8], s[8];
+        if constexpr (HT) {
+          raw8_get<TD>(tr2[q], c2);
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            if (TAB == TAB_F32 && B0) c2[i] = rbf(c2[i]);
+        }
+        raw8_get<D0>(u2[q], s);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float sum = HT ? c2[i] + s[i] : s[i];
+          c2[i] = (HT && B0) ? rbf(sum) : sum;
+        }
+        cst[2][2 * gi] = make_float4(c2[0], c2[1], c2[2], c2[3]);
+        cst[2][2 * gi + 1] = make_float4(c2[4], c2[5], c2[6], c2[7]);
+        if constexpr (RES == RES_GATE_BIAS) {
+          float bb[8];
+          if (a.bias_dt == OGA_DT_BF16) {
+            unpack8(bias_raw[q][0], bb);
+          } else {
+            const uint4 l = bias_raw[q][0], h = bias_raw[q][1];
+            const uint32_t w8[8] = {l.x, l.y, l.z, l.w, h.x, h.y, h.z, h.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) bb[i] = rbf(__uint_as_float(w8[i]));
+          }
+          cst[3][2 * gi] = make_float4(bb[0], bb[1], bb[2], bb[3]);
+          cst[3][2 * gi + 1] = make_float4(bb[4], bb[5], bb[6], bb[7]);
+        }
+      }
       cst[0][2 * gi] = make_float4(c0[0], c0[1], c0[2], c0[3]);
       cst[0][2 * gi + 1] = make_float4(c0[4], c0[5], c0[6], c0[7]);
       cst[1][2 * gi] = make_float4(c1[0], c1[1], c1[2], c1[3]);
@@ -549,7 +618,7 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
   if constexpr (Q8 != Q8_NONE && UNIFORM) {
     uint32_t any_bad = 0;
 #pragma unroll
-    for (int i = 0; i < kAdaWaves; ++i) any_bad |= ada_bad[i];
+    for (int i = 0; i < NW; ++i) any_bad |= ada_bad[i];
     clean_consts = !any_bad && __builtin_isfinite(qr) && qr >= 0x1p-126f;
   }
 
@@ -562,7 +631,8 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
   // loads of the wave's next row go into `nxt` right after `cur` is
   // unpacked. The first row is peeled off the loop: with one row per wave
   // (2304 tokens) no loop-carried register copies are made at all.
-  auto row = [&](auto first_c, int64_t t, uint4(&cur)[CH], uint4(&nxt)[CH]) {
+  auto row = [&](auto first_c, int64_t t, uint4(&cur)[CH], uint4(&nxt)[CH], uint4(&cury)[CH],
+                 uint4(&nxty)[CH]) {
     if (!decltype(first_c)::value && !UNIFORM) {
 #pragma unroll
       for (int j = 0; j < CH; ++j) cur[j] = *(const uint4*)(xb + t * C + j * 512);
@@ -580,7 +650,33 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
     double ss[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
-      unpack8(cur[j], f[j]);
+      if constexpr (RES != RES_NONE) {  // x' = R(x + R?(y_in' * gate)), stored, then normalised
+        const int gi = j * 64 + lane;
+        const float4 g0 = cst[2][2 * gi], g1 = cst[2][2 * gi + 1];
+        const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+        float bv[8];
+        if constexpr (RES == RES_GATE_BIAS) {
+          const float4 b0 = cst[3][2 * gi], b1 = cst[3][2 * gi + 1];
+          bv[0] = b0.x; bv[1] = b0.y; bv[2] = b0.z; bv[3] = b0.w;
+          bv[4] = b1.x; bv[5] = b1.y; bv[6] = b1.z; bv[7] = b1.w;
+        }
+        float xf[8], yf[8], o[8];
+        unpack8(cur[j], xf);
+        unpack8(cury[j], yf);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float yy = yf[i];
+          if constexpr (RES == RES_GATE_BIAS) yy = rbf(yy + bv[i]);
+          float p = yy * gv[i];
+          if constexpr (B0) p = rbf(p);
+          o[i] = xf[i] + p;
+        }
+        const uint4 xp = pack8(o);
+        st_nt16(xo + t * C + j * 512, xp);
+        unpack8(xp, f[j]);
+      } else {
+        unpack8(cur[j], f[j]);
+      }
 #pragma unroll
       for (int i = 0; i < 8; ++i) ss[i & 3] = fma((double)f[j][i], (double)f[j][i], ss[i & 3]);
     }
@@ -588,7 +684,10 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
       const int64_t tn = t + V;
       if (tn < a.tokens) {
 #pragma unroll
-        for (int j = 0; j < CH; ++j) nxt[j] = *(const uint4*)(xb + tn * C + j * 512);
+        for (int j = 0; j < CH; ++j) {
+          nxt[j] = *(const uint4*)(xb + tn * C + j * 512);
+          if constexpr (RES != RES_NONE) nxty[j] = *(const uint4*)(ib + tn * C + j * 512);
+        }
       }
     }
     const double tot = wave_sum_d((ss[0] + ss[1]) + (ss[2] + ss[3]));
@@ -678,11 +777,11 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
   // Rows alternate between two load buffers, so a row's next-row loads never
   // need a register copy at the loop's end.
   if (t_first < a.tokens) {
-    uint4 xw[CH];
-    row(IC<1>{}, t_first, xv, xw);  // its loads went out before the fill
+    uint4 xw[CH], yw[CH];
+    row(IC<1>{}, t_first, xv, xw, yv, yw);  // its loads went out before the fill
     for (int64_t t = t_first + V; t < a.tokens; t += 2 * V) {
-      row(IC<0>{}, t, xw, xv);
-      if (t + V < a.tokens) row(IC<0>{}, t + V, xv, xw);
+      row(IC<0>{}, t, xw, xv, yw, yv);
+      if (t + V < a.tokens) row(IC<0>{}, t + V, xv, xw, yv, yw);
     }
   }
 }
@@ -691,14 +790,14 @@ __global__ __launch_bounds__(64 * kAdaWaves) void k_adazero_rows(RowArgs a, int6
 // rows = ceil(batch*tokens / (CUs * kAdaWaves)) rows per wave, and V =
 // ceil(tokens / rows) waves per batch, so every wave gets rows or rows - 1.
 static void adazero_rows_grid(int64_t batch, int64_t tokens, dim3& grid, int64_t& waves_per_batch,
-                              int64_t& rows_per_wave) {
-  const int64_t slots = (int64_t)cu_count() * kAdaWaves;
+                              int64_t& rows_per_wave, int waves = kAdaWaves) {
+  const int64_t slots = (int64_t)cu_count() * waves;
   int64_t rows = (batch * tokens + slots - 1) / slots;
   if (rows < 1) rows = 1;
   const int64_t v = (tokens + rows - 1) / rows;
   rows_per_wave = (tokens + v - 1) / v;
   waves_per_batch = v;
-  grid = dim3((unsigned)((v + kAdaWaves - 1) / kAdaWaves), (unsigned)batch);
+  grid = dim3((unsigned)((v + waves - 1) / waves), (unsigned)batch);
 }
 
 // Grid of k_adazero: about OGA_ADA_WGS_PER_CU workgroups per CU, each
@@ -828,6 +927,40 @@ static void launch_adazero_q8(RowArgs& a, dim3 grid, dim3 block, int64_t vpb, hi
     hipLaunchKernelGGL((k_adazero_rows<CH, UNIFORM, D0, D1, TAB_BF16, Q8>), grid, block, 0, st, a, vpb);
   else
     hipLaunchKernelGGL((k_adazero_rows<CH, UNIFORM, D0, D1, TAB_F32, Q8>), grid, block, 0, st, a, vpb);
+}
+
+// The residual form: 4096 columns, a shared timestep row, one Ada dtype.
+template <int D, int TAB, int Q8>
+static void launch_res_ada_q(RowArgs& a, int res, dim3 grid, int64_t vpb, hipStream_t st) {
+  const dim3 block(64 * kResAdaWaves);
+  if (res == RES_GATE_BIAS)
+    hipLaunchKernelGGL((k_adazero_rows<8, true, D, D, TAB, Q8, RES_GATE_BIAS>), grid, block, 0, st, a, vpb);
+  else
+    hipLaunchKernelGGL((k_adazero_rows<8, true, D, D, TAB, Q8, RES_GATE>), grid, block, 0, st, a, vpb);
+}
+template <int D, int TAB>
+static void launch_res_ada_t(RowArgs& a, int res, dim3 grid, int64_t vpb, hipStream_t st) {
+  if (!a.q8)
+    launch_res_ada_q<D, TAB, Q8_NONE>(a, res, grid, vpb, st);
+  else if (a.q_zero_dim)
+    launch_res_ada_q<D, TAB, Q8_BF16>(a, res, grid, vpb, st);
+  else
+    launch_res_ada_q<D, TAB, Q8_F32>(a, res, grid, vpb, st);
+}
+static int launch_res_ada(RowArgs& a, int res, int64_t batch, hipStream_t st) {
+  dim3 grid;
+  int64_t vpb = 0, rpw = 0;
+  adazero_rows_grid(batch, a.tokens, grid, vpb, rpw, kResAdaWaves);
+  const bool d_bf = a.s0.ts_dt == OGA_DT_BF16, t_bf = a.s0.tab_dt == OGA_DT_BF16;
+  if (d_bf && t_bf)
+    launch_res_ada_t<OGA_DT_BF16, TAB_BF16>(a, res, grid, vpb, st);
+  else if (d_bf)
+    launch_res_ada_t<OGA_DT_BF16, TAB_F32>(a, res, grid, vpb, st);
+  else if (t_bf)
+    launch_res_ada_t<OGA_DT_F32, TAB_BF16>(a, res, grid, vpb, st);
+  else
+    launch_res_ada_t<OGA_DT_F32, TAB_F32>(a, res, grid, vpb, st);
+  return launch_status();
 }
 
 template <int CH, int OP, bool UNIFORM, int D0, int D1>
@@ -1021,6 +1154,42 @@ extern "C" int oga_residual_gate_bias_from_ada(const void* x, const void* y, con
   if ((rc = make_ada_src(a.s0, table, table_dtype, tab_s0, tab_s1, timestep, ts_dtype, ts_strides, gate_index, INT64_MAX))) return rc;
   a.s1 = a.s0;
   return run_row<OP_RESID_BIAS>(a, batch, (hipStream_t)stream);
+}
+
+extern "C" int oga_residual_gate_adazero_from_ada(const void* x, const void* y, const void* bias, int bias_dtype,
+                                                 void* x_out, void* out, int64_t batch, int64_t tokens, int64_t cols,
+                                                 const void* table, int table_dtype, int64_t tab_s0, int64_t tab_s1,
+                                                 const void* timestep, int ts_dtype, const int64_t ts_strides[4],
+                                                 int gate_index, int shift_index, int scale_index, float eps,
+                                                 const float* input_scale, int scale_zero_dim, void* stream) {
+  RowArgs a{};
+  if (!y || !x_out) return fail("null y/x_out");
+  int rc = row_common(a, x, y, out, batch, tokens, cols);
+  if (rc) return rc;
+  if (!aligned(x_out, 16)) return fail("x_out must be 16-byte aligned");
+  if (cols != 4096) return unsupported("the residual-gate AdaZero takes 4096 columns");
+  if (bias) {
+    if (!dt_ok(bias_dtype)) return fail("bias dtype must be bf16 or f32");
+    if (!aligned(bias, 32)) return fail("bias must be 32-byte aligned");
+  }
+  a.bias = bias;
+  a.bias_dt = bias_dtype;
+  a.xout = (uint16_t*)x_out;
+  a.eps = eps;
+  if (input_scale) {
+    a.q8 = 1;
+    a.qscale = input_scale;
+    a.q_zero_dim = scale_zero_dim ? 1 : 0;
+  }
+  if ((rc = make_ada_src(a.s0, table, table_dtype, tab_s0, tab_s1, timestep, ts_dtype, ts_strides, shift_index, INT64_MAX))) return rc;
+  if ((rc = make_ada_src(a.s1, table, table_dtype, tab_s0, tab_s1, timestep, ts_dtype, ts_strides, scale_index, INT64_MAX))) return rc;
+  if ((rc = make_ada_src(a.s2, table, table_dtype, tab_s0, tab_s1, timestep, ts_dtype, ts_strides, gate_index, INT64_MAX))) return rc;
+  if (batch == 0 || tokens == 0) return OGA_OK;
+  if (batch > 65535) return unsupported("batch > 65535");
+  if (ts_strides[1] != 0) return unsupported("the residual-gate AdaZero takes a timestep row shared by all tokens");
+  if (!(a.s0.ts_vec && a.s1.ts_vec && a.s2.ts_vec && a.s0.tab_vec && a.s1.tab_vec && a.s2.tab_vec))
+    return unsupported("the residual-gate AdaZero needs 16-byte table and timestep rows");
+  return launch_res_ada(a, bias ? RES_GATE_BIAS : RES_GATE, batch, (hipStream_t)stream);
 }
 
 extern "C" int oga_residual_gate_bf16(const void* x, const void* y, const void* gate, const int64_t gate_strides[3],

@@ -44,6 +44,7 @@ __all__ = [
     "fused_residual_gate_bf16",
     "fused_head_gate_mul_bf16",
     "fused_residual_gate_from_ada",
+    "fused_residual_gate_adazero_from_ada",
     "fused_mul_from_ada",
     "fp8_linear_from_quantized_e4m3",
     "fp8_linear_without_bias",
@@ -673,6 +674,82 @@ def fused_residual_gate_bias_from_ada(
               scale_shift_table.stride(0), scale_shift_table.stride(1), _ptr(ts_view), _dt(timestep), st, gi,
               _stream(x))
     return out
+
+
+def fused_residual_gate_adazero_from_ada(
+    x: torch.Tensor,
+    y: torch.Tensor,
+    scale_shift_table: torch.Tensor,
+    timestep: torch.Tensor,
+    *,
+    gate_index: int,
+    shift_index: int,
+    scale_index: int,
+    eps: float,
+    bias: torch.Tensor | None = None,
+    input_scale: torch.Tensor | None = None,
+    count_video_ada: bool = True,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """A residual gate and the AdaZero pass that reads its output, as the
+    block runs them back to back (the self-attention's residual :3057-3064,
+    then the cross-attention's rms_norm + AdaLN :2856-2862; the
+    cross-attention's residual :2881-2888, then the feed-forward's AdaZero
+    :3226-3233), in one HIP pass over the rows. Returns (x_new, out):
+    x_new = `fused_residual_gate_bias_from_ada(x, y, bias, ...)` (:204-262;
+    bias None: `fused_residual_gate_from_ada`, :640-692) and
+    out = `fused_adazero_from_ada(x_new, eps, ...)` (:40-91), or with
+    input_scale the e4m3 codes of `fused_adazero_from_ada_fp8`; both are
+    bit-identical to those calls, which also serve every input the pass
+    does not take (hidden size other than 4096, per-token timesteps,
+    misaligned rows). No single counterpart in the reference. The Ada
+    counters move as the separate calls move them."""
+    global _VIDEO_ADA_VALUES_CALLS, _VIDEO_TEXT_ADALN_CALLS
+    ok = (_can_use_ada_from_table(x, scale_shift_table, timestep) and x.shape[-1] == 4096
+          and y.is_cuda and y.dtype == torch.bfloat16 and y.is_contiguous() and y.shape == x.shape and _aligned(y)
+          and scale_shift_table.device == x.device and timestep.device == x.device and y.device == x.device)
+    if ok and bias is not None:
+        ok = (_can_use_fused_bias_add(y, bias) and bias.ndim == 1 and bias.dtype in (torch.bfloat16, torch.float32)
+              and bias.device == x.device and (not bias.is_contiguous() or _aligned(bias, 32)))
+    if ok and input_scale is not None:
+        ok = _can_use_fused_fp8_quantize(x, input_scale) and input_scale.device == x.device
+    if ok:
+        ts_view, st, (gi, si, ci) = _ada_args(x, scale_shift_table, timestep, gate_index, shift_index, scale_index)
+        tab_s = scale_shift_table.stride()
+        ok = ts_view.stride(1) == 0 and all(
+            _ada_rows_vec8(scale_shift_table, i * tab_s[0], tab_s[1])
+            and _ada_rows_vec8(ts_view, i * ts_view.stride(2), ts_view.stride(0), ts_view.stride(1),
+                               ts_view.stride(3))
+            for i in (gi, si, ci))
+    if not ok:
+        _fallback("fused_residual_gate_adazero_from_ada", x, y, scale_shift_table, timestep)
+        if bias is not None:
+            x_new = fused_residual_gate_bias_from_ada(x, y, bias, scale_shift_table, timestep, gate_index=gate_index,
+                                                      count_video_ada=count_video_ada)
+        else:
+            x_new = fused_residual_gate_from_ada(x, y, scale_shift_table, timestep, gate_index=gate_index,
+                                                 count_video_ada=count_video_ada)
+        if input_scale is not None:
+            out = fused_adazero_from_ada_fp8(x_new, eps, scale_shift_table, timestep, input_scale,
+                                             shift_index=shift_index, scale_index=scale_index)
+        else:
+            out = fused_adazero_from_ada(x_new, eps, scale_shift_table, timestep, shift_index=shift_index,
+                                         scale_index=scale_index)
+        return x_new, out
+    if count_video_ada:
+        _VIDEO_ADA_VALUES_CALLS += 1
+    else:
+        _VIDEO_TEXT_ADALN_CALLS += 1
+    _increment_ada_counter("video")
+    bias_c = bias.contiguous() if bias is not None else None
+    x_new = torch.empty_like(x)
+    out = torch.empty(x.shape, device=x.device, dtype=_FP8) if input_scale is not None else torch.empty_like(x)
+    _hip("fused_residual_gate_adazero_from_ada")
+    _lib.call("oga_residual_gate_adazero_from_ada", _ptr(x), _ptr(y), _ptr(bias_c),
+              _dt(bias_c) if bias_c is not None else 0, _ptr(x_new), _ptr(out), x.shape[0], x.shape[1], x.shape[2],
+              _ptr(scale_shift_table), _dt(scale_shift_table), tab_s[0], tab_s[1], _ptr(ts_view), _dt(timestep), st,
+              gi, si, ci, float(eps), _ptr(input_scale),
+              int(input_scale.dim() == 0) if input_scale is not None else 0, _stream(x))
+    return x_new, out
 
 
 def fused_residual_gate_bf16(x: torch.Tensor, y: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:

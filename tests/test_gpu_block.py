@@ -96,33 +96,42 @@ def _check_attn(got, ref, v, what):
     assert float((err / (2e-3 * vrms + 2e-2 * np.abs(ref))).max()) <= 1.0, what
 
 
-@pytest.mark.parametrize("gated,fused,ada_quant", [(False, False, False), (True, True, False), (False, True, True)])
-def test_block_steps_match_oracle(gated, fused, ada_quant):
+@pytest.mark.parametrize("gated,fused,ada_quant,res_ada", [(False, False, False, False), (True, True, False, False),
+                                                            (False, True, True, False), (False, True, True, True),
+                                                            (True, True, False, True)])
+def test_block_steps_match_oracle(gated, fused, ada_quant, res_ada):
     """Every step of the slice against the oracle on that step's GPU inputs
     (the second case with the MI355X-side fusions: grouped Q/K/V, the
     cross-attention's rms_norm + AdaLN as one AdaZero, GELU in the
     down-projection's quantizer; the third, without head gates, also with
-    each AdaZero that feeds an FP8 linear writing that linear's e4m3 input)."""
+    each AdaZero that feeds an FP8 linear writing that linear's e4m3 input;
+    the last two also with each residual gate and the next branch's AdaZero
+    pass as one)."""
     from opengenie_amd import ltx_ops as L
     from opengenie_amd.block import Stages, random_video_block, video_block_forward
 
-    blk = random_video_block(C, HEADS, seed=11 + gated + 2 * ada_quant, gated=gated)
-    vx, context, ts, pts, cos, sin = _g(*_inputs(300 + 7 * gated + 13 * ada_quant))
+    blk = random_video_block(C, HEADS, seed=11 + gated + 2 * ada_quant + 4 * res_ada, gated=gated)
+    inputs = _inputs(300 + 7 * gated + 13 * ada_quant + 17 * res_ada)
+    vx, context, ts, pts, cos, sin = _g(*inputs)
+    if res_ada:  # the fused residual pass takes a timestep row shared by the tokens (stride 0)
+        ts = inputs[2][:, :1].to(DEV).expand(inputs[2].shape)
     st = Stages()
     out = video_block_forward(blk, vx, context, ts, pts, cos, sin, fuse_gelu_quant=fused, qkv_grouped=fused,
-                              fuse_norm=fused, fuse_ada_quant=ada_quant, stages=st)
+                              fuse_norm=fused, fuse_ada_quant=ada_quant, fuse_residual_ada=res_ada, stages=st)
     torch.cuda.synchronize()
     assert out.shape == vx.shape and out.dtype == torch.bfloat16
     calls = L.collect_hip_calls()
-    for op in ("fp8_scaled_mm", "fused_video_qk_rmsnorm_rope", "flash_attn_func",
-               "fused_residual_gate_bias_from_ada", "fused_residual_gate_from_ada"):
+    for op in ("fp8_scaled_mm", "fused_video_qk_rmsnorm_rope", "flash_attn_func", "fused_residual_gate_from_ada"):
         assert calls.get(op, 0) > 0, (op, calls)
+    assert calls.get("fused_residual_gate_bias_from_ada", 0) == (0 if res_ada else 1), calls
+    assert calls.get("fused_residual_gate_adazero_from_ada", 0) == (2 if res_ada else 0), calls
     assert (calls.get("fp8_grouped_linear", 0) > 0) == fused, calls
     # one AdaLN-affine launch either way: the query affine (production flags)
     # or the context affine (with the fusions, where the query side is AdaZero)
     assert calls.get("fused_adaln_affine_from_ada", 0) == 1, calls
-    assert calls.get("fused_adazero_from_ada", 0) == (0 if ada_quant else 3 if fused else 2), calls
-    assert calls.get("fused_adazero_from_ada_fp8", 0) == (3 if ada_quant else 0), calls
+    n_ada = 1 if res_ada else 3 if fused else 2  # the other two inside the residual passes
+    assert calls.get("fused_adazero_from_ada", 0) == (0 if ada_quant else n_ada), calls
+    assert calls.get("fused_adazero_from_ada_fp8", 0) == (n_ada if ada_quant else 0), calls
     assert calls.get("qk_rmsnorm", 0) == (2 if fused else 0), calls
     tab, tsT = to_T(blk.table), to_T(ts)
     a1, a2 = blk.attn1, blk.attn2
@@ -262,3 +271,29 @@ def test_block_end_to_end_against_oracle():
           f"exact {float((got == ref).mean()):.3f}")
     assert base > 0
     assert rms_rel <= 3 * base
+
+
+@pytest.mark.parametrize("ada_quant", [False, True])
+def test_block_residual_ada_fusion_changes_no_bit(ada_quant):
+    """The residual gates fused with the next branch's AdaZero pass give the
+    slice's output bit for bit as the separate passes do (the fused pass is
+    their composition, and everything else is deterministic), at 2304 tokens
+    (several rows per wave of the fused pass)."""
+    from opengenie_amd import ltx_ops as L
+    from opengenie_amd.block import random_video_block, video_block_forward
+
+    n = 2304
+    blk = random_video_block(C, HEADS, seed=31)
+    vx = randn((1, n, C), 510)
+    ts = randn((1, 1, 9 * C), 512, std=0.5).expand(1, n, 9 * C)
+    cos = randn((1, HEADS, n, 64), 514).clamp(-1, 1)
+    sin = randn((1, HEADS, n, 64), 515).clamp(-1, 1)
+    context, pts = randn((1, TCTX, C), 511), randn((1, TCTX, 2 * C), 513, std=0.5)
+    args = _g(vx, context, ts, pts, cos, sin)
+    args = args[:2] + (ts[:, :1].to(DEV).expand(ts.shape),) + args[3:]  # stride 0 over the tokens
+    kw = dict(fuse_gelu_quant=True, qkv_grouped=True, fuse_norm=True, fuse_ada_quant=ada_quant)
+    a = video_block_forward(blk, *args, **kw)
+    b = video_block_forward(blk, *args, fuse_residual_ada=True, **kw)
+    torch.cuda.synchronize()
+    assert L.collect_hip_calls().get("fused_residual_gate_adazero_from_ada", 0) == 2
+    assert_same_bits(np32(b), np32(a), "block with and without the residual fusion")
