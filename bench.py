@@ -332,6 +332,8 @@ def _block_op_work(name: str, ctx_tokens: int) -> tuple[str, float] | None:
         "msa.qkv_grouped": ("flop", 2.0 * M * 4096 * 3 * 4096), "ca.q_linear": ("flop", 2.0 * M * 4096 * 4096),
         "ff.up_linear": ("flop", 2.0 * M * 4096 * 16384), "ff.down_linear": ("flop", 2.0 * M * 16384 * 4096),
         "msa.attention": ("flop", 4.0 * M * M * 4096), "ca.attention": ("flop", 4.0 * M * ctx_tokens * 4096),
+        "msa.attention_e4m3": ("flop", 4.0 * M * M * 4096), "ca.attention_e4m3": ("flop", 4.0 * M * ctx_tokens * 4096),
+        "msa.out_linear": ("flop", 2.0 * M * 4096 * 4096), "ca.out_linear": ("flop", 2.0 * M * 4096 * 4096),
     }
     return tab.get(name)
 
@@ -345,12 +347,15 @@ def block_rows(seed: int, reps: int = 5, ctx_tokens: int = 256) -> dict:
     timed between HIP events recorded after each launch
     (`block.launch_marks`), with achieved GB/s (row ops) or TFLOP/s (GEMMs,
     attention) where the op has its own algorithmic work. The FP8 scales are
-    declared fixed (`frozen_fp8_scales`), as a loaded model's are. A spin
-    kernel (`torch.cuda._sleep`, ~10 ms) runs before each rep's start event,
-    so the host enqueues the slice while the GPU is busy and no interval
-    holds host launch time (without it the first op of a rep, and any op
-    whose host-side work outlasts the GPU's, measured the host); the same
-    slice without the head start is reported as `block_host_paced`."""
+    declared fixed (`frozen_fp8_scales`), as a loaded model's are. Each
+    timed slice follows the same slice enqueued just before it, as a model's
+    consecutive blocks run: the host then enqueues the timed slice while the
+    GPU still works on the previous one, so no interval holds host launch
+    time (timed after a synchronisation, the first op of a rep, and any op
+    whose host-side work outlasts the GPU's, measured the host) and the
+    clock is at its loaded level. The slice timed right after a
+    synchronisation is reported as `block_host_paced`. Reps go round-robin
+    over the modes."""
     import torch
 
     from opengenie_amd import block as B
@@ -366,25 +371,31 @@ def block_rows(seed: int, reps: int = 5, ctx_tokens: int = 256) -> dict:
     sin = torch.randn((1, 32, M, 64), generator=g, device="cuda").clamp(-1, 1).to(torch.bfloat16)
     st = torch.cuda.current_stream()
     rows = {}
-    modes = ("production_flags", "mi355x_fusions", "mi355x_fusions_ada_quant", "mi355x_fusions_residual_ada")
+    modes = ("production_flags", "mi355x_fusions", "mi355x_fusions_ada_quant", "mi355x_fusions_residual_ada",
+             "mi355x_fusions_out_quant")
 
     def run(key):
         # production flags; then the MI355X-side fusions (grouped Q/K/V,
         # rms_norm + AdaLN as one AdaZero, GELU in the down-projection's
         # quantizer); then also each AdaZero that feeds an FP8 linear writing
         # that linear's e4m3 input; then also each residual gate and the next
-        # branch's AdaZero pass as one
+        # branch's AdaZero pass as one; then also each attention writing its
+        # output projection's e4m3 input
         fuse = key != "production_flags"
-        aq = key in ("mi355x_fusions_ada_quant", "mi355x_fusions_residual_ada")
-        ra = key == "mi355x_fusions_residual_ada"
+        aq = key in ("mi355x_fusions_ada_quant", "mi355x_fusions_residual_ada", "mi355x_fusions_out_quant")
+        ra = key in ("mi355x_fusions_residual_ada", "mi355x_fusions_out_quant")
+        oq = key == "mi355x_fusions_out_quant"
         return B.video_block_forward(blk, vx, ctx, ts, pts, cos, sin, fuse_gelu_quant=fuse, qkv_grouped=fuse,
-                                     fuse_norm=fuse, fuse_ada_quant=aq, fuse_residual_ada=ra)
+                                     fuse_norm=fuse, fuse_ada_quant=aq, fuse_residual_ada=ra, fuse_out_quant=oq)
 
     with L.frozen_fp8_scales():
-        for key in modes:
-            parts = {"self_attention": [], "text_cross_attention": [], "feed_forward": [], "block": [],
-                     "block_host_paced": []}
-            for rep in range(2 * reps + 2):
+        # reps round-robin over the modes, so the clock's drift over the run
+        # falls on every mode alike
+        allparts = {key: {"self_attention": [], "text_cross_attention": [], "feed_forward": [], "block": [],
+                          "block_host_paced": []} for key in modes}
+        for rep in range(2 * reps + 2):
+            for key in modes:
+                parts = allparts[key]
                 ev = {}
                 head_start = rep % 2 == 0
 
@@ -393,8 +404,8 @@ def block_rows(seed: int, reps: int = 5, ctx_tokens: int = 256) -> dict:
                     e.record(st)
                     ev[name] = e
 
-                if head_start:
-                    torch.cuda._sleep(20_000_000)  # GPU cycles: ~10 ms at the loaded clock
+                if head_start:  # the same slice enqueued just before, as consecutive blocks run
+                    run(key)
                 mark("start")
                 with B.launch_marks(mark):
                     run(key)
@@ -414,6 +425,8 @@ def block_rows(seed: int, reps: int = 5, ctx_tokens: int = 256) -> dict:
                     parts[k].append(ev[a].elapsed_time(ev[b]) * 1000.0)
                 for prev, name in zip(names, names[1:]):
                     parts.setdefault("op:" + name, []).append(ev[prev].elapsed_time(ev[name]) * 1000.0)
+        for key in modes:
+            parts = allparts[key]
             row = {k: round(statistics.median(v), 1) for k, v in parts.items() if not k.startswith("op:")}
             kern = {}
             for k, v in parts.items():
@@ -427,7 +440,7 @@ def block_rows(seed: int, reps: int = 5, ctx_tokens: int = 256) -> dict:
                     ent.update({"GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)})
                 elif work:
                     tf = work[1] / (us * 1e-6) / 1e12
-                    peak = BF16_PEAK_TFLOPS if name.endswith("attention") else FP8_PEAK_TFLOPS
+                    peak = BF16_PEAK_TFLOPS if "attention" in name else FP8_PEAK_TFLOPS
                     ent.update({"TFLOP/s": round(tf, 1), "frac_peak": round(tf / peak, 3)})
                 kern[name] = ent
             row["ops"] = kern

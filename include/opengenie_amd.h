@@ -328,6 +328,24 @@ int oga_attention_ws(const void* q, const int64_t q_strides[3], const void* k, c
                      int64_t workspace_bytes, void* stream);
 
 /*
+ * oga_attention_ws whose output goes straight into the input quantizer of
+ * the FP8 linear that reads it (the attention module's to_out,
+ * triton_ltx_ops.py:1691-1709 / :762-781 after the attention call,
+ * benchmarks/official_ltx23_benchmark.py:3294-3369): o8 receives
+ * e4m3(clamp(R(o) * r, +-448)), one byte per element with o_strides, as
+ * `fused_fp8_quantize_e4m3` (:144-161) writes for the bf16 o of
+ * oga_attention_ws (r = 1/out_scale[0]; scale_zero_dim: a 0-dim scale, r and
+ * the product rounded to bf16). No counterpart in the reference: the codes
+ * are bit for bit those of the two calls, and the bf16 o is never written.
+ * Same workspace as oga_attention_ws.
+ */
+int oga_attention_e4m3_out_ws(const void* q, const int64_t q_strides[3], const void* k, const int64_t k_strides[3],
+                              const void* v, const int64_t v_strides[3], void* o8, const int64_t o_strides[3],
+                              int64_t batch, int64_t nq, int64_t nk, int64_t heads, int64_t head_dim,
+                              float softmax_scale, const float* out_scale, int scale_zero_dim, void* workspace,
+                              int64_t workspace_bytes, void* stream);
+
+/*
  * FP8 inputs of the attention (benchmarks/official_ltx23_benchmark.py
  * :3333-3340, descales from `fused_fp8_quantize_e4m3_per_head_4d`):
  * out[b, n, h, :] = R(e4m3(x8[b, n, h, :]) * descale[b, h]) as bf16;

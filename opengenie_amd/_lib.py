@@ -70,6 +70,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "oga_attention_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64]),
     "oga_attention_ws": (_i32, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64, _f32, _p,
                                 _i64, _p]),
+    "oga_attention_e4m3_out_ws": (_i32, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64,
+                                         _f32, _p, _i32, _p, _i64, _p]),
     "oga_fp8_dequant_per_head": (_i32, [_p, _p, _p, _i64, _i64, _i64, _i64, _p]),
     "oga_attention_fp8_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64]),
     "oga_attention_fp8_ws": (_i32, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _p, _p, _p, _i64p, _i64, _i64, _i64, _i64,

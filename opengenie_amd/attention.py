@@ -23,9 +23,9 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .ltx_ops import _fallback, _hip, _stream
+from .ltx_ops import _fallback, _hip, _stream, fused_fp8_quantize_e4m3
 
-__all__ = ["flash_attn_func", "attention_video"]
+__all__ = ["flash_attn_func", "attention_video", "attention_video_e4m3_out"]
 
 _FP8 = torch.float8_e4m3fn
 
@@ -163,3 +163,37 @@ def attention_video(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, heads: in
     qv, kv, vv = (t.view(b, -1, heads, dim_head) for t in (q, k, v))
     out = flash_attn_func(qv, kv, vv, q_descale=q_descale, k_descale=k_descale, v_descale=v_descale)
     return out.reshape(b, -1, heads * dim_head)
+
+
+def attention_video_e4m3_out(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, heads: int,
+                             input_scale: torch.Tensor) -> torch.Tensor:
+    """`attention_video(q, k, v, heads)` handed to the FP8 linear that reads
+    it: the e4m3 codes `fused_fp8_quantize_e4m3(attention_video(...),
+    input_scale)` (:144-161; the attention module's to_out quantizes its
+    input so, :1691-1709 / :762-781), from one HIP pass whose epilogue
+    quantizes the bf16 output instead of writing it
+    (`oga_attention_e4m3_out_ws`). No counterpart in the reference; bit for
+    bit the two calls. Inputs the bf16 kernel does not take, or a scale the
+    quantizer does not take, run the two calls."""
+    b = q.shape[0]
+    dim_head = q.shape[-1] // heads
+    qv, kv, vv = (t.view(b, -1, heads, dim_head) for t in (q, k, v))
+    # the quantizer's guard (:1021-1022, the HIP quantizer's float32 scale on
+    # the same device) holds for the fresh bf16 output the two calls make
+    ok = (all(t.dtype == torch.bfloat16 for t in (qv, kv, vv)) and _kernel_ok(qv, kv, vv)
+          and isinstance(input_scale, torch.Tensor) and input_scale.numel() == 1 and input_scale.is_cuda
+          and input_scale.dtype == torch.float32 and input_scale.device == q.device)
+    if not ok:
+        _fallback("attention_video_e4m3_out", q, k, v)
+        return fused_fp8_quantize_e4m3(attention_video(q, k, v, heads), input_scale)
+    nq, nk = qv.shape[1], kv.shape[1]
+    out = torch.empty((b, nq, heads * dim_head), device=q.device, dtype=_FP8)
+    ov = out.view(b, nq, heads, dim_head)
+    _hip("attention_video_e4m3_out")
+    ws_bytes = int(_lib.load().oga_attention_workspace_bytes(b, nq, nk, heads, dim_head))
+    ws = torch.empty((ws_bytes // 4,), device=q.device, dtype=torch.float32) if ws_bytes else None
+    _lib.call("oga_attention_e4m3_out_ws", qv.data_ptr(), _strides3(qv), kv.data_ptr(), _strides3(kv), vv.data_ptr(),
+              _strides3(vv), ov.data_ptr(), _strides3(ov), b, nq, nk, heads, dim_head, float(dim_head ** -0.5),
+              input_scale.data_ptr(), int(input_scale.dim() == 0), ws.data_ptr() if ws is not None else None,
+              ws_bytes, _stream(q))
+    return out

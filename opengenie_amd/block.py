@@ -32,7 +32,7 @@ from dataclasses import dataclass, field
 import torch
 
 from . import ltx_ops as L
-from .attention import attention_video
+from .attention import attention_video, attention_video_e4m3_out
 
 _FP8 = torch.float8_e4m3fn
 
@@ -166,7 +166,8 @@ def _rms_norm(x: torch.Tensor, eps: float, weight: torch.Tensor | None = None) -
 
 def video_self_attention(block: VideoBlock, vx: torch.Tensor, timesteps: torch.Tensor, cos: torch.Tensor,
                          sin: torch.Tensor, stages: Stages | None = None, *, qkv_grouped: bool = False,
-                         fuse_ada_quant: bool = False, next_adazero: dict | None = None):
+                         fuse_ada_quant: bool = False, next_adazero: dict | None = None,
+                         fuse_out_quant: bool = False):
     """:3006-3083 with `_attention_without_out_bias` (:2561-2648). With
     `qkv_grouped` the three projections run as one grouped FP8 GEMM
     (`fp8_qkv_from_grouped_mm`, :890-925; off in the reference's
@@ -176,7 +177,9 @@ def video_self_attention(block: VideoBlock, vx: torch.Tensor, timesteps: torch.T
     `next_adazero` (the keyword arguments of the AdaZero pass that reads the
     output: shift_index, scale_index, and input_scale for e4m3 codes) the
     residual gate and that pass run as one (`fused_residual_gate_adazero_from_ada`)
-    and the call returns (output, that pass's output)."""
+    and the call returns (output, that pass's output). With
+    `fuse_out_quant` (and no head gates) the attention writes the output
+    projection's e4m3 input itself (`attention_video_e4m3_out`)."""
     a = block.attn1
     norm_vx = norm_q8 = qkv = None
     # The grouped projection's guard is checked before the e4m3 AdaZero pass,
@@ -206,18 +209,27 @@ def video_self_attention(block: VideoBlock, vx: torch.Tensor, timesteps: torch.T
         _mark("msa.quant_v_linear")
     qr, kr = L.fused_video_qk_rmsnorm_rope(q, k, a.q_norm_weight, a.k_norm_weight, block.eps, cos, sin)
     _mark("msa.qk_rmsnorm_rope")
-    o = attention_video(qr, kr, v, a.heads)
-    _mark("msa.attention")
-    if a.to_gate_logits is not None:
-        gates = 2.0 * torch.sigmoid(a.to_gate_logits(norm_vx))
-        og = L.fused_head_gate_mul_bf16(o, gates, a.heads, o.shape[-1] // a.heads)
-        _mark("msa.head_gates")
+    o = o8 = gates = og = None
+    if fuse_out_quant and a.to_gate_logits is None and L._is_fp8_linear(a.to_out):
+        # the output projection without its bias (the residual gate adds it)
+        o8 = attention_video_e4m3_out(qr, kr, v, a.heads, a.to_out.input_scale)
+        _mark("msa.attention_e4m3")
+        proj = L.fp8_scaled_mm(o8.reshape(-1, o8.shape[-1]), a.to_out.weight, a.to_out.input_scale,
+                               a.to_out.weight_scale, None, out_dtype=vx.dtype).reshape(o8.shape[0], o8.shape[1], -1)
+        _mark("msa.out_linear")
     else:
-        gates, og = None, o
-    proj = L.fp8_linear_without_bias(a.to_out, og, out_dtype=og.dtype)
-    if proj is None:
-        raise RuntimeError("to_out is not an FP8 linear")
-    _mark("msa.quant_out_linear")
+        o = attention_video(qr, kr, v, a.heads)
+        _mark("msa.attention")
+        if a.to_gate_logits is not None:
+            gates = 2.0 * torch.sigmoid(a.to_gate_logits(norm_vx))
+            og = L.fused_head_gate_mul_bf16(o, gates, a.heads, o.shape[-1] // a.heads)
+            _mark("msa.head_gates")
+        else:
+            og = o
+        proj = L.fp8_linear_without_bias(a.to_out, og, out_dtype=og.dtype)
+        if proj is None:
+            raise RuntimeError("to_out is not an FP8 linear")
+        _mark("msa.quant_out_linear")
     nxt = None
     if next_adazero is not None:
         out, nxt = L.fused_residual_gate_adazero_from_ada(vx, proj, block.table, timesteps, gate_index=2,
@@ -228,7 +240,7 @@ def video_self_attention(block: VideoBlock, vx: torch.Tensor, timesteps: torch.T
         _mark("msa.residual_gate_bias")
     if stages is not None:
         for name, val in (("msa.x", vx), ("msa.norm", norm_vx), ("msa.norm_q8", norm_q8), ("msa.q", q), ("msa.k", k), ("msa.v", v),
-                          ("msa.qr", qr), ("msa.kr", kr), ("msa.attn", o), ("msa.gates", gates),
+                          ("msa.qr", qr), ("msa.kr", kr), ("msa.attn", o), ("msa.attn_q8", o8), ("msa.gates", gates),
                           ("msa.gated", og), ("msa.proj", proj), ("msa.out", out)):
             stages[name] = val
     return out if next_adazero is None else (out, nxt)
@@ -238,7 +250,8 @@ def video_text_cross_attention(block: VideoBlock, vx: torch.Tensor, context: tor
                                timesteps: torch.Tensor, prompt_timestep: torch.Tensor,
                                stages: Stages | None = None, *, fuse_norm: bool = False,
                                fuse_context: bool | None = None, fuse_ada_quant: bool = False,
-                               pre_norm: torch.Tensor | None = None, next_adazero: dict | None = None):
+                               pre_norm: torch.Tensor | None = None, next_adazero: dict | None = None,
+                               fuse_out_quant: bool = False):
     """:2810-2888 (cross_attention_adaln, production flags). rms_norm
     followed by the AdaLN affine of Ada rows 6/7 is AdaZero's composition
     (R(R(R(rms_norm(x)) R(1 + scale)) + shift)); with `fuse_norm` it runs as
@@ -252,8 +265,8 @@ def video_text_cross_attention(block: VideoBlock, vx: torch.Tensor, context: tor
     `fuse_ada_quant` (with `fuse_norm`) has that AdaZero pass write the
     q-projection's e4m3 input directly. `pre_norm` is that pass's output
     computed already (by the previous residual gate's fused pass: bf16 rows,
-    or e4m3 codes with `fuse_ada_quant`); `next_adazero` as in
-    `video_self_attention`."""
+    or e4m3 codes with `fuse_ada_quant`); `next_adazero` and
+    `fuse_out_quant` as in `video_self_attention`."""
     a = block.attn2
     b = vx.shape[0]
     if fuse_context is None:
@@ -299,10 +312,17 @@ def video_text_cross_attention(block: VideoBlock, vx: torch.Tensor, context: tor
     _mark("ca.k_rmsnorm")
     v = L.fp8_linear_forward(a.to_v, enc)
     _mark("ca.quant_v_linear")
-    o = attention_video(q, k, v, a.heads)
-    _mark("ca.attention")
-    ca = L.fp8_linear_forward(a.to_out, o)
-    _mark("ca.quant_out_linear")
+    o = o8 = None
+    if fuse_out_quant and L._is_fp8_linear(a.to_out):
+        o8 = attention_video_e4m3_out(q, k, v, a.heads, a.to_out.input_scale)
+        _mark("ca.attention_e4m3")
+        ca = L.fp8_linear_from_quantized_e4m3(a.to_out, o8, out_dtype=vx.dtype)
+        _mark("ca.out_linear")
+    else:
+        o = attention_video(q, k, v, a.heads)
+        _mark("ca.attention")
+        ca = L.fp8_linear_forward(a.to_out, o)
+        _mark("ca.quant_out_linear")
     nxt = None
     if next_adazero is not None:
         out, nxt = L.fused_residual_gate_adazero_from_ada(vx, ca, block.table, timesteps, gate_index=8,
@@ -314,7 +334,8 @@ def video_text_cross_attention(block: VideoBlock, vx: torch.Tensor, context: tor
     if stages is not None:
         for name, val in (("ca.x", vx), ("ca.enc", enc), ("ca.normed", normed), ("ca.in", attn_in),
                           ("ca.in_q8", attn_in_q8), ("ca.qp", qp),
-                          ("ca.kp", kp), ("ca.q", q), ("ca.k", k), ("ca.v", v), ("ca.attn", o), ("ca.proj", ca),
+                          ("ca.kp", kp), ("ca.q", q), ("ca.k", k), ("ca.v", v), ("ca.attn", o), ("ca.attn_q8", o8),
+                          ("ca.proj", ca),
                           ("ca.out", out)):
             stages[name] = val
     return out if next_adazero is None else (out, nxt)
@@ -375,7 +396,7 @@ def video_block_forward(block: VideoBlock, vx: torch.Tensor, context: torch.Tens
                         prompt_timestep: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, *,
                         fuse_gelu_quant: bool = False, qkv_grouped: bool = False, fuse_norm: bool = False,
                         fuse_ada_quant: bool = False, fuse_residual_ada: bool = False,
-                        stages: Stages | None = None) -> torch.Tensor:
+                        fuse_out_quant: bool = False, stages: Stages | None = None) -> torch.Tensor:
     """The video branches of one block: self-attention, text cross-attention,
     feed-forward (:2989-3298 without the audio and audio-video branches).
     vx (B, N, C) bf16; context (B, T, C) bf16; timesteps (B, N, 9C) or a
@@ -385,7 +406,10 @@ def video_block_forward(block: VideoBlock, vx: torch.Tensor, context: torch.Tens
     `fuse_residual_ada` runs each branch's residual gate together with the
     next branch's AdaZero pass (`fused_residual_gate_adazero_from_ada`): the
     self-attention's with the cross-attention's (which is an AdaZero pass
-    only with `fuse_norm`), the cross-attention's with the feed-forward's."""
+    only with `fuse_norm`), the cross-attention's with the feed-forward's.
+    `fuse_out_quant` has each attention write its output projection's e4m3
+    input (`attention_video_e4m3_out`; the self-attention's only without
+    head gates)."""
     ca_next = ff_next = None
     if fuse_residual_ada:
         if fuse_norm:
@@ -396,10 +420,11 @@ def video_block_forward(block: VideoBlock, vx: torch.Tensor, context: torch.Tens
         if fuse_ada_quant:
             ff_next["input_scale"] = block.ff_up.input_scale
     r = video_self_attention(block, vx, timesteps, cos, sin, stages, qkv_grouped=qkv_grouped,
-                             fuse_ada_quant=fuse_ada_quant, next_adazero=ca_next)
+                             fuse_ada_quant=fuse_ada_quant, next_adazero=ca_next, fuse_out_quant=fuse_out_quant)
     vx, pre_ca = r if ca_next is not None else (r, None)
     r = video_text_cross_attention(block, vx, context, timesteps, prompt_timestep, stages, fuse_norm=fuse_norm,
-                                   fuse_ada_quant=fuse_ada_quant, pre_norm=pre_ca, next_adazero=ff_next)
+                                   fuse_ada_quant=fuse_ada_quant, pre_norm=pre_ca, next_adazero=ff_next,
+                                   fuse_out_quant=fuse_out_quant)
     vx, pre_ff = r if ff_next is not None else (r, None)
     return video_feed_forward(block, vx, timesteps, fuse_gelu_quant=fuse_gelu_quant, fuse_ada_quant=fuse_ada_quant,
                               stages=stages, pre_norm=pre_ff)

@@ -104,7 +104,34 @@ struct AttnArgs {
   const float* q_ds;
   const float* k_ds;
   const float* v_ds;
+  // bf16 kernel and its merge: with oq set, the output goes to oq as the
+  // e4m3 codes of the FP8 linear that reads it, e4m3(clamp(R(o) * r, +-448))
+  // (o's strides, one byte per element; r = 1/scale in float32, and with
+  // oq_bf16, for a 0-dim scale, r and the product rounded to bf16: the
+  // input quantizer of that linear), instead of the bf16 o.
+  uint8_t* oq;
+  const float* oq_scale;
+  int oq_bf16;
 };
+
+// 8 bf16 output values (one 16-byte piece) as the e4m3 codes the input
+// quantizer of the following FP8 linear writes for them (rows.hip's Q8 path
+// and k_fp8_quant compute the same expression).
+OGA_DEVICE uint2 e4m3_of_bf16x8(const uint4& w, float r, bool rb) {
+  float f[8];
+  unpack8(w, f);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float v = f[i] * r;
+    if (rb) v = rbf(v);
+    f[i] = clamp448(v);
+  }
+  return make_uint2(e4m3x4(f[0], f[1], f[2], f[3]), e4m3x4(f[4], f[5], f[6], f[7]));
+}
+OGA_DEVICE float e4m3_recip(const AttnArgs& a) {
+  const float r = 1.0f / a.oq_scale[0];
+  return a.oq_bf16 ? rbf(r) : r;
+}
 
 OGA_DEVICE f32x16 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -274,6 +301,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   const int64_t q0 = (int64_t)qb * kQB + wv * 32;
   const int hl = lane >> 5;  // lane half
   const int ql = lane & 31;
+  // r of the e4m3 output (if any), read now: its load latency is then not
+  // paid after the last step
+  const float oq_r = a.oq ? e4m3_recip(a) : 0.0f;
 
   // Q^T fragments: step s covers d = 16s .. 16s+15; lane holds d = 16s + 8*hl .. +7
   // of query q0 + ql (queries past nq read the last query, never stored).
@@ -539,6 +569,17 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     }
   __syncthreads();
   const int oc = lane & 15;
+  if (a.oq) {  // e4m3 codes of R(o) for the FP8 linear that reads it
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int r = 4 * it + (lane >> 4);
+      const uint4 w = *(const uint4*)(otile + r * 256 + ((oc ^ (r & 15)) << 4));
+      const int64_t qr = q0 + r;
+      if (qr < a.nq)
+        *(uint2*)(a.oq + b * a.o_sb + qr * a.o_sn + (int64_t)h * a.o_sh + 8 * oc) = e4m3_of_bf16x8(w, oq_r, a.oq_bf16);
+    }
+    return;
+  }
 #pragma unroll
   for (int it = 0; it < 8; ++it) {
     const int r = 4 * it + (lane >> 4);
@@ -979,7 +1020,11 @@ __global__ __launch_bounds__(256) void k_attention_combine(AttnArgs a, int64_t r
   w.y = pack2(acc[2] * inv, acc[3] * inv);
   w.z = pack2(acc[4] * inv, acc[5] * inv);
   w.w = pack2(acc[6] * inv, acc[7] * inv);
-  *(uint4*)(a.o + b * a.o_sb + qi * a.o_sn + (int64_t)h * a.o_sh + 8 * c) = w;
+  const int64_t off = b * a.o_sb + qi * a.o_sn + (int64_t)h * a.o_sh + 8 * c;
+  if (a.oq)
+    *(uint2*)(a.oq + off) = e4m3_of_bf16x8(w, e4m3_recip(a), a.oq_bf16);
+  else
+    *(uint4*)(a.o + off) = w;
 }
 
 // out[b, n, h, d] = R(e4m3(x8[b, n, h, d]) * descale[b, h]); 16 values per
@@ -1092,10 +1137,12 @@ AttnPlan attention_plan(int64_t wgs, int64_t nk, int64_t slots) {
 }
 int64_t attention_ws_bytes(const AttnPlan& p, int qpb) { return p.units * qpb * (kAD + 2) * (int64_t)sizeof(float); }
 
+// oq_scale given: o is the e4m3 output of the quantizer with that scale
+// (AttnArgs::oq).
 int attention_run(const void* q, const int64_t q_strides[3], const void* k, const int64_t k_strides[3],
                   const void* v, const int64_t v_strides[3], void* o, const int64_t o_strides[3], int64_t batch,
                   int64_t nq, int64_t nk, int64_t heads, int64_t head_dim, float softmax_scale, void* workspace,
-                  int64_t workspace_bytes, void* stream) {
+                  int64_t workspace_bytes, void* stream, const float* oq_scale = nullptr, int oq_zero_dim = 0) {
   if (!q || !k || !v || !o || !q_strides || !k_strides || !v_strides || !o_strides) return fail("null pointer");
   if (head_dim != kAD) return unsupported("head_dim must be %d", kAD);
   if (batch < 0 || nq < 0 || nk < 0 || heads < 0) return fail("bad shape");
@@ -1111,7 +1158,14 @@ int attention_run(const void* q, const int64_t q_strides[3], const void* k, cons
   if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace)) return fail("bad workspace");
   if (workspace && !aligned(workspace, 16)) return fail("workspace must be 16-byte aligned");
   AttnArgs a{};
-  a.q = q; a.k = k; a.v = v; a.o = (uint16_t*)o;
+  a.q = q; a.k = k; a.v = v;
+  if (oq_scale) {
+    a.oq = (uint8_t*)o;
+    a.oq_scale = oq_scale;
+    a.oq_bf16 = oq_zero_dim ? 1 : 0;
+  } else {
+    a.o = (uint16_t*)o;
+  }
   a.q_sb = q_strides[0]; a.q_sn = q_strides[1]; a.q_sh = q_strides[2];
   a.k_sb = k_strides[0]; a.k_sn = k_strides[1]; a.k_sh = k_strides[2];
   a.v_sb = v_strides[0]; a.v_sn = v_strides[1]; a.v_sh = v_strides[2];
@@ -1247,6 +1301,17 @@ extern "C" int oga_attention_ws(const void* q, const int64_t q_strides[3], const
                                 float softmax_scale, void* workspace, int64_t workspace_bytes, void* stream) {
   return attention_run(q, q_strides, k, k_strides, v, v_strides, o, o_strides, batch, nq, nk, heads, head_dim,
                        softmax_scale, workspace, workspace_bytes, stream);
+}
+
+extern "C" int oga_attention_e4m3_out_ws(const void* q, const int64_t q_strides[3], const void* k,
+                                         const int64_t k_strides[3], const void* v, const int64_t v_strides[3],
+                                         void* o8, const int64_t o_strides[3], int64_t batch, int64_t nq, int64_t nk,
+                                         int64_t heads, int64_t head_dim, float softmax_scale,
+                                         const float* out_scale, int scale_zero_dim, void* workspace,
+                                         int64_t workspace_bytes, void* stream) {
+  if (!out_scale) return fail("null output scale");
+  return attention_run(q, q_strides, k, k_strides, v, v_strides, o8, o_strides, batch, nq, nk, heads, head_dim,
+                       softmax_scale, workspace, workspace_bytes, stream, out_scale, scale_zero_dim);
 }
 
 extern "C" int64_t oga_attention_fp8_workspace_bytes(int64_t batch, int64_t nq, int64_t nk, int64_t heads,

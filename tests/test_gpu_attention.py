@@ -404,3 +404,57 @@ def test_attention_config_shape():
         rms_rel = float(np.sqrt((err ** 2).mean()) / np.sqrt((ref ** 2).mean()))
         print(f"attention 1x9216x32x128 whole head {head}: worst/bound {worst:.3f} rms_rel {rms_rel:.3e}")
         assert worst <= 1.0 and rms_rel < 4e-3, (head, worst, rms_rel)
+
+
+@pytest.mark.parametrize("b,nq,nk,h", [(1, 300, 256, 4),     # few keys: the 4-wave form
+                                       (2, 200, 1536, 3),    # the 8-wave form
+                                       (1, 9216, 9216, 32),  # the configured shape: key-split last round
+                                       (1, 9216, 256, 32)])  # the text cross-attention's shape
+@pytest.mark.parametrize("zero_dim", [True, False])
+def test_attention_e4m3_out_is_the_quantized_attention(b, nq, nk, h, zero_dim):
+    """attention_video_e4m3_out: the codes the output projection's input
+    quantizer writes for the bf16 attention output, bit for bit, from one
+    pass: against `fused_fp8_quantize_e4m3(attention_video(...))` (the same
+    deterministic kernel, so the same bf16 output) and against the oracle's
+    quantizer applied to that bf16 output; the key-split merge included
+    (9216 queries x 32 heads leave a partial last round)."""
+    from opengenie_amd.attention import attention_video, attention_video_e4m3_out
+    from opengenie_amd.ltx_ops import fused_fp8_quantize_e4m3
+
+    q = randn((b, nq, h * 128), 700 + nq, std=2.0).to(DEV)
+    k = randn((b, nk, h * 128), 701 + nk, std=2.0).to(DEV)
+    v = randn((b, nk, h * 128), 702 + nk).to(DEV)
+    scale = 0.004
+    s = torch.tensor(scale, device=DEV) if zero_dim else torch.tensor([scale], device=DEV)
+    codes = attention_video_e4m3_out(q, k, v, h, s)
+    _ran("attention_video_e4m3_out")
+    o = attention_video(q, k, v, h)
+    ref = fused_fp8_quantize_e4m3(o, s)
+    torch.cuda.synchronize()
+    assert codes.dtype == torch.float8_e4m3fn and codes.shape == (b, nq, h * 128)
+    got = codes.view(torch.uint8).cpu().numpy()
+    assert np.array_equal(got, ref.view(torch.uint8).cpu().numpy())
+    rows = slice(0, min(nq, 600))  # the oracle's quantizer on part of the rows
+    want = O.fp8_quantize_e4m3(O.bf(np32(o[:, rows].cpu())), scale, zero_dim, device="cuda")
+    assert np.array_equal(got[:, rows], want.reshape(got[:, rows].shape))
+    if zero_dim:
+        assert (np.abs(np32(codes.float().cpu())) == 448).any()  # saturated tails
+
+
+def test_attention_e4m3_out_falls_back_to_the_two_calls(monkeypatch):
+    """A head size the kernel does not take runs attention then the
+    quantizer (torch's attention here); strict mode raises instead."""
+    from opengenie_amd import ltx_ops as L
+    from opengenie_amd.attention import attention_video, attention_video_e4m3_out
+
+    monkeypatch.delenv("OPENGENIE_AMD_STRICT", raising=False)
+    q, k, v = (randn((1, 64, 4 * 64), 720 + i).to(DEV) for i in range(3))
+    s = torch.tensor(0.01, device=DEV)
+    L.reset_hip_calls()
+    codes = attention_video_e4m3_out(q, k, v, 4, s)
+    assert L.collect_hip_calls().get("attention_video_e4m3_out", 0) == 0
+    ref = L.fused_fp8_quantize_e4m3(attention_video(q, k, v, 4), s)
+    assert torch.equal(codes.view(torch.uint8), ref.view(torch.uint8))
+    monkeypatch.setenv("OPENGENIE_AMD_STRICT", "1")
+    with pytest.raises(RuntimeError):
+        attention_video_e4m3_out(q, k, v, 4, s)

@@ -96,18 +96,21 @@ def _check_attn(got, ref, v, what):
     assert float((err / (2e-3 * vrms + 2e-2 * np.abs(ref))).max()) <= 1.0, what
 
 
-@pytest.mark.parametrize("gated,fused,ada_quant,res_ada", [(False, False, False, False), (True, True, False, False),
-                                                            (False, True, True, False), (False, True, True, True),
-                                                            (True, True, False, True)])
-def test_block_steps_match_oracle(gated, fused, ada_quant, res_ada):
+@pytest.mark.parametrize("gated,fused,ada_quant,res_ada,out_quant", [
+    (False, False, False, False, False), (True, True, False, False, False), (False, True, True, False, False),
+    (False, True, True, True, False), (True, True, False, True, True), (False, True, True, True, True)])
+def test_block_steps_match_oracle(gated, fused, ada_quant, res_ada, out_quant):
     """Every step of the slice against the oracle on that step's GPU inputs
     (the second case with the MI355X-side fusions: grouped Q/K/V, the
     cross-attention's rms_norm + AdaLN as one AdaZero, GELU in the
     down-projection's quantizer; the third, without head gates, also with
     each AdaZero that feeds an FP8 linear writing that linear's e4m3 input;
-    the last two also with each residual gate and the next branch's AdaZero
-    pass as one)."""
+    the fourth and fifth also with each residual gate and the next branch's
+    AdaZero pass as one; the last two also with each attention writing its
+    output projection's e4m3 input, the self-attention's only without head
+    gates)."""
     from opengenie_amd import ltx_ops as L
+    from opengenie_amd.attention import attention_video
     from opengenie_amd.block import Stages, random_video_block, video_block_forward
 
     blk = random_video_block(C, HEADS, seed=11 + gated + 2 * ada_quant + 4 * res_ada, gated=gated)
@@ -117,14 +120,18 @@ def test_block_steps_match_oracle(gated, fused, ada_quant, res_ada):
         ts = inputs[2][:, :1].to(DEV).expand(inputs[2].shape)
     st = Stages()
     out = video_block_forward(blk, vx, context, ts, pts, cos, sin, fuse_gelu_quant=fused, qkv_grouped=fused,
-                              fuse_norm=fused, fuse_ada_quant=ada_quant, fuse_residual_ada=res_ada, stages=st)
+                              fuse_norm=fused, fuse_ada_quant=ada_quant, fuse_residual_ada=res_ada,
+                              fuse_out_quant=out_quant, stages=st)
     torch.cuda.synchronize()
     assert out.shape == vx.shape and out.dtype == torch.bfloat16
     calls = L.collect_hip_calls()
-    for op in ("fp8_scaled_mm", "fused_video_qk_rmsnorm_rope", "flash_attn_func", "fused_residual_gate_from_ada"):
+    for op in ("fp8_scaled_mm", "fused_video_qk_rmsnorm_rope", "fused_residual_gate_from_ada"):
         assert calls.get(op, 0) > 0, (op, calls)
     assert calls.get("fused_residual_gate_bias_from_ada", 0) == (0 if res_ada else 1), calls
     assert calls.get("fused_residual_gate_adazero_from_ada", 0) == (2 if res_ada else 0), calls
+    msa_q8 = out_quant and not gated
+    assert calls.get("attention_video_e4m3_out", 0) == (int(msa_q8) + 1 if out_quant else 0), calls
+    assert calls.get("flash_attn_func", 0) + calls.get("attention_video_e4m3_out", 0) == 2, calls
     assert (calls.get("fp8_grouped_linear", 0) > 0) == fused, calls
     # one AdaLN-affine launch either way: the query affine (production flags)
     # or the context affine (with the fusions, where the query side is AdaZero)
@@ -149,11 +156,17 @@ def test_block_steps_match_oracle(gated, fused, ada_quant, res_ada):
                                      to_T(a1.k_norm_weight), EPS, to_T(cos), to_T(sin))
     assert_same_bits(np32(st["msa.qr"]), rq.v, "msa.qr")
     assert_same_bits(np32(st["msa.kr"]), rk.v, "msa.kr")
+    if msa_q8:  # the attention's bf16 output, by the same kernel, then its codes
+        st["msa.attn"] = attention_video(st["msa.qr"], st["msa.kr"], st["msa.v"], HEADS)
     _check_attn(st["msa.attn"], _attn_ref(st["msa.qr"], st["msa.kr"], st["msa.v"]), st["msa.v"], "msa.attn")
     if gated:
         ref = O.head_gate_mul(to_T(st["msa.attn"]), to_T(st["msa.gates"]), HEADS, C // HEADS)
         assert_same_bits(np32(st["msa.gated"]), ref.v, "msa.gated")
-    _check_linear(st["msa.proj"], _lin_ref(a1.to_out, to_T(st["msa.gated"]), bias=False), "msa.proj")
+    if msa_q8:
+        codes = _check_codes(st["msa.attn_q8"], to_T(st["msa.attn"]), a1.to_out, "msa.attn_q8")
+        _check_linear(st["msa.proj"], _lin_ref_codes(a1.to_out, codes, bias=False), "msa.proj")
+    else:
+        _check_linear(st["msa.proj"], _lin_ref(a1.to_out, to_T(st["msa.gated"]), bias=False), "msa.proj")
     ref = O.residual_gate_bias_from_ada(to_T(st["msa.x"]), to_T(st["msa.proj"]), to_T(a1.to_out.bias), tab, tsT, 2)
     assert_same_bits(np32(st["msa.out"]), ref.v, "msa.out")
 
@@ -180,8 +193,14 @@ def test_block_steps_match_oracle(gated, fused, ada_quant, res_ada):
             assert_same_bits(np32(st[f"ca.{nm}"]), nref.v, f"ca.{nm}")
         else:  # torch's rms_norm on the GPU: within one bf16 step
             assert (bf16_ulp_distance(np32(st[f"ca.{nm}"]), nref.v) <= 1).all(), f"ca.{nm}"
+    if out_quant:
+        st["ca.attn"] = attention_video(st["ca.q"], st["ca.k"], st["ca.v"], HEADS)
     _check_attn(st["ca.attn"], _attn_ref(st["ca.q"], st["ca.k"], st["ca.v"]), st["ca.v"], "ca.attn")
-    _check_linear(st["ca.proj"], _lin_ref(a2.to_out, to_T(st["ca.attn"])), "ca.proj")
+    if out_quant:
+        codes = _check_codes(st["ca.attn_q8"], to_T(st["ca.attn"]), a2.to_out, "ca.attn_q8")
+        _check_linear(st["ca.proj"], _lin_ref_codes(a2.to_out, codes), "ca.proj")
+    else:
+        _check_linear(st["ca.proj"], _lin_ref(a2.to_out, to_T(st["ca.attn"])), "ca.proj")
     ref = O.residual_gate_from_ada(to_T(st["ca.x"]), to_T(st["ca.proj"]), tab, tsT, 8)
     assert_same_bits(np32(st["ca.out"]), ref.v, "ca.out")
 
@@ -275,10 +294,12 @@ def test_block_end_to_end_against_oracle():
 
 @pytest.mark.parametrize("ada_quant", [False, True])
 def test_block_residual_ada_fusion_changes_no_bit(ada_quant):
-    """The residual gates fused with the next branch's AdaZero pass give the
-    slice's output bit for bit as the separate passes do (the fused pass is
-    their composition, and everything else is deterministic), at 2304 tokens
-    (several rows per wave of the fused pass)."""
+    """The residual gates fused with the next branch's AdaZero pass, and the
+    attentions writing their output projections' e4m3 inputs, give the
+    slice's output bit for bit as the separate passes do (each fused pass is
+    the composition of the passes it replaces, and everything else is
+    deterministic), at 2304 tokens (several rows per wave of the fused
+    residual pass)."""
     from opengenie_amd import ltx_ops as L
     from opengenie_amd.block import random_video_block, video_block_forward
 
@@ -294,6 +315,9 @@ def test_block_residual_ada_fusion_changes_no_bit(ada_quant):
     kw = dict(fuse_gelu_quant=True, qkv_grouped=True, fuse_norm=True, fuse_ada_quant=ada_quant)
     a = video_block_forward(blk, *args, **kw)
     b = video_block_forward(blk, *args, fuse_residual_ada=True, **kw)
+    c = video_block_forward(blk, *args, fuse_residual_ada=True, fuse_out_quant=True, **kw)
     torch.cuda.synchronize()
-    assert L.collect_hip_calls().get("fused_residual_gate_adazero_from_ada", 0) == 2
+    calls = L.collect_hip_calls()
+    assert calls.get("fused_residual_gate_adazero_from_ada", 0) == 4 and calls.get("attention_video_e4m3_out") == 2
     assert_same_bits(np32(b), np32(a), "block with and without the residual fusion")
+    assert_same_bits(np32(c), np32(a), "block with and without the attention's e4m3 output")
