@@ -743,6 +743,49 @@ def test_fp8_linear_split_k_through_c_abi(m, n, k):
     assert (bf16_ulp_distance(outs[0], outs[1]) > 1).mean() < 1e-3
 
 
+@pytest.mark.parametrize("m,n,k", [(4352, 4096, 4096), (256, 4096, 4096), (9216, 4096, 16384)])
+def test_fp8_linear_split_k_workspace_reuse(m, n, k):
+    """The split-K schedule keeps nothing in its workspace from one call to
+    the next: three calls on one workspace and one on a fresh workspace full
+    of garbage give identical bits (the chunk sums are taken in chunk order),
+    within the oracle's bar; 256 rows split every tile (no whole round), the
+    down-projection's tail splits K = 16384."""
+    from opengenie_amd import _lib
+
+    lib = _lib.load()
+    ws_bytes = int(lib.oga_fp8_linear_workspace_bytes(m, n, k))
+    assert ws_bytes > 0
+    x = randn((m, k), 380 + m, std=1.0)
+    sa = (x.float().abs().amax() / 448.0).reshape(())
+    a = torch.clamp(x.float() / sa, -448, 448).to(torch.float8_e4m3fn)
+    w, sb = _fp8_weights(n, k, 381 + n)
+    bias = randn((n,), 382, std=0.01)
+    ga, gw, gsa, gsb, gb = g(a), g(w), g(sa).float(), g(sb).float(), g(bias)
+    stream = torch.cuda.current_stream().cuda_stream
+    ws = torch.empty((ws_bytes // 4,), device="cuda", dtype=torch.float32)
+    outs = []
+    for call in range(4):
+        if call == 3:  # a fresh workspace full of garbage
+            ws = torch.full((ws_bytes // 4,), -7.0, device="cuda", dtype=torch.float32)
+        out = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
+        _lib.call("oga_fp8_linear_ws", ga.data_ptr(), k, gw.data_ptr(), k, gsa.data_ptr(), gsb.data_ptr(),
+                  gb.data_ptr(), _lib.DT_BF16, out.data_ptr(), n, m, n, k, ws.data_ptr(), ws_bytes, stream)
+        outs.append(out)
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16))
+    if m <= 4352:
+        ref = O.fp8_linear(a.view(torch.uint8).numpy(), w.view(torch.uint8).numpy(), float(sa), float(sb),
+                           to_T(bias))
+        got = out_np(outs[0])
+        close = np.isclose(got, ref, rtol=1e-2, atol=1e-3 * float(np.abs(ref).max()))
+        assert (~close).mean() < 1e-5 and (bf16_ulp_distance(got[~close], ref[~close]) <= 2).all()
+    else:  # the configured down-projection: every output against the device checker of the decoded codes
+        from tests.test_gpu_config_shapes import _device_fp8_linear, _linear_full_check
+
+        _linear_full_check(outs[0], _device_fp8_linear(ga, gw, gsa, gsb, gb), "down-projection, split tail")
+
+
 def _bias_epilogue_ref(out_nobias: np.ndarray, bias: torch.Tensor, r=bf16_round) -> np.ndarray:
     """R(out + R(bias)): the second rounding of the FP8 linear (:1705-1709),
     R the output dtype's rounding."""
