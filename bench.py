@@ -63,6 +63,8 @@ def _parse():
     ap.add_argument("--seed", type=int, default=20260100)
     ap.add_argument("--only", choices=["gemm", "quant", "fused", "copy", "attention", "linears", "block"], default=None,
                     help="run one workload --steps times and print its mean time (for profiler runs)")
+    ap.add_argument("--block-modes", default=",".join(BLOCK_MODES),
+                    help="with --only block: the comma-separated modes of the block slice to time")
     return ap.parse_args()
 
 
@@ -338,7 +340,11 @@ def _block_op_work(name: str, ctx_tokens: int) -> tuple[str, float] | None:
     return tab.get(name)
 
 
-def block_rows(seed: int, reps: int = 5, ctx_tokens: int = 256) -> dict:
+BLOCK_MODES = ("production_flags", "mi355x_fusions", "mi355x_fusions_ada_quant", "mi355x_fusions_residual_ada",
+               "mi355x_fusions_out_quant")
+
+
+def block_rows(seed: int, reps: int = 5, ctx_tokens: int = 256, modes: tuple[str, ...] = BLOCK_MODES) -> dict:
     """One video transformer-block slice at 9216 tokens (self-attention, text
     cross-attention over ctx_tokens text tokens, feed-forward; the production
     op order of opengenie_amd.block), random-init synthetic parameters of the
@@ -371,8 +377,6 @@ def block_rows(seed: int, reps: int = 5, ctx_tokens: int = 256) -> dict:
     sin = torch.randn((1, 32, M, 64), generator=g, device="cuda").clamp(-1, 1).to(torch.bfloat16)
     st = torch.cuda.current_stream()
     rows = {}
-    modes = ("production_flags", "mi355x_fusions", "mi355x_fusions_ada_quant", "mi355x_fusions_residual_ada",
-             "mi355x_fusions_out_quant")
 
     def run(key):
         # production flags; then the MI355X-side fusions (grouped Q/K/V,
@@ -755,7 +759,7 @@ def main() -> None:
         print(json.dumps(attention_rows(args.seed)))
         return
     if args.only == "block":
-        print(json.dumps(block_rows(args.seed)))
+        print(json.dumps(block_rows(args.seed, modes=tuple(args.block_modes.split(",")))))
         return
     if args.only == "linears":
         print(json.dumps(linear_rows(args.seed)))
