@@ -256,7 +256,9 @@ def video_text_cross_attention(block: VideoBlock, vx: torch.Tensor, context: tor
     followed by the AdaLN affine of Ada rows 6/7 is AdaZero's composition
     (R(R(R(rms_norm(x)) R(1 + scale)) + shift)); with `fuse_norm` it runs as
     one AdaZero pass instead of torch's rms_norm and the affine kernel.
-    `fuse_context` (default: `fuse_norm`) takes the reference's
+    With `fuse_norm` the K and V projections of the text tokens run as one
+    grouped FP8 GEMM when to_k and to_v share their input scale
+    (`fp8_kv_from_grouped_mm`). `fuse_context` (default: `fuse_norm`) takes the reference's
     _FUSE_VIDEO_TEXT_CONTEXT_ADALN path (:2839-2850, off in its production):
     the context affine of the prompt table's rows 0/1 as one AdaLN-affine
     launch, the same expression as the torch form beside it. With `fuse_norm`
@@ -304,14 +306,20 @@ def video_text_cross_attention(block: VideoBlock, vx: torch.Tensor, context: tor
     else:
         qp = L.fp8_linear_forward(a.to_q, attn_in)
         _mark("ca.quant_q_linear")
-    kp = L.fp8_linear_forward(a.to_k, enc)
-    _mark("ca.quant_k_linear")
+    kv = L.fp8_kv_from_grouped_mm(a, enc) if fuse_norm and enc.is_cuda else None
+    if kv is not None:  # K and V of the text tokens as one grouped GEMM
+        kp, v = kv
+        _mark("ca.quant_kv_grouped")
+    else:
+        kp = L.fp8_linear_forward(a.to_k, enc)
+        _mark("ca.quant_k_linear")
     q = qk_norm(qp, a.q_norm_weight, block.eps)
     _mark("ca.q_rmsnorm")
     k = qk_norm(kp, a.k_norm_weight, block.eps)
     _mark("ca.k_rmsnorm")
-    v = L.fp8_linear_forward(a.to_v, enc)
-    _mark("ca.quant_v_linear")
+    if kv is None:
+        v = L.fp8_linear_forward(a.to_v, enc)
+        _mark("ca.quant_v_linear")
     o = o8 = None
     if fuse_out_quant and L._is_fp8_linear(a.to_out):
         o8 = attention_video_e4m3_out(q, k, v, a.heads, a.to_out.input_scale)

@@ -54,6 +54,7 @@ __all__ = [
     "fp8_qkv_from_grouped_mm",
     "fp8_qkv_from_quantized_e4m3",
     "fp8_qk_from_grouped_mm",
+    "fp8_kv_from_grouped_mm",
     "fp8_qkv_from_packed_linear",
     "fp8_qkv_from_packed_requant",
     "collect_video_qkv_packed_linear_stats",
@@ -1444,6 +1445,23 @@ def fp8_qkv_from_quantized_e4m3(attn: torch.nn.Module, qinput: torch.Tensor, *, 
     if not _video_qkv_linears_ok(attn, qinput, ("to_q", "to_k", "to_v"), grouped=True):
         return None
     return _fp8_grouped_linear((attn.to_q, attn.to_k, attn.to_v), qinput, out_dtype)
+
+
+def fp8_kv_from_grouped_mm(attn: torch.nn.Module, context: torch.Tensor):
+    """The text cross-attention's K and V projections of the encoder states
+    (the attention module's to_k / to_v FP8Linears, :1691-1709 each, inside
+    the cross-attention's `attn(attn_input, context=...)`, :2880) as one
+    grouped FP8 GEMM when the
+    two linears share their input scale: one quantization (to_k's scale), one
+    launch over both linears' tiles, each with its own weight scale and bias.
+    No counterpart in the reference; the roundings are those of the two
+    forwards (R(R(acc * sa * sb_i) + R(bias_i))), only the float32 sum order
+    of a split tile's K-chunks may differ. None when the guard fails (the
+    caller then runs the two forwards)."""
+    if _grouped_guard_reason(attn, context, ("to_k", "to_v")) is not None:
+        return None
+    qinput = fused_fp8_quantize_e4m3(context.contiguous(), attn.to_k.input_scale)
+    return _fp8_grouped_linear((attn.to_k, attn.to_v), qinput, context.dtype)
 
 
 def fp8_qk_from_grouped_mm(attn: torch.nn.Module, x: torch.Tensor):

@@ -1156,3 +1156,33 @@ def test_fp8_linear_forward_module():
     q = O.fp8_quantize_e4m3(to_T(x), 0.0123, True, device="cuda").reshape(77, 256)
     ref = O.fp8_linear(q, w.view(torch.uint8).numpy(), 0.0123, float(sb), to_T(lin.bias.cpu()))
     np.testing.assert_allclose(out_np(out).reshape(77, 512), ref, rtol=1e-2, atol=1e-3 * float(np.abs(ref).max()))
+
+
+@pytest.mark.parametrize("tokens", [256, 77])
+def test_fp8_kv_grouped_mm_of_the_text_context(tokens):
+    """fp8_kv_from_grouped_mm: the text cross-attention's K and V projections
+    as one grouped launch, each against the oracle and against its own
+    FP8Linear forward (same roundings; only the float32 order of split
+    K-chunks may differ); None when the two input scales differ."""
+    from opengenie_amd import ltx_ops as L
+
+    attn = torch.nn.Module()
+    s_in = g(torch.tensor(0.0123))
+    attn.to_k = _FP8Lin(4096, 4096, 400, s_in)
+    attn.to_v = _FP8Lin(4096, 4096, 407, s_in)
+    ctx = g(randn((1, tokens, 4096), 410))
+    kv = L.fp8_kv_from_grouped_mm(attn, ctx)
+    _ran("fp8_grouped_linear")
+    assert kv is not None and len(kv) == 2
+    q = O.fp8_quantize_e4m3(to_T(ctx.cpu()), 0.0123, True, device="cuda").reshape(tokens, 4096)
+    for out, lin in zip(kv, (attn.to_k, attn.to_v)):
+        assert out.shape == (1, tokens, 4096) and out.dtype == torch.bfloat16
+        ref = O.fp8_linear(q, lin.weight.view(torch.uint8).cpu().numpy(), 0.0123, float(lin.weight_scale),
+                           to_T(lin.bias.cpu()))
+        got = out_np(out).reshape(tokens, 4096)
+        close = np.isclose(got, ref, rtol=1e-2, atol=1e-3 * float(np.abs(ref).max()))
+        assert (~close).mean() < 1e-5 and (bf16_ulp_distance(got[~close], ref[~close]) <= 2).all()
+        one = out_np(L.fp8_linear_forward(lin, ctx)).reshape(tokens, 4096)
+        assert (bf16_ulp_distance(got, one) > 1).mean() < 1e-3
+    attn.to_v.input_scale = g(torch.tensor(0.02))
+    assert L.fp8_kv_from_grouped_mm(attn, ctx) is None
