@@ -499,6 +499,14 @@ def attention_rows(seed: int, reps: int = 10) -> dict:
                                             "rms_over_ref_rms": round(float(diff.square().mean().sqrt() /
                                                                             ref.square().mean().sqrt()), 4),
                                             "mean_rel": round(float((diff / ref.abs().clamp_min(1e-6)).mean()), 4)}}
+    # the text cross-attention's shape: 9216 video queries over 256 text keys
+    kt, vt = (torch.randn((1, 256, ATT_H, ATT_D), generator=g, device="cuda").to(torch.bfloat16) for _ in range(2))
+    flops_t = 4.0 * ATT_N * 256 * ATT_H * ATT_D
+    us_t = timed(lambda: A.flash_attn_func(q, kt, vt))
+    rows["bf16_256_keys"] = {"shape": "q [1,9216,32,128], k,v [1,256,32,128]", "us": round(us_t, 1),
+                             "TFLOP/s": round(flops_t / (us_t * 1e-6) / 1e12, 1),
+                             "frac_bf16_peak": round(flops_t / (us_t * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                             "hbm_GB/s": round((2 * q.numel() + 2 * kt.numel()) * 2 / (us_t * 1e-6) / 1e9, 1)}
     return rows
 
 

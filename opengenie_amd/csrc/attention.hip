@@ -589,6 +589,242 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   }
 }
 
+// ------------------------------------------------- few keys (text tokens)
+// At most kFewKeys keys (the text cross-attention's 256): the whole K and V
+// of a (batch, head) stay in LDS (4 tile pairs, 128 KiB, the swizzled layout
+// of k_attention) for the workgroup's life. A workgroup of kFewW waves takes
+// one (batch, head) and a range of its 32-query groups; after one barrier
+// (K/V landed) each wave runs its groups on its own, with no further
+// barrier: Q^T fragments from HBM, the key steps of k_attention against the
+// resident tiles (S^T, online softmax, P.V), the output through the wave's
+// own 4 KiB of staging in two 16-row passes. The two waves of a SIMD cover
+// each other's Q loads and stores. (k_attention re-fetched K/V per block of
+// queries and ran each block's Q loads, key steps and stores in lockstep
+// across its workgroup, so the per-block fixed cost dominated at 4 steps.)
+constexpr int kFewKeys = 256;                        // 4 steps of 64 keys
+constexpr int kFewSteps = kFewKeys / kAK;
+constexpr int kFewW = 8;                             // waves per workgroup (two per SIMD)
+constexpr int kFewStage = kFewSteps * kParBytes;     // staging after the tiles: 128 KiB
+constexpr int kFewStageWave = 4096;                  // 16 rows x 256 bytes
+static_assert(kFewStage + kFewW * kFewStageWave <= 160 * 1024, "LDS budget");
+
+__global__ __launch_bounds__(64 * kFewW) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attention_fewkeys(
+    AttnArgs a, int slices) {
+  constexpr int kDI = 16 / kFewW;  // DMA instructions per wave per tile
+  __shared__ uint4 smem[(kFewStage + kFewW * kFewStageWave) / 16];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int hl = lane >> 5, ql = lane & 31, hl4 = 4 * hl;
+  // The eight XCDs receive workgroups round-robin (XCD = blockIdx.x % 8):
+  // renumbered so that each XCD's workgroups are consecutive, the slices of a
+  // head share one XCD and its L2 holds the head's K/V for all of them.
+  const uint32_t xcd = blockIdx.x & 7, per = gridDim.x >> 3, extra = gridDim.x & 7;
+  const int64_t wg = (int64_t)xcd * per + min(xcd, extra) + (blockIdx.x >> 3);
+  const int64_t bh = wg / slices;
+  const int slice = (int)(wg % slices);
+  const int h = (int)(bh % a.heads);
+  const int64_t b = bh / a.heads;
+  const int64_t ngroups = (a.nq + 31) / 32;
+  const int64_t g_begin = ngroups * slice / slices, g_end = ngroups * (slice + 1) / slices;
+  const int nsteps = (int)((a.nk + kAK - 1) / kAK);  // 1 .. kFewSteps
+  const float oq_r = a.oq ? e4m3_recip(a) : 0.0f;
+
+  // K and V of the head into the tile pairs, once.
+  const uint16_t* kbase = (const uint16_t*)a.k + b * a.k_sb + (int64_t)h * a.k_sh;
+  const uint16_t* vbase = (const uint16_t*)a.v + b * a.v_sb + (int64_t)h * a.v_sh;
+  for (int st = 0; st < nsteps; ++st) {
+    const int64_t key0 = (int64_t)st * kAK;
+    const bool clamp = key0 + kAK > a.nk;
+    const TileSrc<kDI> ks = tile_src<kDI>(a.k_sn, key0, a.nk, wv, lane, clamp);
+    const TileSrc<kDI> vs = tile_src<kDI>(a.v_sn, key0, a.nk, wv, lane, clamp);
+    tile_dma<kDI>((const char*)(kbase + key0 * a.k_sn), ks, smem + 2 * st * kATileU4, wv);
+    tile_dma<kDI>((const char*)(vbase + key0 * a.v_sn), vs, smem + (2 * st + 1) * kATileU4, wv);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  asm volatile("s_barrier" ::: "memory");
+
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
+  uint32_t kaddr[8], vaddr[4][2];
+  {
+    const int x = hl ^ swz(ql & 15);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) kaddr[s] = lds0 + ql * 256 + (((2 * s) ^ x) << 4);
+    const int a4 = lane & 3, j4 = (lane & 15) >> 2, g2 = (lane >> 4) & 1;
+#pragma unroll
+    for (int dblk = 0; dblk < 4; ++dblk)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        vaddr[dblk][u] = lds0 + kVBuf + (4 * hl + j4) * 256 +
+                         ((4 * (dblk ^ j4) + ((2 * g2 + (a4 >> 1)) ^ (2 * u + hl))) << 4) + (a4 & 1) * 8;
+  }
+  char* const stage = (char*)smem + kFewStage + wv * kFewStageWave;
+
+  for (int64_t grp = g_begin + wv; grp < g_end; grp += kFewW) {
+    const int64_t q0 = grp * 32;
+    bf16x8 qf[8];
+    {
+      const int64_t qi = min(q0 + ql, a.nq - 1);
+      const uint16_t* qrow = (const uint16_t*)a.q + b * a.q_sb + qi * a.q_sn + (int64_t)h * a.q_sh;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) qf[s] = __builtin_bit_cast(bf16x8, *(const uint4*)(qrow + 16 * s + 8 * hl));
+    }
+    f32x16 o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[i][e] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    // One key step against resident pair ST (k_attention's s_phase,
+    // softmax and pv_phase).
+    auto step = [&](auto st_c) {
+      constexpr int ST = decltype(st_c)::value;
+      constexpr int KB = ST * kParBytes + kKBuf;
+      f32x16 sacc[2];
+      auto s_block = [&](auto j_c) {
+        constexpr int OFF = KB + 8192 * decltype(j_c)::value;
+        bf16x8 kf[8];
+        kf[0] = lds_b128<OFF>(kaddr[0]);
+        kf[1] = lds_b128<OFF>(kaddr[1]);
+        kf[2] = lds_b128<OFF>(kaddr[2]);
+        kf[3] = lds_b128<OFF>(kaddr[3]);
+        kf[4] = lds_b128<OFF>(kaddr[4]);
+        kf[5] = lds_b128<OFF>(kaddr[5]);
+        kf[6] = lds_b128<OFF>(kaddr[6]);
+        kf[7] = lds_b128<OFF>(kaddr[7]);
+        OGA_LGKM(0, "+v"(kf[0]), "+v"(kf[1]), "+v"(kf[2]), "+v"(kf[3]), "+v"(kf[4]), "+v"(kf[5]), "+v"(kf[6]),
+                 "+v"(kf[7]));
+        f32x16 acc;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) acc = mfma_bf16(kf[s], qf[s], acc);
+        return acc;
+      };
+      sacc[0] = s_block(IC<0>{});
+      sacc[1] = s_block(IC<1>{});
+      auto read_v = [&](auto c_c, u32x2(&vr)[8]) {
+        constexpr int OFF = ST * kParBytes + 4096 * decltype(c_c)::value;  // vaddr includes kVBuf
+        vr[0] = lds_tr16<OFF>(vaddr[0][0]);
+        vr[1] = lds_tr16<OFF + 2048>(vaddr[0][1]);
+        vr[2] = lds_tr16<OFF>(vaddr[1][0]);
+        vr[3] = lds_tr16<OFF + 2048>(vaddr[1][1]);
+        vr[4] = lds_tr16<OFF>(vaddr[2][0]);
+        vr[5] = lds_tr16<OFF + 2048>(vaddr[2][1]);
+        vr[6] = lds_tr16<OFF>(vaddr[3][0]);
+        vr[7] = lds_tr16<OFF + 2048>(vaddr[3][1]);
+      };
+      u32x2 vr0[8], vr1[8];
+      read_v(IC<0>{}, vr0);  // in flight under the softmax
+      // softmax: keys past nk score -inf; the running max moves lazily
+      const int64_t rem64 = a.nk - (int64_t)ST * kAK;
+      if (rem64 < kAK) {
+        int remh = (int)rem64 - hl4;
+        asm volatile("" : "+v"(remh));  // compares here, not 32 lane masks hoisted out of the loop
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            if (32 * j + 8 * (e >> 2) + (e & 3) >= remh) sacc[j][e] = -INFINITY;
+      }
+      float mx = sacc[0][0];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = (j == 0 ? 1 : 0); e < 16; ++e) mx = __builtin_fmaxf(mx, sacc[j][e]);
+      const float ms = max_halves(mx) * a.scale_log2;
+      if (__any(ms > m_run + 8.0f)) {
+        const float m_new = __builtin_fmaxf(m_run, ms);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run *= alpha;
+        m_run = m_new;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
+      }
+      const float nm = -m_run;
+      float ps0 = 0.0f, ps1 = 0.0f;
+      uint32_t pb[2][8];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j][e], a.scale_log2, nm));
+          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j][e + 1], a.scale_log2, nm));
+          ps0 += p0;
+          ps1 += p1;
+          pb[j][e >> 1] = pack2(p0, p1);
+        }
+      l_run += ps0 + ps1;
+      auto pv = [&](auto c_c, u32x2(&cur)[8], u32x2(&nxt)[8]) {
+        constexpr int C = decltype(c_c)::value;
+        if constexpr (C + 1 < 4) {
+          read_v(IC<C + 1>{}, nxt);
+          OGA_LGKM(8, "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3]), "+v"(cur[4]), "+v"(cur[5]),
+                   "+v"(cur[6]), "+v"(cur[7]));
+        } else {
+          OGA_LGKM(0, "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3]), "+v"(cur[4]), "+v"(cur[5]),
+                   "+v"(cur[6]), "+v"(cur[7]));
+        }
+        const uint32_t* pw = &pb[C >> 1][4 * (C & 1)];
+        const uint4 pu = {pw[0], pw[1], pw[2], pw[3]};
+        const bf16x8 pf = __builtin_bit_cast(bf16x8, pu);
+#pragma unroll
+        for (int dblk = 0; dblk < 4; ++dblk) {
+          const uint4 vu = {cur[2 * dblk][0], cur[2 * dblk][1], cur[2 * dblk + 1][0], cur[2 * dblk + 1][1]};
+          o[dblk] = mfma_bf16(__builtin_bit_cast(bf16x8, vu), pf, o[dblk]);
+        }
+      };
+      pv(IC<0>{}, vr0, vr1);
+      pv(IC<1>{}, vr1, vr0);
+      pv(IC<2>{}, vr0, vr1);
+      pv(IC<3>{}, vr1, vr0);
+    };
+    step(IC<0>{});
+    if (nsteps > 1) step(IC<1>{});
+    if (nsteps > 2) step(IC<2>{});
+    if (nsteps > 3) step(IC<3>{});
+
+    // O = O^T / l through the wave's staging, 16 query rows per pass: lanes
+    // of rows 16p .. 16p+15 write their 256-byte rows (16-byte chunk c of
+    // row r at chunk c ^ r), then the wave stores four whole rows per
+    // instruction.
+    const float inv = 1.0f / sum_halves(l_run);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      if ((ql >> 4) == p) {
+        const int r = ql & 15;
+#pragma unroll
+        for (int dblk = 0; dblk < 4; ++dblk)
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) {
+            uint2 w;
+            w.x = pack2(o[dblk][4 * gq] * inv, o[dblk][4 * gq + 1] * inv);
+            w.y = pack2(o[dblk][4 * gq + 2] * inv, o[dblk][4 * gq + 3] * inv);
+            *(uint2*)(stage + r * 256 + (((4 * dblk + gq) ^ r) << 4) + 8 * hl) = w;
+          }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      const int oc = lane & 15;
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int r = 4 * it + (lane >> 4);
+        const uint4 w = *(const uint4*)(stage + r * 256 + ((oc ^ r) << 4));
+        const int64_t qr = q0 + 16 * p + r;
+        if (qr < a.nq) {
+          const int64_t off = b * a.o_sb + qr * a.o_sn + (int64_t)h * a.o_sh + 8 * oc;
+          if (a.oq)
+            *(uint2*)(a.oq + off) = e4m3_of_bf16x8(w, oq_r, a.oq_bf16);
+          else
+            *(uint4*)(a.o + off) = w;
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the staging reads, before the next pass writes
+    }
+  }
+}
+
 // ------------------------------------------------------- FP8 attention
 // FlashAttention-3's FP8 path, as the reference calls it with per-head e4m3
 // q, k, v and their [B, H] descales (official_ltx23_benchmark.py:3330-3340):
@@ -1172,6 +1408,17 @@ int attention_run(const void* q, const int64_t q_strides[3], const void* k, cons
   a.o_sb = o_strides[0]; a.o_sn = o_strides[1]; a.o_sh = o_strides[2];
   a.nq = nq; a.nk = nk; a.heads = (int)heads;
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
+  if (nk <= kFewKeys) {  // K/V of a head resident in LDS, no workspace
+    const int64_t bhs = batch * heads;
+    const int64_t groups = (nq + 31) / 32;
+    int64_t slices = (int64_t)cu_count() / bhs;
+    if (slices < 1) slices = 1;
+    if (slices > groups) slices = groups;
+    if (bhs * slices > (int64_t)UINT32_MAX || slices > INT32_MAX) return unsupported("too many query groups");
+    hipLaunchKernelGGL(k_attention_fewkeys, dim3((unsigned)(bhs * slices)), dim3(64 * kFewW), 0,
+                       (hipStream_t)stream, a, (int)slices);
+    return launch_status();
+  }
   const AttnKernel kern = bf16_kernel(nk);
   const AttnCfg cfg = attn_cfg(kern);
   const int64_t nqb = (nq + cfg.qpb - 1) / cfg.qpb;

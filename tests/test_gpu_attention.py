@@ -458,3 +458,30 @@ def test_attention_e4m3_out_falls_back_to_the_two_calls(monkeypatch):
     monkeypatch.setenv("OPENGENIE_AMD_STRICT", "1")
     with pytest.raises(RuntimeError):
         attention_video_e4m3_out(q, k, v, 4, s)
+
+
+@pytest.mark.parametrize("b,nq,nk,h", [(1, 1, 1, 1), (2, 31, 33, 3), (1, 33, 64, 2), (2, 1000, 65, 3),
+                                       (1, 700, 200, 4), (1, 4096, 256, 32), (3, 97, 256, 1)])
+def test_attention_few_keys_resident_kernel(b, nq, nk, h):
+    """Up to 256 keys the K and V of a head stay in LDS for the workgroup's
+    life and each wave runs its 32-query groups on its own: partial key
+    tiles (1, 33, 65, 200 keys), partial query groups, one query, several
+    batches and heads, grids of fewer than 8 and of no multiple of 8
+    workgroups (the XCD-contiguous numbering); against the oracle, and the
+    e4m3 output against the quantizer on the bf16 output."""
+    from opengenie_amd.attention import attention_video, attention_video_e4m3_out, flash_attn_func
+    from opengenie_amd.ltx_ops import fused_fp8_quantize_e4m3
+
+    q = randn((b, nq, h, 128), 960 + nq)
+    k = randn((b, nk, h, 128), 961 + nk)
+    v = randn((b, nk, h, 128), 962 + nk)
+    out = flash_attn_func(q.to(DEV), k.to(DEV), v.to(DEV))
+    _ran("flash_attn_func")
+    _check(out, _ref(q, k, v), f"few keys b{b} nq{nq} nk{nk} h{h}")
+    qf, kf, vf = (t.reshape(b, t.shape[1], h * 128).to(DEV) for t in (q, k, v))
+    s = torch.tensor(0.01, device=DEV)
+    codes = attention_video_e4m3_out(qf, kf, vf, h, s)
+    ref = fused_fp8_quantize_e4m3(attention_video(qf, kf, vf, h), s)
+    torch.cuda.synchronize()
+    assert torch.equal(codes.view(torch.uint8), ref.view(torch.uint8))
+    assert torch.equal(out.reshape(b, nq, h * 128).view(torch.int16), attention_video(qf, kf, vf, h).view(torch.int16))
