@@ -447,15 +447,15 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
     }
     const float nm = -m_run;
-    float ps0 = 0.0f, ps1 = 0.0f;
+    float ps0, ps1;  // from the first terms (P >= 0 is never -0: 0 + x would be x)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int e = 0; e < 16; e += 2) {
         const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j][e], a.scale_log2, nm));
         const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j][e + 1], a.scale_log2, nm));
-        ps0 += p0;
-        ps1 += p1;
+        ps0 = (j == 0 && e == 0) ? p0 : ps0 + p0;
+        ps1 = (j == 0 && e == 0) ? p1 : ps1 + p1;
         pb[j][e >> 1] = pack2(p0, p1);
       }
     l_run += ps0 + ps1;
@@ -744,7 +744,7 @@ __global__ __launch_bounds__(64 * kFewW) __attribute__((amdgpu_waves_per_eu(2, 2
           for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
       }
       const float nm = -m_run;
-      float ps0 = 0.0f, ps1 = 0.0f;
+      float ps0, ps1;  // from the first terms (P >= 0 is never -0: 0 + x would be x)
       uint32_t pb[2][8];
 #pragma unroll
       for (int j = 0; j < 2; ++j)
@@ -752,8 +752,8 @@ __global__ __launch_bounds__(64 * kFewW) __attribute__((amdgpu_waves_per_eu(2, 2
         for (int e = 0; e < 16; e += 2) {
           const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j][e], a.scale_log2, nm));
           const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j][e + 1], a.scale_log2, nm));
-          ps0 += p0;
-          ps1 += p1;
+          ps0 = (j == 0 && e == 0) ? p0 : ps0 + p0;
+          ps1 = (j == 0 && e == 0) ? p1 : ps1 + p1;
           pb[j][e >> 1] = pack2(p0, p1);
         }
       l_run += ps0 + ps1;
@@ -1080,7 +1080,9 @@ __global__ __launch_bounds__(64 * kF8W) __attribute__((amdgpu_waves_per_eu(kF8W 
         for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
     }
     const float nm = kF8Offset - m_run;
-    float ps0 = 0.0f, ps1 = 0.0f;
+    // (the sums start from their first term: P >= 0 is never -0, so 0 + x,
+    // which the compiler may not drop, would be x)
+    float ps0, ps1;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -1089,9 +1091,14 @@ __global__ __launch_bounds__(64 * kF8W) __attribute__((amdgpu_waves_per_eu(kF8W 
         const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j][e + 1], sl2, nm));
         const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j][e + 2], sl2, nm));
         const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j][e + 3], sl2, nm));
-        ps0 += p0 + p2;
-        ps1 += p1 + p3;
-        pf[4 * j + (e >> 2)] = (int)e4m3x4(p0, p1, p2, p3);
+        if (j == 0 && e == 0) {
+          ps0 = p0 + p2;
+          ps1 = p1 + p3;
+        } else {
+          ps0 += p0 + p2;
+          ps1 += p1 + p3;
+        }
+        pf[4 * j + (e >> 2)] = (int)e4m3x4_valu(p0, p1, p2, p3);
       }
     l_run += ps0 + ps1;
   };

@@ -276,6 +276,21 @@ OGA_DEVICE uint32_t e4m3x4(float a, float b, float c, float d) {
   return (uint32_t)w;
 }
 
+// e4m3x4 without the zero the builtin's first conversion starts from: that
+// conversion writes the low half and its high half is overwritten by the
+// second, so the first goes through inline assembly with an output-only
+// destination (no v_mov of a zero per word). Its leading s_nop 0 is the one
+// wait state a VALU read of a transcendental's result needs on gfx950, which
+// the compiler inserts for its own instructions but not before inline
+// assembly. For VALU-computed inputs only (an MFMA result needs more wait
+// states).
+OGA_DEVICE uint32_t e4m3x4_valu(float a, float b, float c, float d) {
+  int w;
+  asm("s_nop 0\n\tv_cvt_pk_fp8_f32 %0, %1, %2" : "=v"(w) : "v"(a), "v"(b));
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (uint32_t)w;
+}
+
 // clamp(v, -448, 448) that keeps NaN (torch.clamp propagates NaN).
 OGA_DEVICE float clamp448(float v) {
   float c = fminf(fmaxf(v, -448.0f), 448.0f);

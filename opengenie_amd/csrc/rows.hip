@@ -758,7 +758,7 @@ __global__ __launch_bounds__(64 * ada_waves<RES>()) void k_adazero_rows(RowArgs 
           }
         }
         typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-        const u32x2 o = {e4m3x4(qv[0], qv[1], qv[2], qv[3]), e4m3x4(qv[4], qv[5], qv[6], qv[7])};
+        const u32x2 o = {e4m3x4_valu(qv[0], qv[1], qv[2], qv[3]), e4m3x4_valu(qv[4], qv[5], qv[6], qv[7])};
         __builtin_nontemporal_store(o, (u32x2*)(qb + t * C + j * 512));
       } else {
         st_nt16(yb + t * C + j * 512, make_uint4(ow[0], ow[1], ow[2], ow[3]));
