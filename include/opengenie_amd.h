@@ -303,6 +303,10 @@ int oga_fp8_linear_dt_ws(const void* a, int64_t lda, const void* w, int64_t ldw,
  * given by element strides (batch, token, head) with unit stride along D
  * (multiples of 8, 16-byte aligned bases). o = softmax(q k^T * scale) v with
  * float32 softmax and accumulation, P rounded to bf16 before the P.V product.
+ * Up to 256 keys (the text cross-attention's prompt) each head's K and V stay
+ * in LDS while a workgroup runs a range of its 32-query groups; the result
+ * is bit for bit the streaming kernel's (the same key steps in the same
+ * order).
  */
 int oga_attention(const void* q, const int64_t q_strides[3], const void* k, const int64_t k_strides[3],
                   const void* v, const int64_t v_strides[3], void* o, const int64_t o_strides[3], int64_t batch,
