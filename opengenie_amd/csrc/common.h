@@ -38,18 +38,17 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 OGA_DEVICE float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 OGA_DEVICE float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
-// Round a float to the nearest bf16 (ties to even) and return it as float.
-OGA_DEVICE float rbf(float v) {
-  __bf16 b = (__bf16)v;
-  return (float)b;
-}
-
 // Pack two floats (already bf16 values or not) into two bf16 with RNE.
 OGA_DEVICE uint32_t pack_bf16(float lo, float hi) {
   f32x2 v = {lo, hi};
   bf16x2 b = __builtin_convertvector(v, bf16x2);
   return __builtin_bit_cast(uint32_t, b);
 }
+
+// Round a float to the nearest bf16 (ties to even) and return it as float:
+// one v_cvt_pk_bf16_f32 with +0 in the low half, whose 32 bits are then the
+// float of the bf16 value (NaN and infinities included), no shift.
+OGA_DEVICE float rbf(float v) { return __uint_as_float(pack_bf16(0.0f, v)); }
 
 // 8 bf16 <-> 8 floats
 OGA_DEVICE void unpack8(const uint4& u, float* f) {

@@ -190,6 +190,9 @@ __global__ __launch_bounds__(256) void k_elem(RowArgs a) {
         }
       }
     }
+    // Every load of the group issued before any use (the scheduler may
+    // otherwise sink one into the arithmetic, which then waits for it alone).
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t t = t0 + u;
@@ -727,41 +730,29 @@ __global__ __launch_bounds__(64 * ada_waves<RES>()) void k_adazero_rows(RowArgs 
           v1[i] = B1 ? rbf(fv) : fv;
         }
       }
-      uint32_t ow[4];
+      // y = R(R(R(x * inv) * (1 + scale)) + shift) per value (the middle
+      // rounding with a bf16 table); each intermediate R as one conversion
+      // that leaves the float (rbf), the output packed in pairs.
+      float pv[8];
 #pragma unroll
-      for (int i = 0; i < 8; i += 2) {
-        const uint32_t n = pack_bf16(f[j][i] * inv, f[j][i + 1] * inv);
-        float pa = bf16_lo(n) * v1[i], pb = bf16_hi(n) * v1[i + 1];
-        if constexpr (B1) {
-          const uint32_t p = pack_bf16(pa, pb);
-          pa = bf16_lo(p);
-          pb = bf16_hi(p);
-        }
-        ow[i / 2] = pack_bf16(pa + v0[i], pb + v0[i + 1]);
+      for (int i = 0; i < 8; ++i) {
+        const float p = rbf(f[j][i] * inv) * v1[i];
+        pv[i] = (B1 ? rbf(p) : p) + v0[i];
       }
       if constexpr (Q8 != Q8_NONE) {
         float qv[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float lo = bf16_lo(ow[i]) * qr, hi = bf16_hi(ow[i]) * qr;
-          if constexpr (Q8 == Q8_BF16) {  // both rounded by one conversion
-            const uint32_t pq = pack_bf16(lo, hi);
-            lo = bf16_lo(pq);
-            hi = bf16_hi(pq);
-          }
-          if constexpr (CLEAN) {
-            qv[2 * i] = __builtin_amdgcn_fmed3f(lo, -448.0f, 448.0f);
-            qv[2 * i + 1] = __builtin_amdgcn_fmed3f(hi, -448.0f, 448.0f);
-          } else {
-            qv[2 * i] = clamp448(lo);
-            qv[2 * i + 1] = clamp448(hi);
-          }
+        for (int i = 0; i < 8; ++i) {
+          float q = rbf(pv[i]) * qr;
+          if constexpr (Q8 == Q8_BF16) q = rbf(q);
+          qv[i] = CLEAN ? __builtin_amdgcn_fmed3f(q, -448.0f, 448.0f) : clamp448(q);
         }
         typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
         const u32x2 o = {e4m3x4_valu(qv[0], qv[1], qv[2], qv[3]), e4m3x4_valu(qv[4], qv[5], qv[6], qv[7])};
         __builtin_nontemporal_store(o, (u32x2*)(qb + t * C + j * 512));
       } else {
-        st_nt16(yb + t * C + j * 512, make_uint4(ow[0], ow[1], ow[2], ow[3]));
+        st_nt16(yb + t * C + j * 512, make_uint4(pack_bf16(pv[0], pv[1]), pack_bf16(pv[2], pv[3]),
+                                                 pack_bf16(pv[4], pv[5]), pack_bf16(pv[6], pv[7])));
       }
     }
     };
