@@ -461,7 +461,9 @@ def test_attention_e4m3_out_falls_back_to_the_two_calls(monkeypatch):
 
 
 @pytest.mark.parametrize("b,nq,nk,h", [(1, 1, 1, 1), (2, 31, 33, 3), (1, 33, 64, 2), (2, 1000, 65, 3),
-                                       (1, 700, 200, 4), (1, 4096, 256, 32), (3, 97, 256, 1)])
+                                       (1, 700, 200, 4), (1, 4096, 256, 32), (3, 97, 256, 1),
+                                       # more (batch, head) pairs than CUs: one workgroup each
+                                       (3, 70, 100, 100)])
 def test_attention_few_keys_resident_kernel(b, nq, nk, h):
     """Up to 256 keys the K and V of a head stay in LDS for the workgroup's
     life and each wave runs its 32-query groups on its own: partial key
