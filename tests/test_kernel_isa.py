@@ -4,7 +4,8 @@ reliably (CPU only: hipcc cross-compiles, nothing is launched).
 The attention kernel fills LDS with global_load_lds (DMA counted by vmcnt)
 and reads it with inline-assembly ds_read instructions after a workgroup
 barrier. Nothing at the barrier waits for loads by itself, so each barrier
-must be preceded, in its own basic block, by an explicit s_waitcnt vmcnt(n)
+must be preceded, in its own basic block or one that falls through into it,
+by an explicit s_waitcnt vmcnt(n)
 with no LDS DMA issued between that wait and the barrier; otherwise a wave
 may read a tile before its DMA has landed, a timing-dependent error in the
 attention output. n may leave the DMA of the next step in flight (the K and
@@ -54,7 +55,11 @@ def _kernel_body(asm: str, kernel_substr: str) -> list[str]:
 
 def barrier_violations(body: list[str], max_vmcnt: int = 0) -> list[int]:
     """Indexes of s_barrier instructions not preceded, within their basic
-    block, by s_waitcnt vmcnt(n <= max_vmcnt) with no LDS DMA after it."""
+    block or the blocks that fall through into it, by s_waitcnt
+    vmcnt(n <= max_vmcnt) with no LDS DMA after it. A block without a label
+    is entered only by falling through, so the scan goes on past the
+    conditional branch that ends the block before it; a label (a jump
+    target) or an unconditional branch ends it."""
     bad = []
     for i, ins in enumerate(body):
         if ins != "s_barrier":
@@ -62,8 +67,8 @@ def barrier_violations(body: list[str], max_vmcnt: int = 0) -> list[int]:
         ok = False
         for j in range(i - 1, -1, -1):
             prev = body[j]
-            if prev.endswith(":") or prev.startswith("s_cbranch") or prev.startswith("s_branch"):
-                break  # start of the basic block
+            if prev.endswith(":") or prev.startswith("s_branch"):
+                break  # a block other code can jump into
             if "load_lds" in prev:
                 break
             m = re.search(r"\bvmcnt\((\d+)\)", prev) if prev.startswith("s_waitcnt") else None
@@ -87,6 +92,19 @@ def test_barrier_check_sees_a_missing_wait():
     body = ["s_waitcnt vmcnt(4)", "s_barrier"]
     assert barrier_violations(body) == [1] and barrier_violations(body, 4) == []
     assert barrier_violations(["s_waitcnt vmcnt(8)", "s_barrier"], 4) == [1]
+
+
+def test_barrier_check_follows_fall_through_only():
+    """A wait before a conditional branch covers the barrier of the block the
+    branch falls through to, not one behind a jump target."""
+    through = ["global_load_lds_dwordx4 v1, s[2:3]", "s_waitcnt vmcnt(0)", "s_cbranch_scc0 .LBB0_9", "",
+               "v_mov_b32_e32 v0, v1", "s_barrier"]
+    assert barrier_violations(through) == []
+    target = ["global_load_lds_dwordx4 v1, s[2:3]", "s_waitcnt vmcnt(0)", "s_cbranch_scc0 .LBB0_9",
+              ".LBB0_8:", "s_barrier"]
+    assert barrier_violations(target) == [4]
+    after_dma = ["s_waitcnt vmcnt(0)", "s_cbranch_scc0 .LBB0_9", "global_load_lds_dwordx4 v1, s[2:3]", "s_barrier"]
+    assert barrier_violations(after_dma) == [3]
 
 
 @pytest.mark.skipif(not os.path.exists("/opt/rocm/bin/hipcc") and not os.environ.get("HIPCC"),
